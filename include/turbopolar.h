@@ -1,0 +1,174 @@
+/*
+ * turbopolar.h -- C ABI of the MI355X (gfx950) TurboPolar compressed-KV
+ * decode-attention library (libturbopolar_hip.so).
+ *
+ * The library replaces the reference's kernel bridge
+ * (rfsn_v11/kernels/turbo_polar/metal.py, class MetalKernelBridge) and the
+ * MLX-op codecs it calls.  Every entry point takes plain device pointers and
+ * sizes, is stream-ordered and asynchronous (no host synchronisation), never
+ * allocates device memory, and returns a status code (TP_OK on success);
+ * tp_last_error() returns the message of the last failure on the calling
+ * thread.
+ *
+ * Page layout (one page = 64 tokens of one (batch, kv-head); "bh" below is
+ * batch * num_kv_heads + kv_head).  It is the structure-of-arrays layout of
+ * PolarKBlockStorage / QuantVBlockStorage (rfsn_v11/generation/storage.py:17-169),
+ * with `capacity` page slots per bh:
+ *   radii        [bh][capacity][64][64]  fp16, or int8 log-radius codes
+ *   radii_scales [bh][capacity]          fp16, int8 layout only (else NULL)
+ *   angle_l1     [bh][capacity][64][l1_row_bytes]    uint8, packed
+ *   angle_deep   [bh][capacity][64][deep_row_bytes]  uint8, packed
+ *   v_codes      [bh][capacity][64][128] int8
+ *   v_scales     [bh][capacity][64][4]   fp16 (one per group of 32 dims)
+ */
+#ifndef TURBOPOLAR_H_
+#define TURBOPOLAR_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TP_PAGE_TOKENS 64
+#define TP_HEAD_DIM 128
+
+/* Status codes.  The Python shim maps TP_ERR_INVALID to ValueError and the
+ * others to RuntimeError, mirroring the reference's exception contract. */
+enum {
+  TP_OK = 0,
+  TP_ERR_INVALID = 1,     /* bad argument (shape, pointer, size) */
+  TP_ERR_UNSUPPORTED = 2, /* layout the kernels do not implement */
+  TP_ERR_HIP = 3,         /* HIP launch/runtime error */
+  TP_ERR_WORKSPACE = 4    /* workspace missing or too small */
+};
+
+/* Compression layout of the key codes; the fields of TurboPolarConfig that
+ * fix the page format (rfsn_v11/candidates/turbo_polar_config.py:11-21) and the
+ * encoder's metadata (rfsn_v11/quant/polar/encoder.py:85-97). */
+typedef struct tp_page_layout {
+  int32_t int8_radii; /* 0: fp16 radii; 1: int8 log radii + fp16 page scale */
+  int32_t l1_bits;    /* 4 or 8: angle bits of pairs [0, split_dim/2) */
+  int32_t deep_bits;  /* 2, 4 or 8: angle bits of pairs [split_dim/2, 64) */
+  int32_t split_dim;  /* even, 0..128 */
+} tp_page_layout;
+
+/* Device pointers of one page store (see the layout above). */
+typedef struct tp_pages {
+  void* radii;
+  void* radii_scales;
+  uint8_t* angle_l1;
+  uint8_t* angle_deep;
+  int8_t* v_codes;
+  void* v_scales;
+  int64_t capacity; /* page slots per bh */
+} tp_pages;
+
+/* Last error message of the calling thread ("" if none). */
+const char* tp_last_error(void);
+
+/* Library ABI version (major * 100 + minor). */
+int32_t tp_version(void);
+
+/* Packed bytes per token of the l1 and deep angle-code rows.  Restates the
+ * packed shapes of PolarQuantEncoder._pack_4bit/_pack_2bit
+ * (rfsn_v11/quant/polar/encoder.py:56-83,101-130). */
+int32_t tp_layout_row_bytes(const tp_page_layout* layout, int32_t* l1_row_bytes,
+                            int32_t* deep_row_bytes);
+
+/*
+ * Encode pages: polar keys + grouped int8 values.
+ * Replaces PolarQuantEncoder.encode_block (rfsn_v11/quant/polar/encoder.py:24-98)
+ * and GroupedVQuantizer.quantize_block (rfsn_v11/quant/v_quant/encoder.py:16-30)
+ * as called by TurboPolarKVCacheRuntime._flush_block / _maybe_encode_partial
+ * (rfsn_v11/generation/turbo_polar_cache.py:128-161,276-319).
+ *
+ * k, v: [bh][in_tokens][128], fp16 (in_dtype 0) or fp32 (in_dtype 1); either may
+ * be NULL to encode only the other.  Tokens [token_begin, token_begin+n_tokens)
+ * are encoded into page slots [page_begin, page_begin + ceil(n_tokens/64)) of
+ * `pages`; a last partial page is zero-padded (as _maybe_encode_partial does).
+ * Codes and scales are bit-exact with the reference encoder's fp16 semantics.
+ */
+int32_t tp_encode_pages(const void* k, const void* v, int32_t in_dtype, int64_t bh,
+                        int64_t in_tokens, int64_t token_begin, int64_t n_tokens,
+                        const tp_page_layout* layout, const tp_pages* pages,
+                        int64_t page_begin, void* stream);
+
+/*
+ * Fused dequant . QK scores over all n_pages*64 page slots (no masking).
+ * Replaces MetalKernelBridge.execute_fused_qk (metal.py:494-530) and its kernel
+ * tqpolar_fused_dequant_qk (tqpolar_fused_qk.metal:4-100).
+ * q: fp16 [batch][hq][128]; scores: fp16 [batch][hq][n_pages*64].
+ * scale is applied in fp32 (the shim passes fp16(attention_scale), as
+ * metal.py:518 does).
+ */
+int32_t tp_fused_qk(const void* q, int64_t batch, int32_t hq, int32_t hkv,
+                    const tp_page_layout* layout, const tp_pages* pages, int32_t n_pages,
+                    float scale, void* scores, void* stream);
+
+/*
+ * Split-K decode attention over compressed pages plus an optional dense tail.
+ * Replaces MetalKernelBridge.execute_online_attention_quant_v (metal.py:651-715)
+ * and execute_online_attention_quant_v_dense_tail (metal.py:717-792), kernels
+ * tqpolar_online_attention_quant_v[_dense_tail]
+ * (tqpolar_online_attention.metal:197-390,393-629).
+ *
+ * q: fp16 [batch][hq][128]; out: fp16 [batch][hq][128].
+ * tail_k, tail_v: fp16 [batch][hkv][tail_stride][128] holding tail_len (0..63)
+ *   dense tokens that follow the pages (NULL when tail_len == 0).
+ * Tokens with global index >= actual_seq_len are masked.
+ * pages_per_split: pages per workgroup (0 = library default).
+ * workspace: device memory of at least tp_decode_workspace_bytes(...) bytes.
+ *   Its counter area (the first tp_decode_counter_bytes(batch, hq, hkv) bytes)
+ *   must be zero before the first call; every call leaves it zero again.  One
+ *   workspace must not be used by two calls that can run concurrently.
+ */
+int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hkv,
+                            const tp_page_layout* layout, const tp_pages* pages,
+                            int32_t n_pages, const void* tail_k, const void* tail_v,
+                            int32_t tail_len, int64_t tail_stride, int64_t actual_seq_len,
+                            float scale, int32_t pages_per_split, void* workspace,
+                            size_t workspace_bytes, void* out, void* stream);
+
+/* Workspace size for tp_decode_attention (same arguments). */
+size_t tp_decode_workspace_bytes(int64_t batch, int32_t hq, int32_t hkv, int32_t n_pages,
+                                 int32_t tail_len, int32_t pages_per_split);
+
+/* Size of the zero-initialised counter area at the start of the workspace. */
+size_t tp_decode_counter_bytes(int64_t batch, int32_t hq, int32_t hkv);
+
+/* Pages per workgroup that tp_decode_attention uses when given 0. */
+int32_t tp_default_pages_per_split(int64_t batch, int32_t hq, int32_t hkv, int32_t n_pages);
+
+/*
+ * Decode pages back to dense fp16 K and V (decompress-on-read).
+ * Replaces PolarQuantDecoder.decode_block (rfsn_v11/quant/polar/decoder.py:7-67)
+ * and GroupedVQuantizer.dequantize_block (rfsn_v11/quant/v_quant/encoder.py:32-38).
+ * k_out, v_out: fp16 [bh][n_pages*64][128] (either may be NULL).
+ */
+int32_t tp_decode_pages(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
+                        int64_t page_begin, int32_t n_pages, void* k_out, void* v_out,
+                        void* stream);
+
+/* ---- Self-test hooks: no counterpart in the reference.  They evaluate the
+ * encoder's scalar fp16 helpers so tests can check them exhaustively. ---- */
+
+/* For every 16-bit pattern b: sqrt_out[b] = fp16 sqrt of b, log_out[b] = fp16
+ * log(max(b, fp16(1e-6))), codes_out[3*b + {0,1,2}] = angle code of the fp16
+ * angle b for 2, 4 and 8 bits (fp16 input rules). */
+int32_t tp_selftest_f16_tables(uint16_t* sqrt_out, uint16_t* log_out, uint8_t* codes_out,
+                               void* stream);
+
+/* Counts, over x bit patterns [x_begin, x_begin+x_count) and all 65536 y
+ * patterns (finite values only), the pairs where the encoder's fast fp16
+ * atan2 differs from the float64 reference path.  *mismatches is accumulated
+ * (atomic add), so zero it first. */
+int32_t tp_selftest_atan2_exhaustive(unsigned long long* mismatches, int32_t x_begin,
+                                     int32_t x_count, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TURBOPOLAR_H_ */

@@ -1,0 +1,173 @@
+"""Fused QK and split-K decode attention parity against the oracle.
+
+The pages are encoded once on the GPU; the same pages (copied to the host)
+feed the oracle's restatement of _cpu_fused_qk / _cpu_online_attention /
+_cpu_online_attention_dense_tail (metal.py:254-332), evaluated in float64.
+Tolerances: attention outputs max-abs <= 2e-3 and
+relative L2 <= 1e-3; fused QK scores (fp16 out) max-abs <= 1e-2 and cosine
+>= 0.999 (tests/benchmarks/test_turbo_polar_kernel_qk.py:57-58 of the reference).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from common import ATOL, LAYOUTS, PAGE, RTOL_L2, cosine, gen_kv, gen_q, max_abs, rel_l2
+from turbopolar_amd import kernels
+from turbopolar_amd.kernels import PageSet, fp16_scale
+from turbopolar_amd.payload import PolarKeyBlock, QuantizedVBlock
+from test_gpu_encode import encode_gpu
+
+pytestmark = pytest.mark.gpu
+
+SCALE16 = fp16_scale(1.0 / np.sqrt(128.0))
+
+
+def build_case(device, layout, hq, hkv, S, tail, seed=0, kind="normal", qscale=1.0):
+    """Encode S pages on the GPU; returns GPU page views, host pages, tails, q."""
+    k, v = gen_kv(seed, 1, hkv, S * PAGE + tail, kind, np.float16)
+    q = gen_q(seed, 1, hq, qscale)
+    host = None
+    block = qv = None
+    if S:
+        host = encode_gpu(k[:, :, : S * PAGE], v[:, :, : S * PAGE], layout, device)
+        meta = oracle.encode_block(k[:, :, :PAGE], l1_bits=layout[1], deep_bits=layout[2],
+                                   split_dim=layout[3], use_int8_radii=layout[0])["metadata"]
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+        block = PolarKeyBlock(
+            radii=t(host["radii"]), angle_codes_l1=t(host["angle_codes_l1"]),
+            angle_codes_deep=t(host["angle_codes_deep"]), shape=(1, hkv, S * PAGE, 128),
+            block_size=PAGE, head_dim=128, metadata=meta,
+            radii_scales=t(host["radii_scales"]) if layout[0] else None,
+        )
+        qv = QuantizedVBlock(codes=t(host["v_codes"]), scales=t(host["v_scales"]), group_size=32)
+        host["metadata"] = meta
+    tk = k[:, :, S * PAGE:]
+    tv = v[:, :, S * PAGE:]
+    return block, qv, host, tk, tv, q
+
+
+def oracle_out(host, tk, tv, q, seq_len):
+    if host is None:
+        return oracle.softmax_attention(q, tk, tv, SCALE16, seq_len)
+    blk = {k: host[k] for k in ("radii", "radii_scales", "angle_codes_l1", "angle_codes_deep", "metadata")}
+    if blk["radii_scales"] is not None:
+        blk["radii_scales"] = blk["radii_scales"].reshape(blk["radii"].shape[:3] + (1, 1))
+    return oracle.cpu_online_attention_dense_tail(
+        q, blk, (host["v_codes"], host["v_scales"]), tk, tv, SCALE16, seq_len
+    )
+
+
+def run_gpu(device, block, qv, tk, tv, q, seq_len, pps=0):
+    pages = PageSet(block, qv) if block is not None else None
+    tkt = torch.from_numpy(tk).to(device) if tk.shape[2] else None
+    tvt = torch.from_numpy(tv).to(device) if tv.shape[2] else None
+    out = kernels.decode_attention(torch.from_numpy(q).to(device), pages, tkt, tvt, seq_len, SCALE16,
+                                   pages_per_split=pps)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def check(out, ref, what):
+    assert np.all(np.isfinite(out)), f"{what}: non-finite output"
+    ma, rl = max_abs(out, ref), rel_l2(out, ref)
+    assert ma <= ATOL and rl <= RTOL_L2, f"{what}: max_abs={ma:.3g} rel_l2={rl:.3g}"
+
+
+CASES = [
+    # layout, hq, hkv, S pages, tail tokens, pages_per_split
+    ("default", 2, 2, 2, 0, 0),
+    ("default", 2, 2, 2, 37, 0),
+    ("default", 4, 2, 2, 0, 1),
+    ("default", 4, 2, 3, 63, 1),
+    ("default", 32, 8, 5, 1, 2),
+    ("default", 64, 8, 4, 36, 3),
+    ("default", 8, 1, 9, 0, 4),
+    ("default", 4, 4, 0, 37, 0),
+    ("fast", 4, 4, 2, 0, 0),
+    ("fast", 4, 2, 2, 37, 1),
+    ("fast", 32, 8, 6, 63, 2),
+    ("fast", 64, 8, 3, 0, 1),
+    ("deep2", 4, 2, 3, 5, 1),
+    ("l1_8bit", 4, 2, 2, 17, 0),
+    ("odd_split", 8, 4, 3, 9, 2),
+    ("int8_default_angles", 4, 2, 2, 0, 1),
+    ("default", 40, 2, 2, 11, 1),  # GQA 20 > 16: two head blocks
+]
+
+
+@pytest.mark.parametrize("layout_name,hq,hkv,S,tail,pps", CASES)
+def test_decode_attention_parity(device, layout_name, hq, hkv, S, tail, pps):
+    print(f"[attn] layout={layout_name} hq={hq} hkv={hkv} S={S} tail={tail} pps={pps}", flush=True)
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS[layout_name], hq, hkv, S, tail, seed=S * 7 + tail)
+    seq = S * PAGE + tail
+    out = run_gpu(device, block, qv, tk, tv, q, seq, pps)
+    check(out, oracle_out(host, tk, tv, q, seq), layout_name)
+
+
+@pytest.mark.parametrize("drop", [1, 5, 64, 100])
+def test_decode_attention_masked_suffix(device, drop):
+    """actual_seq_len below the stored tokens masks the suffix (metal.py:318-319)."""
+    print(f"[attn-mask] drop={drop}", flush=True)
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], 8, 2, 4, 20, seed=4)
+    seq = 4 * PAGE + 20 - drop
+    for pps in (0, 1):
+        out = run_gpu(device, block, qv, tk, tv, q, seq, pps)
+        check(out, oracle_out(host, tk, tv, q, seq), f"drop={drop} pps={pps}")
+
+
+@pytest.mark.parametrize("layout_name", ["default", "fast", "deep2", "odd_split"])
+def test_fused_qk_parity(device, layout_name):
+    print(f"[qk] layout={layout_name}", flush=True)
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS[layout_name], 8, 2, 3, 0, seed=9)
+    scores = kernels.fused_qk(torch.from_numpy(q).to(device), PageSet(block, None), SCALE16)
+    torch.cuda.synchronize()
+    got = scores.float().cpu().numpy()
+    blk = {k: host[k] for k in ("radii", "radii_scales", "angle_codes_l1", "angle_codes_deep", "metadata")}
+    if blk["radii_scales"] is not None:
+        blk["radii_scales"] = blk["radii_scales"].reshape(blk["radii"].shape[:3] + (1, 1))
+    ref = oracle.cpu_fused_qk(q, blk, SCALE16)
+    assert got.shape == ref.shape
+    assert max_abs(got, ref) <= 1e-2, max_abs(got, ref)
+    assert cosine(got, ref) >= 0.999
+
+
+@pytest.mark.parametrize("layout_name,kind,qscale", [
+    ("default", "outlier", 1.0 / np.sqrt(128.0)),
+    ("fast", "outlier", 1.0 / np.sqrt(128.0)),
+    ("default", "normal", 1.0),
+])
+def test_north_star_shape_32k(device, layout_name, kind, qscale):
+    """Llama-3-8B shape (32 q / 8 kv heads) at 32768 tokens, default split."""
+    print(f"[attn-32k] layout={layout_name} kind={kind}", flush=True)
+    S = 512
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS[layout_name], 32, 8, S, 0, seed=3, kind=kind, qscale=qscale)
+    out = run_gpu(device, block, qv, tk, tv, q, S * PAGE)
+    check(out, oracle_out(host, tk, tv, q, S * PAGE), "32k")
+
+
+def test_split_invariance(device):
+    """Split-K online softmax equals the one-pass result for every split size."""
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], 32, 8, 40, 13, seed=12)
+    seq = 40 * PAGE + 13
+    outs = [run_gpu(device, block, qv, tk, tv, q, seq, pps) for pps in (1, 2, 3, 8, 40)]
+    for o in outs[1:]:
+        assert max_abs(o, outs[0]) <= 1e-3
+    check(outs[0], oracle_out(host, tk, tv, q, seq), "split")
+
+
+def test_page_decode_parity(device):
+    """tp_decode_pages: V exactly the dequantised codes; K within one fp16 ulp."""
+    for name in ("default", "fast", "deep2", "odd_split"):
+        block, qv, host, tk, tv, q = build_case(device, LAYOUTS[name], 4, 2, 3, 0, seed=2)
+        kg, vg = kernels.decode_pages(PageSet(block, qv))
+        torch.cuda.synchronize()
+        blk = {k: host[k] for k in ("radii", "radii_scales", "angle_codes_l1", "angle_codes_deep", "metadata")}
+        rs = None if blk["radii_scales"] is None else blk["radii_scales"].reshape(blk["radii"].shape[:3] + (1, 1))
+        kref = oracle.decode_block(blk["radii"], rs, blk["angle_codes_l1"], blk["angle_codes_deep"], blk["metadata"])
+        vref = oracle.dequantize_block(host["v_codes"], host["v_scales"]).reshape(kref.shape)
+        assert np.array_equal(vg.cpu().numpy().view(np.uint16), vref.view(np.uint16)), name
+        kd = kg.cpu().numpy().astype(np.float64)
+        ulp = np.spacing(np.abs(kref).astype(np.float16)).astype(np.float64)
+        assert np.all(np.abs(kd - kref) <= ulp + 1e-12), name

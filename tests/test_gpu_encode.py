@@ -1,0 +1,182 @@
+"""Encode kernel parity: codes and scales bit-exact against the oracle.
+
+Runs tp_encode_pages through the C ABI on the GPU and compares every output
+buffer byte for byte with the NumPy restatement of
+PolarQuantEncoder.encode_block / GroupedVQuantizer.quantize_block.  The scalar
+fp16 helpers the kernel is built on are checked exhaustively.
+"""
+
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from common import LAYOUTS, PAGE, gen_kv, oracle_pages
+from turbopolar_amd import _lib, kernels
+from turbopolar_amd.codecs import PolarQuantEncoder
+from turbopolar_amd.config import TurboPolarConfig
+
+pytestmark = pytest.mark.gpu
+
+
+def _encoder(layout):
+    int8, l1b, deepb, split = layout
+    cfg = TurboPolarConfig(
+        k_angle_bits_level1=l1b, k_angle_bits_deep=deepb, split_dim=split, use_int8_radii=int8,
+        num_q_heads=8, num_kv_heads=8,
+    )
+    return PolarQuantEncoder(cfg)
+
+
+def encode_gpu(k, v, layout, device, capacity=None, page_begin=0, n_tokens=None):
+    """Encode [B,H,T,128] numpy inputs on the GPU; returns numpy page buffers."""
+    enc = _encoder(layout)
+    B, H, T, _ = k.shape
+    n_tokens = T if n_tokens is None else n_tokens
+    S = (n_tokens + PAGE - 1) // PAGE
+    cap = capacity or (page_begin + S)
+    bufs = enc.alloc_pages(B, H, cap, device)
+    codes = torch.zeros((B, H, cap, PAGE, 128), dtype=torch.int8, device=device)
+    scales = torch.zeros((B, H, cap, PAGE, 4), dtype=torch.float16, device=device)
+    pages = _lib.TPPages(
+        _lib.ptr(bufs["radii"]), _lib.ptr(bufs["radii_scales"]), _lib.ptr(bufs["angle_codes_l1"]),
+        _lib.ptr(bufs["angle_codes_deep"]), _lib.ptr(codes), _lib.ptr(scales), cap,
+    )
+    kernels.encode_pages(
+        torch.from_numpy(k).to(device), torch.from_numpy(v).to(device), 0, n_tokens, enc.layout, pages, page_begin
+    )
+    torch.cuda.synchronize()
+    sl = slice(page_begin, page_begin + S)
+    out = {name: (t[:, :, sl].cpu().numpy() if t is not None else None) for name, t in bufs.items()}
+    out["v_codes"] = codes[:, :, sl].cpu().numpy()
+    out["v_scales"] = scales[:, :, sl].cpu().numpy()
+    return out
+
+
+def assert_bits_equal(gpu, ref, what):
+    gpu = np.ascontiguousarray(gpu)
+    ref = np.ascontiguousarray(ref)
+    assert gpu.shape == ref.shape, (what, gpu.shape, ref.shape)
+    g = gpu.view(np.uint8)
+    r = ref.view(np.uint8)
+    bad = np.count_nonzero(g != r)
+    assert bad == 0, f"{what}: {bad} of {g.size} bytes differ"
+
+
+def check_against_oracle(k, v, layout, device, **kw):
+    gpu = encode_gpu(k, v, layout, device, **kw)
+    blk, (vc, vs) = oracle_pages(k, v, layout)
+    assert_bits_equal(gpu["radii"], blk["radii"], "radii")
+    if layout[0]:
+        assert_bits_equal(gpu["radii_scales"], blk["radii_scales"].reshape(gpu["radii_scales"].shape), "radii_scales")
+    assert_bits_equal(gpu["angle_codes_l1"], blk["angle_codes_l1"], "angle_codes_l1")
+    assert_bits_equal(gpu["angle_codes_deep"], blk["angle_codes_deep"], "angle_codes_deep")
+    assert_bits_equal(gpu["v_codes"], vc, "v_codes")
+    assert_bits_equal(gpu["v_scales"], vs, "v_scales")
+
+
+@pytest.mark.parametrize("layout_name", sorted(LAYOUTS))
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_encode_random_bit_exact(device, layout_name, dtype):
+    print(f"[encode] layout={layout_name} dtype={np.dtype(dtype).name}", flush=True)
+    k, v = gen_kv(3, 1, 2, 4 * PAGE, "normal", dtype)
+    check_against_oracle(k, v, LAYOUTS[layout_name], device)
+
+
+@pytest.mark.parametrize("kind", ["loguniform", "outlier", "studentt"])
+@pytest.mark.parametrize("layout_name", ["default", "fast"])
+def test_encode_baseline_distributions(device, kind, layout_name):
+    print(f"[encode] kind={kind} layout={layout_name}", flush=True)
+    k, v = gen_kv(11, 2, 3, 3 * PAGE, kind, np.float16)
+    check_against_oracle(k, v, LAYOUTS[layout_name], device)
+
+
+def _edge_page(dtype):
+    """Axis-aligned pairs, signed zeros, radii at the fp16 x*x overflow edge,
+    exact V quotient ties and an all-zero V group."""
+    k = np.zeros((1, 1, PAGE, 128), dtype=np.float32)
+    v = np.zeros((1, 1, PAGE, 128), dtype=np.float32)
+    specials = [(0, 0), (1, 0), (-1, 0.0), (-1, -0.0), (0, 1), (0, -1), (1, 1), (-1, 1), (3, 4),
+                (255.9, 0), (256, 0), (255, 10), (-300, 2), (1e-7, 1e-7), (65504, 65504), (-0.0, -0.0)]
+    rng = np.random.default_rng(5)
+    for t in range(PAGE):
+        for j in range(64):
+            x, y = specials[(t * 64 + j) % len(specials)] if t < 8 else rng.standard_normal(2) * 4
+            k[0, 0, t, 2 * j], k[0, 0, t, 2 * j + 1] = x, y
+    # V: group 0 all zero; group 1 with many exact half-ties of v / s; group 2 huge range
+    v[0, 0, :, 32:64] = np.arange(32, dtype=np.float32)[None, :] * 0.5 - 8
+    v[0, 0, :, 32] = 127.0
+    v[0, 0, :, 64:96] = rng.standard_normal((PAGE, 32)) * 1000
+    v[0, 0, :, 96:] = rng.standard_normal((PAGE, 32)) * 1e-6
+    return k.astype(dtype), v.astype(dtype)
+
+
+@pytest.mark.parametrize("layout_name", ["default", "fast", "deep2", "l1_8bit"])
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_encode_edge_page(device, layout_name, dtype):
+    print(f"[encode-edge] layout={layout_name} dtype={np.dtype(dtype).name}", flush=True)
+    k, v = _edge_page(dtype)
+    check_against_oracle(k, v, LAYOUTS[layout_name], device)
+
+
+@pytest.mark.parametrize("layout_name", ["default", "fast"])
+def test_encode_partial_page_zero_padded(device, layout_name):
+    """n_tokens < 64: the missing tokens encode as zeros (_maybe_encode_partial)."""
+    print(f"[encode-partial] layout={layout_name}", flush=True)
+    k, v = gen_kv(21, 1, 2, 37, "normal", np.float16)
+    gpu = encode_gpu(k, v, LAYOUTS[layout_name], device)
+    kp = np.zeros((1, 2, PAGE, 128), np.float16)
+    vp = np.zeros((1, 2, PAGE, 128), np.float16)
+    kp[:, :, :37], vp[:, :, :37] = k, v
+    blk, (vc, vs) = oracle_pages(kp, vp, LAYOUTS[layout_name])
+    assert_bits_equal(gpu["radii"], blk["radii"], "radii")
+    assert_bits_equal(gpu["angle_codes_deep"], blk["angle_codes_deep"], "deep")
+    assert_bits_equal(gpu["v_codes"], vc, "v_codes")
+    assert_bits_equal(gpu["v_scales"], vs, "v_scales")
+
+
+def test_encode_into_capacity_slot(device):
+    """Pages land in slots [page_begin, page_begin + S) of a larger store."""
+    k, v = gen_kv(8, 2, 2, 2 * PAGE, "normal", np.float16)
+    check_against_oracle(k, v, LAYOUTS["default"], device, capacity=8, page_begin=3)
+
+
+def test_f16_tables_exhaustive(device):
+    """sqrt, log and the angle->code rule over all 65536 fp16 bit patterns."""
+    sq = torch.empty(65536, dtype=torch.int16, device=device)
+    lg = torch.empty(65536, dtype=torch.int16, device=device)
+    cd = torch.empty(65536 * 3, dtype=torch.uint8, device=device)
+    st = _lib.lib().tp_selftest_f16_tables(sq.data_ptr(), lg.data_ptr(), cd.data_ptr(),
+                                           torch.cuda.current_stream().cuda_stream)
+    _lib.check(st, "selftest tables")
+    torch.cuda.synchronize()
+    sq = sq.cpu().numpy().view(np.uint16)
+    lg = lg.cpu().numpy().view(np.uint16)
+    cd = cd.cpu().numpy().reshape(65536, 3)
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = bits.view(np.float16)
+    nonneg = np.arange(0, 0x7C01)  # +0 .. +inf
+    ref_sq = np.sqrt(f[nonneg]).view(np.uint16)
+    assert np.array_equal(sq[nonneg], ref_sq), "sqrt table differs"
+    pos = np.arange(1, 0x7C01)
+    ref_lg = oracle.log_cr(np.maximum(f[pos], oracle.turbopolar.F16_RADIUS_FLOOR)).view(np.uint16)
+    assert np.array_equal(lg[pos], ref_lg), f"log differs at {np.count_nonzero(lg[pos] != ref_lg)} inputs"
+    angles = np.concatenate([np.arange(0, 0x4249), np.arange(0x8000, 0xC249)])  # |a| <= fp16(pi)
+    for col, nb in enumerate((2, 4, 8)):
+        ref = oracle.angle_codes_f16(f[angles], nb)
+        bad = np.count_nonzero(cd[angles, col] != ref)
+        assert bad == 0, f"{nb}-bit angle codes differ for {bad} angles"
+
+
+def test_atan2_fast_path_exhaustive(device):
+    """Fast fp32 atan2 + midpoint guard == float64 path for every finite fp16 pair."""
+    cnt = torch.zeros(1, dtype=torch.int64, device=device)
+    step = 4096
+    for x0 in range(0, 65536, step):
+        st = _lib.lib().tp_selftest_atan2_exhaustive(cnt.data_ptr(), x0, step, torch.cuda.current_stream().cuda_stream)
+        _lib.check(st, "selftest atan2")
+    torch.cuda.synchronize()
+    assert int(cnt.item()) == 0, f"{int(cnt.item())} fp16 pairs where the fast atan2 differs"

@@ -1,0 +1,190 @@
+"""Runtime API on the GPU: appends, flushes, telemetry and the decode step.
+
+Mirrors the reference's runtime and integration suites
+(tests/test_turbo_polar_cache_runtime.py, tests/benchmarks/test_turbopolar_fast_attention.py)
+with the oracle standing in for MLX.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from common import ATOL, LAYOUTS, PAGE, RTOL_L2, cosine, max_abs, oracle_pages, rel_l2
+from turbopolar_amd import TurboPolarConfig, TurboPolarFastCache, TurboPolarKVCacheRuntime, make_turbo_caches
+from turbopolar_amd.kernels import fp16_scale
+
+pytestmark = pytest.mark.gpu
+
+
+def _cfg(layout_name, hq=4, hkv=2):
+    int8, l1b, deepb, split = LAYOUTS[layout_name]
+    return TurboPolarConfig(num_q_heads=hq, num_kv_heads=hkv, use_int8_radii=int8, k_angle_bits_level1=l1b,
+                            k_angle_bits_deep=deepb, split_dim=split)
+
+
+def _host_state(runtime):
+    block, qv, tk, tv, _, seq = runtime.get_fused_attention_inputs()
+    blk = None
+    if block is not None:
+        blk = {
+            "radii": block.radii.cpu().numpy(),
+            "radii_scales": block.radii_scales.cpu().numpy() if block.radii_scales is not None else None,
+            "angle_codes_l1": block.angle_codes_l1.cpu().numpy(),
+            "angle_codes_deep": block.angle_codes_deep.cpu().numpy(),
+            "metadata": block.metadata,
+        }
+        qv = (qv.codes.cpu().numpy(), qv.scales.cpu().numpy())
+    tk = tk.cpu().numpy() if tk is not None else np.zeros((1, runtime._num_kv_heads, 0, 128), np.float16)
+    tv = tv.cpu().numpy() if tv is not None else np.zeros_like(tk)
+    return blk, qv, tk, tv, seq
+
+
+@pytest.mark.parametrize("layout_name", ["default", "fast"])
+@pytest.mark.parametrize("total", [37, 64, 100, 130])
+def test_decode_steps_match_oracle(device, layout_name, total):
+    """Token-by-token decode (the reference's 37 / 100 / 64-token integration
+    cases) against the oracle on the identical cache state, and the stored
+    pages against the oracle encoding of the raw tokens."""
+    print(f"[runtime] layout={layout_name} total={total}", flush=True)
+    cfg = _cfg(layout_name)
+    cache = TurboPolarFastCache(cfg)
+    rng = np.random.default_rng(2026 + total)
+    ks, vs = [], []
+    for _ in range(total):
+        q = rng.standard_normal((1, 4, 1, 128)).astype(np.float16)
+        kn = rng.standard_normal((1, 2, 1, 128)).astype(np.float16)
+        vn = rng.standard_normal((1, 2, 1, 128)).astype(np.float16)
+        ks.append(kn)
+        vs.append(vn)
+        out = cache.decode_attention(torch.from_numpy(q).to(device), torch.from_numpy(kn).to(device),
+                                     torch.from_numpy(vn).to(device), cfg.attention_scale)
+        assert out.shape == (1, 4, 128)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    blk, qv, tk, tv, seq = _host_state(cache.runtime)
+    assert seq == total
+    qq = q[:, :, 0]
+    scale = fp16_scale(cfg.attention_scale)
+    if blk is None:
+        ref = oracle.softmax_attention(qq, tk, tv, scale, seq)
+    else:
+        if blk["radii_scales"] is not None:
+            blk["radii_scales"] = blk["radii_scales"].reshape(blk["radii"].shape[:3] + (1, 1))
+        ref = oracle.cpu_online_attention_dense_tail(qq, blk, qv, tk, tv, scale, seq)
+    assert max_abs(got, ref) <= ATOL and rel_l2(got, ref) <= RTOL_L2
+    # Stored pages equal the oracle encoding of the raw tokens.
+    S = total // PAGE
+    if S:
+        kk = np.concatenate(ks, axis=2)[:, :, : S * PAGE]
+        vv = np.concatenate(vs, axis=2)[:, :, : S * PAGE]
+        oblk, (vc, vsc) = oracle_pages(kk, vv, LAYOUTS[layout_name])
+        assert np.array_equal(blk["radii"].view(np.uint8), oblk["radii"].view(np.uint8))
+        assert np.array_equal(blk["angle_codes_deep"], oblk["angle_codes_deep"])
+        assert np.array_equal(qv[0], vc) and np.array_equal(qv[1].view(np.uint16), vsc.view(np.uint16))
+    # Against dense attention on the raw tokens (reference integration bound).
+    dense = oracle.softmax_attention(qq, np.concatenate(ks, 2), np.concatenate(vs, 2), scale)
+    assert cosine(got, dense) >= 0.95
+
+
+def test_bulk_equals_incremental(device):
+    """One 200-token append == 200 single-token appends (pages, tail, telemetry)."""
+    cfg = _cfg("fast", hq=8, hkv=4)
+    rng = np.random.default_rng(7)
+    k = torch.from_numpy(rng.standard_normal((1, 4, 200, 128)).astype(np.float16)).to(device)
+    v = torch.from_numpy(rng.standard_normal((1, 4, 200, 128)).astype(np.float16)).to(device)
+    a = TurboPolarKVCacheRuntime(cfg)
+    a.append(k, v)
+    b = TurboPolarKVCacheRuntime(cfg)
+    for t in range(200):
+        b.append(k[:, :, t : t + 1], v[:, :, t : t + 1])
+    for ra, rb in ((a.k_storage.radii, b.k_storage.radii), (a.v_storage.codes, b.v_storage.codes),
+                   (a.k_storage.radii_scales, b.k_storage.radii_scales),
+                   (a.k_storage.angle_codes_deep, b.k_storage.angle_codes_deep)):
+        assert torch.equal(ra, rb)
+    assert torch.equal(a.partial_k, b.partial_k)
+    ta, tb = a.get_io_telemetry(), b.get_io_telemetry()
+    assert ta == tb
+    assert ta["total_blocks"] == 3 and ta["partial_tokens"] == 8
+    assert ta["k_storage_capacity"] == 4 and ta["k_storage_reallocs"] == 0
+
+
+@pytest.mark.parametrize("T", [1, 32, 63, 64, 65, 127, 128, 129])
+@pytest.mark.parametrize("gqa", [1, 4])
+def test_milestone_shapes(device, T, gqa):
+    """turbo_polar_cache_runtime.py:42-56 shape matrix of the reference."""
+    cfg = TurboPolarConfig(head_dim=128, qjl_proj_dim=64, block_size=64, split_dim=0, num_q_heads=4,
+                           num_kv_heads=4 // gqa, use_qjl=False, seed=7)
+    cache = TurboPolarKVCacheRuntime(cfg)
+    hkv = cfg.num_kv_heads
+    g = torch.Generator(device="cpu").manual_seed(T)
+    k = torch.randn((1, hkv, T, 128), generator=g).to(device)
+    v = torch.randn((1, hkv, T, 128), generator=g).to(device)
+    cache.append(k, v)
+    block, quant_v, dense_v, qjl, actual = cache.get_blocks_for_attention()
+    assert actual == T and block is not None and quant_v is not None and dense_v is None and qjl is None
+    S = block.radii.shape[2]
+    assert S * 64 >= T > (S - 1) * 64
+    tel = cache.get_io_telemetry()
+    assert tel["partial_tokens"] == T % 64 and tel["total_blocks"] == T // 64
+
+
+def test_telemetry_closed_forms(device):
+    """Compression ratios 512/296 (default) and 512/264.03 (fast) at page multiples;
+    capacity doubling 4 -> 8 -> 16 with the reference's copy accounting."""
+    for name, ratio in (("default", 512 / 296), ("fast", 512 / (128 + 136 + 2 / 64))):
+        cfg = _cfg(name, hq=8, hkv=8)
+        rt = TurboPolarKVCacheRuntime(cfg)
+        x = torch.randn((1, 8, 256, 128), device=device, dtype=torch.float16)
+        rt.append(x, x)
+        tel = rt.get_io_telemetry()
+        assert abs(tel["compression_ratio"] - ratio) < 1e-9, (name, tel)
+    rt = TurboPolarKVCacheRuntime(_cfg("default", hq=8, hkv=8))
+    for _ in range(9):
+        x = torch.randn((1, 8, 64, 128), device=device, dtype=torch.float16)
+        rt.append(x, x)
+    tel = rt.get_io_telemetry()
+    assert tel["k_storage_capacity"] == 16 and tel["k_storage_reallocs"] == 2
+    per_slot_k = 8 * 64 * (64 * 2 + 16 + 16)
+    assert rt.k_storage.bytes_copied_during_growth == per_slot_k * (4 + 8)
+    per_slot_v = 8 * 64 * (128 + 8)
+    assert rt.v_storage.bytes_copied_during_growth == per_slot_v * (4 + 8)
+
+
+def test_update_and_fetch_prefill(device):
+    """Prefill returns decompressed K/V of every token, incl. the padded tail page."""
+    cfg = _cfg("fast", hq=4, hkv=2)
+    cache = make_turbo_caches(1, 4, 2, 128)[0]
+    rng = np.random.default_rng(1)
+    k = rng.standard_normal((1, 2, 100, 128)).astype(np.float16)
+    v = rng.standard_normal((1, 2, 100, 128)).astype(np.float16)
+    kd, vd = cache.update_and_fetch(torch.from_numpy(k).to(device), torch.from_numpy(v).to(device))
+    assert kd.shape == (1, 2, 100, 128) and vd.shape == (1, 2, 100, 128)
+    kp = np.zeros((1, 2, 128, 128), np.float16)
+    vp = np.zeros((1, 2, 128, 128), np.float16)
+    kp[:, :, :100], vp[:, :, :100] = k, v
+    blk, (vc, vsc) = oracle_pages(kp, vp, LAYOUTS["fast"])
+    kref = oracle.decode_block(blk["radii"], blk["radii_scales"].reshape(1, 2, 2, 1, 1), blk["angle_codes_l1"],
+                               blk["angle_codes_deep"], blk["metadata"])[:, :, :100]
+    vref = oracle.dequantize_block(vc, vsc).reshape(1, 2, 128, 128)[:, :, :100]
+    assert np.array_equal(vd.cpu().numpy().view(np.uint16), vref.view(np.uint16))
+    ulp = np.spacing(np.abs(kref).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(kd.cpu().numpy().astype(np.float64) - kref) <= ulp)
+    assert cosine(kd.cpu().numpy(), k) >= 0.99
+
+
+def test_append_rejects_nonfinite_and_changes(device):
+    rt = TurboPolarKVCacheRuntime(_cfg("default", hq=4, hkv=4))
+    good = torch.randn((1, 4, 64, 128), device=device, dtype=torch.float16)
+    rt.append(good, good)
+    assert rt.partial_k is None
+    with pytest.raises(ValueError, match="batch size changed"):
+        x = torch.randn((2, 4, 1, 128), device=device, dtype=torch.float16)
+        rt.append(x, x)
+    with pytest.raises(ValueError, match="dtype changed"):
+        x = torch.randn((1, 4, 1, 128), device=device, dtype=torch.float32)
+        rt.append(x, x)
+    bad = good[:, :, :2].clone()
+    bad[0, 0, 0, 0] = float("inf")
+    with pytest.raises(ValueError, match="finite"):
+        rt.append(bad, good[:, :, :2])

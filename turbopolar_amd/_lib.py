@@ -1,0 +1,149 @@
+"""ctypes binding of the C ABI declared in ``include/turbopolar.h``.
+
+The library is loaded from the package directory (built in-tree by
+``python -m turbopolar_amd.build``).  There is no CPU fallback: if the library
+is missing or the tensors are not on a HIP device, calls raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import torch  # noqa: F401  (loads torch's HIP runtime before the library)
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libturbopolar_hip.so"
+HEADER_PATH = PKG_DIR.parent / "include" / "turbopolar.h"
+
+TP_OK = 0
+TP_ERR_INVALID = 1
+TP_ERR_UNSUPPORTED = 2
+TP_ERR_HIP = 3
+TP_ERR_WORKSPACE = 4
+
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_vp = ctypes.c_void_p
+c_size = ctypes.c_size_t
+c_float = ctypes.c_float
+
+
+class TPPageLayout(ctypes.Structure):
+    _fields_ = [
+        ("int8_radii", c_i32),
+        ("l1_bits", c_i32),
+        ("deep_bits", c_i32),
+        ("split_dim", c_i32),
+    ]
+
+
+class TPPages(ctypes.Structure):
+    _fields_ = [
+        ("radii", c_vp),
+        ("radii_scales", c_vp),
+        ("angle_l1", c_vp),
+        ("angle_deep", c_vp),
+        ("v_codes", c_vp),
+        ("v_scales", c_vp),
+        ("capacity", c_i64),
+    ]
+
+
+class TurboPolarHipError(RuntimeError):
+    """A HIP runtime or launch failure inside the TurboPolar library."""
+
+
+_P_LAYOUT = ctypes.POINTER(TPPageLayout)
+_P_PAGES = ctypes.POINTER(TPPages)
+
+_SIGNATURES = {
+    "tp_last_error": (ctypes.c_char_p, []),
+    "tp_version": (c_i32, []),
+    "tp_layout_row_bytes": (c_i32, [_P_LAYOUT, ctypes.POINTER(c_i32), ctypes.POINTER(c_i32)]),
+    "tp_encode_pages": (
+        c_i32,
+        [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, _P_LAYOUT, _P_PAGES, c_i64, c_vp],
+    ),
+    "tp_fused_qk": (c_i32, [c_vp, c_i64, c_i32, c_i32, _P_LAYOUT, _P_PAGES, c_i32, c_float, c_vp, c_vp]),
+    "tp_decode_attention": (
+        c_i32,
+        [
+            c_vp, c_i64, c_i32, c_i32, _P_LAYOUT, _P_PAGES, c_i32,
+            c_vp, c_vp, c_i32, c_i64, c_i64, c_float, c_i32, c_vp, c_size, c_vp, c_vp,
+        ],
+    ),
+    "tp_decode_workspace_bytes": (c_size, [c_i64, c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "tp_decode_counter_bytes": (c_size, [c_i64, c_i32, c_i32]),
+    "tp_default_pages_per_split": (c_i32, [c_i64, c_i32, c_i32, c_i32]),
+    "tp_decode_pages": (c_i32, [_P_LAYOUT, _P_PAGES, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp]),
+    "tp_selftest_f16_tables": (c_i32, [c_vp, c_vp, c_vp, c_vp]),
+    "tp_selftest_atan2_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
+}
+
+_lib = None
+
+
+def header_symbols() -> list[str]:
+    """Function names declared in include/turbopolar.h."""
+    text = HEADER_PATH.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(tp_\w+)\s*\(", text, re.M)))
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libturbopolar_hip.so (once) and declares the C signatures."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH.name} is not built; run `python -m turbopolar_amd.build` "
+                "(the TurboPolar path has no CPU fallback)"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    """Maps a C status code to the reference's exception types."""
+    if status == TP_OK:
+        return
+    msg = lib().tp_last_error().decode(errors="replace")
+    if status in (TP_ERR_INVALID, TP_ERR_UNSUPPORTED):
+        raise ValueError(f"{what}: {msg}")
+    raise TurboPolarHipError(f"{what}: {msg}")
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None for None or an empty tensor)."""
+    if t is None or t.numel() == 0:
+        return None
+    return t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_hip(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"{name} must be on a HIP device; the TurboPolar path has no CPU fallback "
+            f"(got device {t.device})"
+        )
+
+
+def make_layout(int8_radii: bool, l1_bits: int, deep_bits: int, split_dim: int) -> TPPageLayout:
+    return TPPageLayout(int(bool(int8_radii)), int(l1_bits), int(deep_bits), int(split_dim))
+
+
+def row_bytes(layout: TPPageLayout) -> tuple[int, int]:
+    l1 = c_i32(0)
+    deep = c_i32(0)
+    check(lib().tp_layout_row_bytes(ctypes.byref(layout), ctypes.byref(l1), ctypes.byref(deep)), "layout")
+    return l1.value, deep.value

@@ -1,0 +1,121 @@
+"""HIP kernel bridge: the drop-in for ``MetalKernelBridge``.
+
+Same method names, arguments and return values as
+rfsn_v11/kernels/turbo_polar/metal.py:57-792 for the supported path:
+
+* ``execute_fused_qk(q, block, config) -> scores``            (metal.py:494-530)
+* ``execute_online_attention_quant_v(...) -> (out, trace)``    (metal.py:651-715)
+* ``execute_online_attention_quant_v_dense_tail(...)``         (metal.py:717-792)
+
+Differences: there is no silent CPU fallback (unsupported inputs raise), the
+trace reports ``hip_used`` where the reference reports ``metal_used``, and
+QJL (``use_qjl=True``) raises NotImplementedError -- the config rejects it
+(turbo_polar_config.py:46-47).  ``attention_scale`` reaches the kernels as
+fp16, as the reference passes it (metal.py:518,692,774).
+"""
+
+from __future__ import annotations
+
+from typing import Any, Dict, Optional, Tuple
+
+import torch
+
+from . import _lib
+from .kernels import PageSet, decode_attention, fp16_scale, fused_qk
+from .payload import PolarKeyBlock, QuantizedVBlock
+
+
+class HipKernelBridge:
+    """Process-wide singleton, like the reference bridge (metal.py:72-86)."""
+
+    _instance: "HipKernelBridge | None" = None
+
+    def __new__(cls, *args, **kwargs):
+        if cls._instance is None:
+            inst = super().__new__(cls)
+            _lib.lib()  # fail loudly if the HIP library is missing
+            inst.threadgroup_supported = True
+            cls._instance = inst
+        return cls._instance
+
+    @staticmethod
+    def _supports_block(block: PolarKeyBlock) -> None:
+        """Raises for formats the kernels cannot decode (metal.py:454-492)."""
+        if block.radii.dtype == torch.int8:
+            if block.radii_scales is None:
+                raise ValueError("int8 radii require radii_scales")
+        elif block.radii.dtype != torch.float16:
+            raise ValueError(f"unsupported radii dtype: {block.radii.dtype}")
+
+    @staticmethod
+    def _no_qjl(use_qjl: bool) -> None:
+        if use_qjl:
+            raise NotImplementedError("QJL is not supported in this release; set use_qjl=False")
+
+    def execute_fused_qk(self, q: torch.Tensor, block: PolarKeyBlock, config) -> torch.Tensor:
+        self._supports_block(block)
+        return fused_qk(q, PageSet(block, None, config.head_dim), fp16_scale(config.attention_scale))
+
+    def execute_online_attention_quant_v(
+        self,
+        q: torch.Tensor,
+        block: PolarKeyBlock,
+        quant_v: QuantizedVBlock,
+        qjl_payload: Optional[Any],
+        q_proj_signs: Optional[torch.Tensor],
+        config,
+        actual_seq_len: int,
+        use_qjl: bool = False,
+    ) -> Tuple[torch.Tensor, Dict[str, Any]]:
+        self._no_qjl(use_qjl)
+        self._supports_block(block)
+        pages = PageSet(block, quant_v, config.head_dim)
+        out = decode_attention(q, pages, None, None, actual_seq_len, fp16_scale(config.attention_scale))
+        trace = {
+            "kernel_name": "tqpolar_online_attention_quant_v",
+            "hip_kernel": "tp_decode_attention",
+            "hip_used": True,
+            "fallback_used": False,
+            "qjl_used": False,
+            "quant_v_used": True,
+            "actual_seq_len": actual_seq_len,
+            "num_queries_per_kv": q.shape[1] // pages.H,
+        }
+        return out, trace
+
+    def execute_online_attention_quant_v_dense_tail(
+        self,
+        q: torch.Tensor,
+        block: Optional[PolarKeyBlock],
+        quant_v: Optional[QuantizedVBlock],
+        tail_k: torch.Tensor,
+        tail_v: torch.Tensor,
+        qjl_payload: Optional[Any],
+        q_proj_signs: Optional[torch.Tensor],
+        config,
+        actual_seq_len: int,
+        use_qjl: bool = False,
+    ) -> Tuple[torch.Tensor, Dict[str, Any]]:
+        self._no_qjl(use_qjl)
+        pages = None
+        if block is not None:
+            self._supports_block(block)
+            pages = PageSet(block, quant_v, config.head_dim)
+        tail_len = int(tail_k.shape[2]) if tail_k is not None else 0
+        out = decode_attention(
+            q, pages, tail_k if tail_len else None, tail_v if tail_len else None,
+            actual_seq_len, fp16_scale(config.attention_scale),
+        )
+        hkv = pages.H if pages is not None else int(tail_k.shape[1])
+        trace = {
+            "kernel_name": "tqpolar_online_attention_quant_v_dense_tail",
+            "hip_kernel": "tp_decode_attention",
+            "hip_used": True,
+            "fallback_used": False,
+            "qjl_used": False,
+            "quant_v_used": True,
+            "tail_length": tail_len,
+            "actual_seq_len": actual_seq_len,
+            "num_queries_per_kv": q.shape[1] // hkv,
+        }
+        return out, trace

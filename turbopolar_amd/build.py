@@ -1,0 +1,81 @@
+"""Builds libturbopolar_hip.so (the C-ABI HIP library) in-tree for gfx950.
+
+Run as ``python -m turbopolar_amd.build`` or through ``__graft_entry__.build()``.
+Every call recompiles.  Objects go to ``turbopolar_amd/_build/`` and the shared
+library to ``turbopolar_amd/libturbopolar_hip.so``.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+CSRC = PKG_DIR / "csrc"
+BUILD_DIR = PKG_DIR / "_build"
+LIB_NAME = "libturbopolar_hip.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+ARCH = os.environ.get("TP_OFFLOAD_ARCH", "gfx950")
+
+SOURCES = ["tp_api.hip", "tp_encode.hip", "tp_attention.hip", "tp_decode.hip"]
+
+# -ffp-contract=off and correctly rounded fp32 divide/sqrt are required for the
+# encoder's bit-exact fp16 rules; packed fp32 VALU ops are disabled.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-result",
+    f"-I{REPO_DIR / 'include'}",
+    f"-I{CSRC}",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found; the TurboPolar HIP library cannot be built")
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
+
+
+def build(verbose: bool = True) -> Path:
+    BUILD_DIR.mkdir(exist_ok=True)
+    objs = []
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as ex:
+        futs = []
+        for name in SOURCES:
+            obj = BUILD_DIR / (Path(name).stem + ".o")
+            objs.append(obj)
+            futs.append(ex.submit(_compile, CSRC / name, obj))
+        for f in futs:
+            f.result()
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

@@ -1,0 +1,163 @@
+// tp_common.h -- shared device helpers of the TurboPolar gfx950 kernels.
+//
+// Bit-exactness of the encoder rests on these scalar helpers.  They restate
+// the fp16 semantics of the reference encoder
+// (rfsn_v11/quant/polar/encoder.py:24-98, rfsn_v11/quant/v_quant/encoder.py:16-30):
+//   * every fp16 op is correctly rounded: computed in fp32 and rounded once to
+//     fp16 (exact for + - * / sqrt because fp32 has >= 2*11+2 significand bits),
+//     which requires IEEE fp32 divide/sqrt and no FMA contraction -- the library
+//     is compiled with -ffp-contract=off -fhip-fp32-correctly-rounded-divide-sqrt;
+//   * round-half-to-even (rintf -> v_rndne_f32);
+//   * atan2 and log are correctly rounded to the output type: a fast fp32 path,
+//     with a float64 recomputation whenever the fp32 result lies within a few
+//     ulps of an fp16 rounding midpoint (checked exhaustively over every pair of
+//     fp16 inputs by tp_selftest_atan2_exhaustive).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "turbopolar.h"
+
+namespace tp {
+
+typedef _Float16 f16;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+constexpr int kPageTokens = 64;
+constexpr int kHeadDim = 128;
+constexpr int kPairs = 64;
+constexpr int kVGroups = 4;
+constexpr int kVGroupSize = 32;
+
+// fp16 constants of the reference's weak-scalar arithmetic.
+constexpr uint16_t kF16Pi = 0x4248;            // fp16(pi) = 3.140625
+constexpr uint16_t kF16TwoPi = 0x4648;         // fp16(2*pi) = 6.28125
+constexpr uint16_t kF16RadiusFloor = 0x0011;   // fp16(1e-6)
+constexpr uint16_t kF16VScaleFloor = 0x068E;   // fp16(1e-4)
+// float32 constants: f32(pi), f32(2*pi), f32(1 - 1e-6)
+constexpr float kF32Pi = 3.14159274101257324f;
+constexpr float kF32TwoPi = 6.28318548202514648f;
+constexpr float kF32OneMinusEps = 0.999998986721038818f;
+
+// fp32 ulps around an fp16 rounding midpoint inside which the fast atan2/log
+// results are recomputed in float64.
+constexpr int kMidpointGuard = 16;
+
+__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(f16, b); }
+__device__ __forceinline__ uint16_t f2h(float x) { return __builtin_bit_cast(uint16_t, (f16)x); }
+
+// float64 -> fp16, round to nearest even, without double rounding:
+// round to fp32 toward zero, make it sticky (round-to-odd), then RNE to fp16.
+__device__ __forceinline__ uint16_t d2h(double d) {
+  float f = __double2float_rz(d);
+  if ((double)f != d) f = __uint_as_float(__float_as_uint(f) | 1u);
+  return f2h(f);
+}
+
+// True when the fp32 value `v` is too close to an fp16 rounding boundary (or in
+// the fp16 subnormal range) for its rounding to be trusted.
+__device__ __forceinline__ bool near_f16_midpoint(float v) {
+  const uint32_t u = __float_as_uint(v) & 0x7fffffffu;
+  const int low = (int)(u & 0x1fffu) - 0x1000;
+  return u < 0x38800000u || (low <= kMidpointGuard && low >= -kMidpointGuard);
+}
+
+// Correctly rounded fp16 atan2(y, x) for fp16-representable x, y.
+__device__ __forceinline__ uint16_t atan2_f16(float y, float x) {
+  if (y == 0.0f && !__builtin_signbit(x)) return f2h(y);  // exact +-0
+  const float a = atan2f(y, x);
+  if (near_f16_midpoint(a)) return d2h(atan2((double)y, (double)x));
+  return f2h(a);
+}
+
+// Correctly rounded fp16 natural log of a positive fp16 value (or +inf).
+__device__ __forceinline__ uint16_t log_f16(float r) {
+  const float l = logf(r);
+  if (near_f16_midpoint(l)) return d2h(log((double)r));
+  return f2h(l);
+}
+
+// Correctly rounded fp16 sqrt of a non-negative fp16 value.
+__device__ __forceinline__ uint16_t sqrt_f16(float s) { return f2h(sqrtf(s)); }
+
+// encoder.py:33 for fp16 inputs: f16(sqrt(f16(f16(x*x) + f16(y*y)))).
+__device__ __forceinline__ uint16_t radius_f16_in(float x, float y) {
+  const float xx = h2f(f2h(x * x));
+  const float yy = h2f(f2h(y * y));
+  return sqrt_f16(h2f(f2h(xx + yy)));
+}
+
+// encoder.py:33 for fp32 inputs: f16(sqrt(x*x + y*y)) with fp32 ops.
+__device__ __forceinline__ uint16_t radius_f32_in(float x, float y) {
+  const float xx = x * x;
+  const float yy = y * y;
+  return f2h(sqrtf(xx + yy));
+}
+
+// encoder.py:47-55 for an fp16 angle: fp16 shift and divide, clip, then the
+// float32 product with (2^bits - 1) rounded half-even.
+__device__ __forceinline__ uint32_t angle_code_f16(uint16_t a16, int bits) {
+  float n = h2f(f2h(h2f(a16) + h2f(kF16Pi)));
+  n = h2f(f2h(n / h2f(kF16TwoPi)));
+  n = fminf(fmaxf(n, 0.0f), 1.0f);
+  const float lv = (float)((1 << bits) - 1);
+  const float c = rintf(n * lv);
+  return (uint32_t)fminf(fmaxf(c, 0.0f), lv);
+}
+
+// encoder.py:47-55 for an fp32 angle: fp32 ops, and the near-one wrap to 0.
+__device__ __forceinline__ uint32_t angle_code_f32(float a, int bits) {
+  float n = (a + kF32Pi) / kF32TwoPi;
+  n = fminf(fmaxf(n, 0.0f), 1.0f);
+  if (n > kF32OneMinusEps) n = 0.0f;
+  const float lv = (float)((1 << bits) - 1);
+  const float c = rintf(n * lv);
+  return (uint32_t)fminf(fmaxf(c, 0.0f), lv);
+}
+
+// Round-half-even to int8 with clipping; NaN maps to 0.
+__device__ __forceinline__ int32_t to_int8_rne(float q) {
+  if (q != q) return 0;
+  return (int32_t)fminf(fmaxf(rintf(q), -128.0f), 127.0f);
+}
+
+// Angle of a code, as PolarQuantDecoder computes it (decoder.py:37-55):
+// f32(code)/f32(levels-1) * f32(2*pi) - f32(pi), three separate fp32 ops.
+__device__ __forceinline__ float code_angle(uint32_t code, int bits) {
+  const float n = (float)code / (float)((1 << bits) - 1);
+  const float t = n * kF32TwoPi;
+  return t - kF32Pi;
+}
+
+// Extract code `idx` of a packed angle-code row (encoder.py:101-130 packing).
+__device__ __forceinline__ uint32_t packed_code(const uint8_t* row, int idx, int bits) {
+  if (bits == 8) return row[idx];
+  if (bits == 4) return (row[idx >> 1] >> ((idx & 1) * 4)) & 15u;
+  return (row[idx >> 2] >> ((idx & 3) * 2)) & 3u;
+}
+
+// Packed row length in bytes of n codes of `bits` bits.
+__host__ __device__ inline int packed_row_bytes(int n, int bits) {
+  if (bits == 8) return n;
+  if (bits == 4) return (n + 1) / 2;
+  return (n + 3) / 4;
+}
+
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+  return __builtin_nontemporal_load(p);
+}
+
+}  // namespace tp
+
+// Host-side error reporting shared by the C-ABI translation units.
+namespace tp {
+void set_error(const char* fmt, ...);
+void clear_error();
+bool check_layout(const tp_page_layout* layout, int* l1_row, int* deep_row);
+int32_t launch_status(const char* what);
+}  // namespace tp

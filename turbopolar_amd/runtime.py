@@ -1,0 +1,331 @@
+"""Incremental compressed KV cache: the reference's ``TurboPolarKVCacheRuntime``.
+
+Same public methods, attributes, telemetry keys and error contract as
+rfsn_v11/generation/turbo_polar_cache.py:18-395.  Differences of mechanism
+(not of behaviour):
+
+* the dense tail lives in a preallocated ``[B, H, 64, D]`` device buffer
+  instead of being re-concatenated on every append (``partial_k`` /
+  ``partial_v`` are views of it);
+* full pages are encoded by one ``tp_encode_pages`` launch per append, written
+  straight into the storage slots (no per-page Python loop, no intermediate
+  block copies);
+* a bulk append reserves capacity once (the doubling telemetry is unchanged).
+"""
+
+from __future__ import annotations
+
+from typing import Any, Dict, Optional, Tuple
+
+import torch
+
+from . import _lib
+from .codecs import GroupedVQuantizer, PolarQuantDecoder, PolarQuantEncoder
+from .config import TurboPolarConfig
+from .kernels import PAGE, encode_pages
+from .payload import PolarKeyBlock, QuantizedVBlock
+from .storage import PolarKBlockStorage, QuantVBlockStorage, pages_of
+
+
+def _nbytes(x: torch.Tensor) -> int:
+    return int(x.numel() * x.element_size())
+
+
+class TurboPolarKVCacheRuntime:
+    def __init__(self, config: TurboPolarConfig):
+        self.config = config
+        self.polar_encoder = PolarQuantEncoder(config)
+        self.v_quantizer = GroupedVQuantizer(group_size=32)
+        # QJL is rejected by the config (turbo_polar_config.py:46-47); the
+        # reference still builds an unused encoder here.
+        self.qjl_encoder = None
+        self.decoder = PolarQuantDecoder()
+
+        self.k_storage = PolarKBlockStorage()
+        self.v_storage = QuantVBlockStorage()
+        self.qjl_blocks: list = []
+        self.actual_seq_len = 0
+        self.total_blocks = 0
+        self.bytes_written = 0
+        self.bytes_read = 0
+        self.compression_time_ns = 0
+
+        self._tail_k: Optional[torch.Tensor] = None
+        self._tail_v: Optional[torch.Tensor] = None
+        self._tail_len = 0
+
+        self._initialized = False
+        self._batch_size: Optional[int] = None
+        self._num_kv_heads: Optional[int] = None
+        self._head_dim: Optional[int] = None
+        self._input_dtype = None
+
+    # ------------------------------------------------------------------
+    @property
+    def partial_k(self) -> Optional[torch.Tensor]:
+        return self._tail_k[:, :, : self._tail_len] if self._tail_len else None
+
+    @property
+    def partial_v(self) -> Optional[torch.Tensor]:
+        return self._tail_v[:, :, : self._tail_len] if self._tail_len else None
+
+    def _validate_append_inputs(self, k_new, v_new):
+        # turbo_polar_cache.py:55-104, same order and messages.
+        if not isinstance(k_new, torch.Tensor) or not isinstance(v_new, torch.Tensor):
+            raise TypeError("append() expects torch.Tensor inputs")
+        if k_new.ndim != 4 or v_new.ndim != 4:
+            raise ValueError(
+                f"append() expects 4-D inputs (B, H_kv, T, D), got {tuple(k_new.shape)} and {tuple(v_new.shape)}"
+            )
+        if k_new.shape != v_new.shape:
+            raise ValueError(f"k_new shape {tuple(k_new.shape)} must match v_new shape {tuple(v_new.shape)}")
+        B, H_kv, T_new, D = k_new.shape
+        if T_new < 1:
+            raise ValueError(f"input must have at least one token, got T={T_new}")
+        if k_new.dtype != v_new.dtype:
+            raise ValueError(f"k_new dtype {k_new.dtype} must match v_new dtype {v_new.dtype}")
+        if k_new.dtype not in (torch.float16, torch.float32):
+            raise ValueError(f"only float16 and float32 inputs are supported, got {k_new.dtype}")
+        if not bool(torch.isfinite(k_new).all()) or not bool(torch.isfinite(v_new).all()):
+            raise ValueError("append() inputs must contain finite values")
+        if self._initialized:
+            if B != self._batch_size:
+                raise ValueError(
+                    f"batch size changed from {self._batch_size} to {B}; "
+                    "TurboPolar cache does not support varying batch size."
+                )
+            if H_kv != self._num_kv_heads:
+                raise ValueError(
+                    f"KV head count changed from {self._num_kv_heads} to {H_kv}; "
+                    "TurboPolar cache does not support varying head counts."
+                )
+            if D != self._head_dim:
+                raise ValueError(
+                    f"head_dim changed from {self._head_dim} to {D}; "
+                    "TurboPolar cache does not support varying head dimension."
+                )
+            if k_new.dtype != self._input_dtype:
+                raise ValueError(
+                    f"input dtype changed from {self._input_dtype} to {k_new.dtype}; "
+                    "TurboPolar cache does not support varying dtype."
+                )
+        else:
+            if H_kv != self.config.num_kv_heads:
+                raise ValueError(f"input has {H_kv} KV heads but config expects {self.config.num_kv_heads}")
+            if D != self.config.head_dim:
+                raise ValueError(f"input head_dim {D} does not match config {self.config.head_dim}")
+            self._batch_size = B
+            self._num_kv_heads = H_kv
+            self._head_dim = D
+            self._input_dtype = k_new.dtype
+            self._initialized = True
+
+    # ------------------------------------------------------------------
+    def _page_bytes(self) -> int:
+        """Bytes the reference's _flush_block adds per page (turbo_polar_cache.py:154-161)."""
+        B, H = self._batch_size, self._num_kv_heads
+        l1_row, deep_row = self.polar_encoder.row_bytes()
+        r_item = 1 if self.polar_encoder.use_int8_radii else 2
+        k = B * H * PAGE * (self._head_dim // 2) * r_item + B * H * PAGE * (l1_row + deep_row)
+        if self.polar_encoder.use_int8_radii:
+            k += B * H * 2
+        v = B * H * PAGE * self._head_dim + B * H * PAGE * (self._head_dim // 32) * 2
+        return k + v
+
+    def _encode_into_storage(self, k: torch.Tensor, v: torch.Tensor, token_begin: int, n_pages: int) -> None:
+        B, H = self._batch_size, self._num_kv_heads
+        start = self.k_storage.block_count
+        self.k_storage.reserve(start + n_pages, self.polar_encoder, B, H, k.device)
+        self.v_storage.reserve(start + n_pages, B, H, k.device)
+        encode_pages(
+            k, v, token_begin, n_pages * PAGE, self.polar_encoder.layout,
+            pages_of(self.k_storage, self.v_storage), start,
+        )
+        self.k_storage.block_count += n_pages
+        self.v_storage.block_count += n_pages
+        self.total_blocks += n_pages
+        self.bytes_written += n_pages * self._page_bytes()
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+        """turbo_polar_cache.py:106-126: extend the tail, flush every full page."""
+        self._validate_append_inputs(k_new, v_new)
+        B, H, T, D = k_new.shape
+        self.actual_seq_len += T
+        if self._tail_k is None:
+            self._tail_k = torch.zeros((B, H, PAGE, D), dtype=k_new.dtype, device=k_new.device)
+            self._tail_v = torch.zeros((B, H, PAGE, D), dtype=k_new.dtype, device=k_new.device)
+        k_new = k_new.contiguous()
+        v_new = v_new.contiguous()
+        pos = 0
+        if self._tail_len:
+            n = min(PAGE - self._tail_len, T)
+            self._tail_k[:, :, self._tail_len : self._tail_len + n] = k_new[:, :, :n]
+            self._tail_v[:, :, self._tail_len : self._tail_len + n] = v_new[:, :, :n]
+            self._tail_len += n
+            pos = n
+            if self._tail_len == PAGE:
+                self._encode_into_storage(self._tail_k, self._tail_v, 0, 1)
+                self._tail_len = 0
+        n_full = (T - pos) // PAGE
+        if n_full:
+            self._encode_into_storage(k_new, v_new, pos, n_full)
+            pos += n_full * PAGE
+        rem = T - pos
+        if rem:
+            self._tail_k[:, :, :rem] = k_new[:, :, pos:]
+            self._tail_v[:, :, :rem] = v_new[:, :, pos:]
+            self._tail_len = rem
+
+    # ------------------------------------------------------------------
+    def get_fused_attention_inputs(
+        self,
+    ) -> Tuple[Optional[PolarKeyBlock], Optional[QuantizedVBlock], Optional[torch.Tensor], Optional[torch.Tensor], None, int]:
+        """turbo_polar_cache.py:163-198: page views, the dense tail, no QJL."""
+        compressed_k = None
+        quant_v = None
+        if self.k_storage.block_count > 0:
+            L = self.config.block_size
+            compressed_k = self.k_storage.to_unified_block(
+                (self._batch_size, self._num_kv_heads, self.k_storage.block_count * L, self._head_dim)
+            )
+            quant_v = self.v_storage.to_quantized_block()
+        return compressed_k, quant_v, self.partial_k, self.partial_v, None, self.actual_seq_len
+
+    def _maybe_encode_partial(self) -> Optional[Dict[str, Any]]:
+        """turbo_polar_cache.py:276-319: encode the zero-padded tail as a temporary page."""
+        if not self._tail_len:
+            return None
+        B, H = self._batch_size, self._num_kv_heads
+        dev = self._tail_k.device
+        bufs = self.polar_encoder.alloc_pages(B, H, 1, dev)
+        codes = torch.zeros((B, H, 1, PAGE, self._head_dim), dtype=torch.int8, device=dev)
+        scales = torch.zeros((B, H, 1, PAGE, self._head_dim // 32), dtype=torch.float16, device=dev)
+        pages = _lib.TPPages(
+            _lib.ptr(bufs["radii"]), _lib.ptr(bufs["radii_scales"]), _lib.ptr(bufs["angle_codes_l1"]),
+            _lib.ptr(bufs["angle_codes_deep"]), _lib.ptr(codes), _lib.ptr(scales), 1,
+        )
+        # The encoder reads tokens past n_tokens as zeros: the reference's
+        # mx.pad zero padding of the tail (turbo_polar_cache.py:282-285).
+        encode_pages(self._tail_k, self._tail_v, 0, self._tail_len, self.polar_encoder.layout, pages, 0)
+        return {
+            "radii": bufs["radii"],
+            "radii_scales": bufs["radii_scales"],
+            "angle_l1": bufs["angle_codes_l1"],
+            "angle_deep": bufs["angle_codes_deep"],
+            "quant_v": QuantizedVBlock(codes=codes, scales=scales, group_size=32),
+            "qjl": None,
+            "metadata": self.polar_encoder.metadata,
+        }
+
+    def get_blocks_for_attention(self):
+        """turbo_polar_cache.py:200-274: pages plus the padded tail page."""
+        partial = self._maybe_encode_partial()
+        L = self.config.block_size
+        if self.k_storage.block_count == 0:
+            if partial is None:
+                return None, None, None, None, self.actual_seq_len
+            r = partial["radii"]
+            unified_k = PolarKeyBlock(
+                radii=r,
+                angle_codes_l1=partial["angle_l1"],
+                angle_codes_deep=partial["angle_deep"],
+                radii_scales=partial["radii_scales"],
+                shape=(r.shape[0], r.shape[1], r.shape[2] * r.shape[3], r.shape[4] * 2),
+                block_size=L,
+                head_dim=self.config.head_dim,
+                metadata=partial["metadata"],
+            )
+            return unified_k, partial["quant_v"], None, None, self.actual_seq_len
+
+        compressed_k = self.k_storage.to_unified_block(
+            (self._batch_size, self._num_kv_heads, self.k_storage.block_count * L, self._head_dim)
+        )
+        quant_v = self.v_storage.to_quantized_block()
+        if partial is not None:
+            radii = torch.cat([compressed_k.radii, partial["radii"]], dim=2)
+            rs = None
+            if compressed_k.radii_scales is not None and partial["radii_scales"] is not None:
+                rs = torch.cat([compressed_k.radii_scales, partial["radii_scales"]], dim=2)
+            compressed_k = PolarKeyBlock(
+                radii=radii,
+                angle_codes_l1=torch.cat([compressed_k.angle_codes_l1, partial["angle_l1"]], dim=2),
+                angle_codes_deep=torch.cat([compressed_k.angle_codes_deep, partial["angle_deep"]], dim=2),
+                radii_scales=rs,
+                shape=(radii.shape[0], radii.shape[1], radii.shape[2] * radii.shape[3], radii.shape[4] * 2),
+                block_size=L,
+                head_dim=self.config.head_dim,
+                metadata=compressed_k.metadata,
+            )
+            pv = partial["quant_v"]
+            quant_v = QuantizedVBlock(
+                codes=torch.cat([quant_v.codes, pv.codes], dim=2),
+                scales=torch.cat([quant_v.scales, pv.scales], dim=2),
+                group_size=quant_v.group_size,
+            )
+        return compressed_k, quant_v, None, None, self.actual_seq_len
+
+    def fetch_blocks(self, indices: Optional[list] = None) -> torch.Tensor:
+        """turbo_polar_cache.py:321-346: decode selected pages to dense fp16 keys."""
+        if self.k_storage.block_count == 0:
+            return torch.empty(0)
+        if indices is None:
+            indices = list(range(self.k_storage.block_count))
+        ks = self.k_storage
+        fetched = []
+        for idx in indices:
+            block = PolarKeyBlock(
+                radii=ks.radii[:, :, idx : idx + 1],
+                angle_codes_l1=ks.angle_codes_l1[:, :, idx : idx + 1],
+                angle_codes_deep=ks.angle_codes_deep[:, :, idx : idx + 1],
+                radii_scales=ks.radii_scales[:, :, idx : idx + 1] if ks.radii_scales is not None else None,
+                shape=(self._batch_size, self._num_kv_heads, self.config.block_size, self._head_dim),
+                block_size=self.config.block_size,
+                head_dim=self._head_dim,
+                metadata=ks.metadata,
+            )
+            self.bytes_read += _nbytes(block.radii) + _nbytes(block.angle_codes_l1) + _nbytes(block.angle_codes_deep)
+            if block.radii_scales is not None:
+                self.bytes_read += _nbytes(block.radii_scales)
+            fetched.append(self.decoder.decode_block(block))
+        return torch.cat(fetched, dim=2)
+
+    def get_io_telemetry(self) -> Dict[str, Any]:
+        """turbo_polar_cache.py:348-377 (same keys and closed forms)."""
+        if self.k_storage.block_count == 0 and not self._tail_len:
+            return {}
+        D = self.config.head_dim
+        B, H = self._batch_size, self._num_kv_heads
+        dense_kv_bytes = B * H * self.actual_seq_len * D * 2 * 2
+        compressed = self.bytes_written
+        if self._tail_len:
+            compressed += 2 * B * H * self._tail_len * D * self._tail_k.element_size()
+        return {
+            "dense_kv_bytes": dense_kv_bytes,
+            "actual_cache_bytes": compressed,
+            "compression_ratio": float(dense_kv_bytes / compressed) if compressed > 0 else 0.0,
+            "total_blocks": self.total_blocks,
+            "partial_tokens": self._tail_len,
+            "k_storage_capacity": self.k_storage.capacity,
+            "v_storage_capacity": self.v_storage.capacity,
+            "k_storage_reallocs": self.k_storage.reallocation_count,
+            "v_storage_reallocs": self.v_storage.reallocation_count,
+        }
+
+    def reset(self) -> None:
+        """turbo_polar_cache.py:379-395."""
+        self.k_storage = PolarKBlockStorage()
+        self.v_storage = QuantVBlockStorage()
+        self.qjl_blocks = []
+        self.actual_seq_len = 0
+        self.total_blocks = 0
+        self.bytes_written = 0
+        self.bytes_read = 0
+        self.compression_time_ns = 0
+        self._tail_k = None
+        self._tail_v = None
+        self._tail_len = 0
+        self._initialized = False
+        self._batch_size = None
+        self._num_kv_heads = None
+        self._head_dim = None
+        self._input_dtype = None
