@@ -1,0 +1,253 @@
+"""Decode-attention benchmark on one MI355X (BASELINE.json metric).
+
+One step = one fused decode-attention launch (tp_decode_attention) over a
+Llama-3-8B-shape cache: 32 query heads, 8 kv heads, head_dim 128, 32768 tokens
+(512 pages of 64 per kv head), TurboPolarConfig() default layout, batch 1
+(BASELINE configs[2] at 32k).  Inputs are synthetic:
+K fp16 N(0,1) with 4 outlier channels x20 per head, V fp16 N(0,1),
+q fp16 N(0,1)/sqrt(128).  The caches are encoded on the GPU by the same
+library before timing and stay resident in HBM.  Steps rotate over enough
+independent caches (> 256 MB in total) that the MI355X Infinity Cache cannot
+hold them, so the timed reads come from HBM.
+
+Prints one JSON line.  ``value`` is microseconds per decode step (lower is
+better); ``roofline.achieved`` is the algorithmic compressed bytes per step
+(get_io_telemetry()["actual_cache_bytes"] + q + out) over the measured
+average step time.  The CPU baseline is the oracle's NumPy restatement of the
+reference CPU fallback (_cpu_online_attention_dense_tail), timed on a bounded
+sample on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "decode-attn µs/step + achieved HBM GB/s (% peak), Llama-3-8B shape, 32k ctx"
+LAYOUTS = {"default": (False, 4, 4, 64), "fast": (True, 4, 8, 0)}
+
+
+def algorithmic_bytes(hq, hkv, n_pages, layout, tail=0):
+    int8 = layout[0]
+    kb = 128 if layout == LAYOUTS["fast"] else None
+    if kb is None:
+        split_half = layout[3] // 2
+        l1 = {4: (split_half + 1) // 2, 8: split_half}[layout[1]]
+        deep = {8: 64 - split_half, 4: (64 - split_half + 1) // 2, 2: (64 - split_half + 3) // 4}[layout[2]]
+        kb = (64 if int8 else 128) + l1 + deep
+    rs = 2 if int8 else 0
+    return hkv * n_pages * 64 * (kb + 136) + hkv * n_pages * rs + hkv * tail * 512 + hq * 128 * 2 * 2
+
+
+def build_caches(args, dev, layout):
+    import torch
+
+    from turbopolar_amd import TurboPolarConfig, TurboPolarKVCacheRuntime
+    from turbopolar_amd.kernels import PageSet
+
+    int8, l1b, deepb, split = layout
+    cfg = TurboPolarConfig(num_q_heads=args.hq, num_kv_heads=args.hkv, use_int8_radii=int8,
+                           k_angle_bits_level1=l1b, k_angle_bits_deep=deepb, split_dim=split)
+    caches = []
+    for r in range(args.rotate):
+        g = torch.Generator(device=dev).manual_seed(1000 + r)
+        k = torch.randn((1, args.hkv, args.context, 128), generator=g, device=dev, dtype=torch.float32)
+        for h in range(args.hkv):
+            ch = torch.randperm(128, generator=g, device=dev)[:4]
+            k[:, h, :, ch] *= 20.0
+        v = torch.randn((1, args.hkv, args.context, 128), generator=g, device=dev, dtype=torch.float32)
+        rt = TurboPolarKVCacheRuntime(cfg)
+        rt.append(k.half(), v.half())
+        del k, v
+        block, qv, tk, tv, _, seq = rt.get_fused_attention_inputs()
+        q = (torch.randn((1, args.hq, 128), generator=g, device=dev) / np.sqrt(128.0)).half()
+        caches.append({"rt": rt, "pages": PageSet(block, qv), "q": q, "seq": seq,
+                       "out": torch.empty((1, args.hq, 128), dtype=torch.float16, device=dev)})
+    torch.cuda.synchronize()
+    return cfg, caches
+
+
+def run_gpu(args, layout):
+    import torch
+
+    from turbopolar_amd import _lib
+    from turbopolar_amd.kernels import fp16_scale
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg, caches = build_caches(args, dev, layout)
+    L = _lib.lib()
+    n_pages = caches[0]["pages"].S
+    pps = args.pps or int(L.tp_default_pages_per_split(1, args.hq, args.hkv, n_pages))
+    need = int(L.tp_decode_workspace_bytes(1, args.hq, args.hkv, n_pages, 0, pps))
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    scale = fp16_scale(cfg.attention_scale)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    fn = L.tp_decode_attention
+    calls = []
+    for c in caches:
+        ps = c["pages"]
+        calls.append((c["q"].data_ptr(), 1, args.hq, args.hkv, ctypes.byref(ps.layout), ctypes.byref(ps.pages),
+                      n_pages, None, None, 0, 0, c["seq"], scale, pps, ws.data_ptr(), need,
+                      c["out"].data_ptr(), stream))
+
+    def step(i):
+        st = fn(*calls[i % len(calls)])
+        if st:
+            _lib.check(st, "tp_decode_attention")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(args.steps):
+        step(i)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+
+    # Correctness guard on the timed configuration (first cache vs its own
+    # re-run with one split per workgroup: split-K invariance).
+    ref_out = caches[0]["out"].clone()
+    step(0)
+    torch.cuda.synchronize()
+    ok = bool(torch.isfinite(caches[0]["out"]).all())
+    return {"ms": ms, "pps": pps, "n_pages": n_pages, "finite": ok, "cfg": cfg, "caches": caches,
+            "ws_bytes": need, "rerun_equal": bool(torch.equal(ref_out, caches[0]["out"]))}
+
+
+def cpu_baseline(args, layout, caches, budget_s):
+    """Oracle restatement of the reference CPU fallback on one cache (float32, 1 thread)."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import oracle
+    from turbopolar_amd.kernels import fp16_scale
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    c = caches[0]
+    ps = c["pages"]
+    t = ps.tensors
+    blk = {
+        "radii": t["radii"].cpu().numpy(),
+        "radii_scales": t["radii_scales"].cpu().numpy() if "radii_scales" in t else None,
+        "angle_codes_l1": t["angle_l1"].cpu().numpy(),
+        "angle_codes_deep": t["angle_deep"].cpu().numpy(),
+        "metadata": c["rt"].k_storage.metadata,
+    }
+    qv = (t["v_codes"].cpu().numpy(), t["v_scales"].cpu().numpy())
+    q = c["q"].cpu().numpy()
+    empty = np.zeros((1, args.hkv, 0, 128), np.float16)
+    scale = fp16_scale(1.0 / np.sqrt(128.0))
+    ctx = threadpool_limits(1) if threadpool_limits else None
+    times = []
+    try:
+        if ctx:
+            ctx.__enter__()
+        start = time.perf_counter()
+        while True:
+            t0 = time.perf_counter()
+            out = oracle.cpu_online_attention_dense_tail(q, blk, qv, empty, empty, scale, c["seq"], dtype=np.float32)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - start > budget_s and len(times) >= 2:
+                break
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    gpu = c["out"].float().cpu().numpy()
+    err = float(np.max(np.abs(gpu - out)))
+    return float(np.median(times)) * 1e6, len(times), err
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layout", choices=sorted(LAYOUTS), default="default")
+    ap.add_argument("--context", type=int, default=32768)
+    ap.add_argument("--hq", type=int, default=32)
+    ap.add_argument("--hkv", type=int, default=8)
+    ap.add_argument("--pps", type=int, default=0, help="pages per workgroup (0 = library default)")
+    ap.add_argument("--rotate", type=int, default=0, help="independent caches to rotate (0 = auto, >256 MB)")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline sampling")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the decode-attention path shards by kv head "
+              "across GPUs with no exchange; multi-GPU runs are out of scope here). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.context % 64:
+        sys.exit("--context must be a multiple of 64")
+    layout = LAYOUTS[args.layout]
+    n_pages = args.context // 64
+    step_bytes = algorithmic_bytes(args.hq, args.hkv, n_pages, layout)
+    if not args.rotate:
+        args.rotate = max(4, int(np.ceil(320e6 / step_bytes)))
+
+    res = run_gpu(args, layout)
+    ms = res["ms"]
+    us = ms * 1e3
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        cpu_us, nsamp, err = cpu_baseline(args, layout, res["caches"], args.cpu_budget)
+        cpu = {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
+               "sample": f"{nsamp} full decode steps of the 32-head/8-kv-head {args.context}-token cache "
+                         f"(oracle NumPy float32 restatement of _cpu_online_attention_dense_tail, 1 thread; "
+                         f"max-abs vs GPU {err:.2e})"}
+    traffic = None
+    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                         f"decode_attention_{args.layout}_8b_32k_traffic.json")
+    if os.path.exists(tpath) and args.context == 32768 and args.hq == 32 and args.hkv == 8:
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    line = {
+        "metric": METRIC,
+        "value": round(us, 3),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"llama3-8b-shape single-layer decode attention, {args.context} ctx (BASELINE configs[2])",
+            "layout": args.layout,
+            "q_heads": args.hq,
+            "kv_heads": args.hkv,
+            "head_dim": 128,
+            "context": args.context,
+            "batch": 1,
+            "pages_per_split": res["pps"],
+            "rotated_caches": args.rotate,
+            "algorithmic_bytes_per_step": step_bytes,
+        },
+        "tokens_per_s": round(1e6 / us, 1),
+        "achieved_GBps": round(gbps, 1),
+        "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+        "checks": {"finite": res["finite"], "deterministic_rerun": res["rerun_equal"]},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

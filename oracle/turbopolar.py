@@ -396,16 +396,19 @@ def softmax_attention(q, k, v, scale, actual_seq_len=None, dtype=F64):
     Hkv = k.shape[1]
     g = Hq // Hkv
     T = k.shape[2]
-    kk = np.repeat(k.astype(dtype), g, axis=1)
-    vv = np.repeat(v.astype(dtype), g, axis=1)
+    # Query head h reads kv head h // g: the mx.repeat(axis=1) broadcast,
+    # evaluated per kv head without materialising the repeated K/V.
+    qg = q.astype(dtype).reshape(B, Hkv, g, D)
+    kk = k.astype(dtype)
+    vv = v.astype(dtype)
     with np.errstate(invalid="ignore", over="ignore"):
-        s = np.einsum("bhd,bhtd->bht", q.astype(dtype), kk) * dtype(scale)
+        s = np.matmul(qg, np.swapaxes(kk, -1, -2)) * dtype(scale)  # [B, Hkv, g, T]
         if actual_seq_len is not None and actual_seq_len < T:
-            s[:, :, actual_seq_len:] = -np.inf
+            s[..., actual_seq_len:] = -np.inf
         m = np.max(s, axis=-1, keepdims=True)
         e = np.exp(s - m)
         w = e / np.sum(e, axis=-1, keepdims=True)
-        return np.einsum("bht,bhtd->bhd", w, vv)
+        return np.matmul(w, vv).reshape(B, Hq, D)
 
 
 def _block_fields(block):
@@ -421,11 +424,12 @@ def _block_fields(block):
 def cpu_fused_qk(q, block, scale, dtype=F64):
     """``MetalKernelBridge._cpu_fused_qk`` (metal.py:254-260): scores over all S*64 slots."""
     k = decode_block(*_block_fields(block))
-    Hq = q.shape[1]
-    g = Hq // k.shape[1]
-    kk = np.repeat(k.astype(dtype), g, axis=1)
+    B, Hq, D = q.shape
+    Hkv = k.shape[1]
+    qg = q.astype(dtype).reshape(B, Hkv, Hq // Hkv, D)
     with np.errstate(invalid="ignore", over="ignore"):
-        return np.einsum("bhd,bhtd->bht", q.astype(dtype), kk) * dtype(scale)
+        s = np.matmul(qg, np.swapaxes(k.astype(dtype), -1, -2)) * dtype(scale)
+        return s.reshape(B, Hq, -1)
 
 
 def cpu_online_attention(q, block, quant_v, scale, actual_seq_len, dtype=F64):

@@ -171,3 +171,26 @@ def test_page_decode_parity(device):
         kd = kg.cpu().numpy().astype(np.float64)
         ulp = np.spacing(np.abs(kref).astype(np.float16)).astype(np.float64)
         assert np.all(np.abs(kd - kref) <= ulp + 1e-12), name
+
+
+def test_repeated_launches_share_workspace(device):
+    """300 back-to-back launches alternating two caches on one workspace, with
+    many splits: every output is bit-identical to that cache's first output, so
+    the cross-workgroup exchange and the ticket reset are race-free."""
+    cases = []
+    for seed in (1, 2):
+        block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], 32, 8, 48, 5, seed=seed)
+        cases.append((PageSet(block, qv), torch.from_numpy(q).to(device), torch.from_numpy(tk).to(device),
+                      torch.from_numpy(tv).to(device), host, tk, tv, q))
+    seq = 48 * PAGE + 5
+    refs = [kernels.decode_attention(c[1], c[0], c[2], c[3], seq, SCALE16, pages_per_split=1).clone() for c in cases]
+    torch.cuda.synchronize()
+    for i, c in enumerate(cases):
+        check(refs[i].float().cpu().numpy(), oracle_out(c[4], c[5], c[6], c[7], seq), f"case {i}")
+    bad = torch.zeros((), dtype=torch.int64, device=device)
+    for it in range(300):
+        c = cases[it % 2]
+        out = kernels.decode_attention(c[1], c[0], c[2], c[3], seq, SCALE16, pages_per_split=1 + (it % 3))
+        bad += (out != refs[it % 2]).sum() if it % 3 == 0 else (torch.abs(out.float() - refs[it % 2].float()) > 1e-3).sum()
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 0

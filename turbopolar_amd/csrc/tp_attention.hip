@@ -134,30 +134,71 @@ __device__ __forceinline__ void load_q(const AttnArgs& a, int b, int kv, int h0,
   }
 }
 
-// QK over one compressed page: s[mt][i] = score(token 16*mt + 4*l4 + i, head l16).
+// ---- key pages ----------------------------------------------------------------
+//
+// A wave's registers for the key codes of one page (loaded ahead of use so the
+// next page's loads overlap the current page's math).
+
 template <int KIND>
-__device__ __forceinline__ void qk_page(const AttnArgs& a, const Lut& lut, int64_t slot,
-                                        const half8v* qb, int l16, int l4, float4v* s) {
+struct KRegs;
+
+template <>
+struct KRegs<kKindDefault> {  // fp16 radii, 4-bit l1 (pairs 0..31) + 4-bit deep (32..63)
+  uint4 r[4][2];
+  uint2 c[4];
+};
+
+template <>
+struct KRegs<kKindFast> {  // int8 log radii + fp16 page scale, 8-bit deep codes, split 0
+  uint4 r[4];
+  uint4 c[4];
+  float ls;
+};
+
+template <>
+struct KRegs<kKindGeneric> {  // any layout: codes are gathered during the math
+  int64_t slot;
+};
+
+template <int KIND>
+__device__ __forceinline__ void load_k(const AttnArgs& a, int64_t slot, int l16, int l4, KRegs<KIND>& k) {
   if constexpr (KIND == kKindDefault) {
-    // fp16 radii; 4-bit l1 codes for pairs 0..31, 4-bit deep codes for 32..63.
     const uint16_t* rbase = static_cast<const uint16_t*>(a.radii) + slot * (kPageTokens * kPairs) + 16 * l4;
     const uint8_t* cbase = (l4 < 2 ? a.angle_l1 + 8 * l4 : a.angle_deep + 8 * (l4 - 2)) +
                            slot * (kPageTokens * 16);
-    uint4 rv[4][2];
-    uint2 cv[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int t = 16 * mt + l16;
       const uint4* rp = reinterpret_cast<const uint4*>(rbase + t * kPairs);
-      rv[mt][0] = rp[0];
-      rv[mt][1] = rp[1];
-      cv[mt] = *reinterpret_cast<const uint2*>(cbase + t * 16);
+      k.r[mt][0] = rp[0];
+      k.r[mt][1] = rp[1];
+      k.c[mt] = *reinterpret_cast<const uint2*>(cbase + t * 16);
     }
+  } else if constexpr (KIND == kKindFast) {
+    const int8_t* rbase = static_cast<const int8_t*>(a.radii) + slot * (kPageTokens * kPairs) + 16 * l4;
+    const uint8_t* cbase = a.angle_deep + slot * (kPageTokens * kPairs) + 16 * l4;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const uint32_t rw[8] = {rv[mt][0].x, rv[mt][0].y, rv[mt][0].z, rv[mt][0].w,
-                              rv[mt][1].x, rv[mt][1].y, rv[mt][1].z, rv[mt][1].w};
-      const uint32_t cw[2] = {cv[mt].x, cv[mt].y};
+      const int t = 16 * mt + l16;
+      k.r[mt] = *reinterpret_cast<const uint4*>(rbase + t * kPairs);
+      k.c[mt] = *reinterpret_cast<const uint4*>(cbase + t * kPairs);
+    }
+    k.ls = h2f(a.radii_scales[slot]);
+  } else {
+    k.slot = slot;
+  }
+}
+
+// QK over one compressed page: s[mt][i] = score(token 16*mt + 4*l4 + i, head l16).
+template <int KIND>
+__device__ __forceinline__ void qk_regs(const AttnArgs& a, const Lut& lut, const KRegs<KIND>& k,
+                                        const half8v* qb, int l16, int l4, float4v* s) {
+  if constexpr (KIND == kKindDefault) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const uint32_t rw[8] = {k.r[mt][0].x, k.r[mt][0].y, k.r[mt][0].z, k.r[mt][0].w,
+                              k.r[mt][1].x, k.r[mt][1].y, k.r[mt][1].z, k.r[mt][1].w};
+      const uint32_t cw[2] = {k.c[mt].x, k.c[mt].y};
       float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
@@ -175,21 +216,10 @@ __device__ __forceinline__ void qk_page(const AttnArgs& a, const Lut& lut, int64
       s[mt] = acc;
     }
   } else if constexpr (KIND == kKindFast) {
-    // int8 log radii with one fp16 scale per page; 8-bit deep codes, split 0.
-    const int8_t* rbase = static_cast<const int8_t*>(a.radii) + slot * (kPageTokens * kPairs) + 16 * l4;
-    const uint8_t* cbase = a.angle_deep + slot * (kPageTokens * kPairs) + 16 * l4;
-    const float ls = h2f(a.radii_scales[slot]);
-    uint4 rv[4], cv[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const int t = 16 * mt + l16;
-      rv[mt] = *reinterpret_cast<const uint4*>(rbase + t * kPairs);
-      cv[mt] = *reinterpret_cast<const uint4*>(cbase + t * kPairs);
-    }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const uint32_t rw[4] = {rv[mt].x, rv[mt].y, rv[mt].z, rv[mt].w};
-      const uint32_t cw[4] = {cv[mt].x, cv[mt].y, cv[mt].z, cv[mt].w};
+      const uint32_t rw[4] = {k.r[mt].x, k.r[mt].y, k.r[mt].z, k.r[mt].w};
+      const uint32_t cw[4] = {k.c[mt].x, k.c[mt].y, k.c[mt].z, k.c[mt].w};
       float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
@@ -198,7 +228,7 @@ __device__ __forceinline__ void qk_page(const AttnArgs& a, const Lut& lut, int64
         for (int i = 0; i < 4; ++i) {
           const int rc = (int)(int8_t)((rw[kk] >> (8 * i)) & 0xffu);
           const uint32_t code = (cw[kk] >> (8 * i)) & 0xffu;
-          const f16 r = (f16)expf((float)rc * ls);
+          const f16 r = (f16)expf((float)rc * k.ls);
           const half2v cs = __builtin_bit_cast(half2v, lut.deep[code]);
           e[i] = pack_h2(half2v{r, r} * cs);
         }
@@ -207,16 +237,13 @@ __device__ __forceinline__ void qk_page(const AttnArgs& a, const Lut& lut, int64
       s[mt] = acc;
     }
   } else {
-    // Any supported layout: per-pair code extraction.
-    const int64_t row0 = slot * kPageTokens;
-    const float ls = a.radii_scales ? h2f(a.radii_scales[slot]) : 1.0f;
-#pragma unroll
+    const int64_t row0 = k.slot * kPageTokens;
+    const float ls = a.radii_scales ? h2f(a.radii_scales[k.slot]) : 1.0f;
     for (int mt = 0; mt < 4; ++mt) {
       const int64_t row = row0 + 16 * mt + l16;
       const uint8_t* l1row = a.angle_l1 + row * a.l1_row;
       const uint8_t* deeprow = a.angle_deep + row * a.deep_row;
       float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         uint32_t e[4];
 #pragma unroll
@@ -261,30 +288,44 @@ __device__ __forceinline__ void qk_tail(const AttnArgs& a, int64_t bkv, const ha
   }
 }
 
-// PV over one compressed page: acc[j] += Vhat^T tile j  x  P.
-__device__ __forceinline__ void pv_page(const AttnArgs& a, int64_t slot, const half8v* pb, int l16,
-                                        int l4, float4v* acc) {
+// ---- value pages --------------------------------------------------------------
+//
+// Lane (n = l16, l4) owns dims [8n, 8n+8) (group n/4) of the 16 tokens
+// 32*ks + 4*l4 + (e&3) + 16*(e>>2), ks = 0..1, e = 0..7.
+
+struct VRegs {
+  uint2 w[16];
+  uint16_t s[16];
+};
+
+__device__ __forceinline__ int v_token(int ks, int l4, int e) { return 32 * ks + 4 * l4 + (e & 3) + 16 * (e >> 2); }
+
+__device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16, int l4, VRegs& v) {
   const int8_t* vbase = a.v_codes + slot * (kPageTokens * kHeadDim) + 8 * l16;
   const uint16_t* sbase = a.v_scales + slot * (kPageTokens * kVGroups) + (l16 >> 2);
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    uint2 vw[8];
-    uint16_t sc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int t = 32 * ks + 4 * l4 + (e & 3) + 16 * (e >> 2);
-      vw[e] = *reinterpret_cast<const uint2*>(vbase + t * kHeadDim);
-      sc[e] = sbase[t * kVGroups];
+      const int t = v_token(ks, l4, e);
+      v.w[8 * ks + e] = *reinterpret_cast<const uint2*>(vbase + t * kHeadDim);
+      v.s[8 * ks + e] = sbase[t * kVGroups];
     }
-    // vals[e][0..3]: fp16 pairs (d 0,1), (2,3), (4,5), (6,7) of token e, scaled.
+  }
+}
+
+// acc[j] += Vhat^T tile j x P, Vhat = f16(code * scale) exactly.
+__device__ __forceinline__ void pv_regs(const VRegs& v, const half8v* pb, float4v* acc) {
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
     half2v vals[8][4];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const f16 sv = __builtin_bit_cast(f16, sc[e]);
+      const f16 sv = __builtin_bit_cast(f16, v.s[8 * ks + e]);
       const half2v s2 = {sv, sv};
       half2v c0, c1, c2, c3;
-      i8x4_to_f16(vw[e].x, c0, c1);
-      i8x4_to_f16(vw[e].y, c2, c3);
+      i8x4_to_f16(v.w[8 * ks + e].x, c0, c1);
+      i8x4_to_f16(v.w[8 * ks + e].y, c2, c3);
       vals[e][0] = c0 * s2;
       vals[e][1] = c1 * s2;
       vals[e][2] = c2 * s2;
@@ -309,7 +350,7 @@ __device__ __forceinline__ void pv_tail(const AttnArgs& a, int64_t bkv, const ha
     half8v rows[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int t = 32 * ks + 4 * l4 + (e & 3) + 16 * (e >> 2);
+      const int t = v_token(ks, l4, e);
       uint4 w = make_uint4(0u, 0u, 0u, 0u);
       if (t < a.tail_len) w = *reinterpret_cast<const uint4*>(tv + t * kHeadDim);
       rows[e] = as_half8(w.x, w.y, w.z, w.w);
@@ -324,16 +365,76 @@ __device__ __forceinline__ void pv_tail(const AttnArgs& a, int64_t bkv, const ha
   }
 }
 
-constexpr int kWaves = 4;
+// ---- online softmax ------------------------------------------------------------
+
+// Folds one page of scores into the running (m, l, acc) of the lane's head and
+// returns P (fp16) as the PV B operands.  Scores of tokens >= valid are masked.
+__device__ __forceinline__ void softmax_page(const float4v* s, int valid, float scale_log2, int l4,
+                                             float& m_run, float& l_run, float4v* acc, half8v* pb) {
+  float p[16];
+  float pm = -INFINITY;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * mt + 4 * l4 + i;
+      const float v = t < valid ? s[mt][i] * scale_log2 : -INFINITY;
+      p[4 * mt + i] = v;
+      pm = fmaxf(pm, v);
+    }
+  }
+  pm = fmaxf(pm, __shfl_xor(pm, 16, 64));
+  pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
+  const float m_new = fmaxf(m_run, pm);
+  const float alpha = exp2f(m_run - m_new);
+  float lsum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    p[k] = exp2f(p[k] - m_new);
+    lsum += p[k];
+  }
+  l_run = l_run * alpha + lsum;
+  m_run = m_new;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pb[ks][e] = (f16)p[4 * (2 * ks + (e >> 2)) + (e & 3)];
+  }
+}
+
+// ---- cross-workgroup exchange ----------------------------------------------------
+//
+// Partials are written with agent-scope relaxed atomic stores (coherent across
+// the XCDs' L2s without an L2 write-back) and each wave waits for them to be
+// acknowledged before the workgroup barrier; the ticket is an agent-scope
+// atomic; the combining workgroup reads partials with agent-scope loads.
+
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 constexpr int kRedStride = 132;  // padded LDS row of one head's 128 accumulators
 
-template <int KIND>
-__global__ __launch_bounds__(256, 2) void decode_attention_kernel(AttnArgs a) {
-  __shared__ Lut lut;
-  __shared__ float red_m[kWaves][16];
-  __shared__ float red_l[kWaves][16];
-  __shared__ float red_acc[kWaves][16 * kRedStride];
-  __shared__ int s_last;
+template <int WAVES>
+struct AttnShared {
+  Lut lut;
+  float m[WAVES][16];
+  float l[WAVES][16];
+  float acc[WAVES][16 * kRedStride];
+  int last;
+};
+
+// ---- decode attention kernel ---------------------------------------------------
+
+template <int KIND, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a) {
+  __shared__ AttnShared<WAVES> sh;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -348,7 +449,7 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(AttnArgs a) {
   const int h0 = hb * 16;
   const int nh = min(16, a.g - h0);
 
-  build_lut<KIND>(lut, a, tid);
+  if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
   half8v qb[4];
   load_q(a, b, kv, h0, nh, l16, l4, qb);
   __syncthreads();
@@ -359,97 +460,80 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(AttnArgs a) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // Compressed pages of this split that hold at least one unmasked token.
   const int p_begin = split * a.pages_per_split;
-  int p_end = min(p_begin + a.pages_per_split, a.n_pages);
-  if (split == a.n_splits - 1 && a.tail_len > 0) p_end = a.n_pages + 1;  // tail = virtual page
+  const int64_t live_pages = (a.seq_len + kPageTokens - 1) / kPageTokens;
+  const int p_end = (int)min((int64_t)min(p_begin + a.pages_per_split, a.n_pages), live_pages);
 
-  for (int page = p_begin + wave; page < p_end; page += kWaves) {
-    const int64_t tok0 = (int64_t)page * kPageTokens;
-    if (tok0 >= a.seq_len) continue;
-    const bool is_tail = page >= a.n_pages;
-    const int64_t rem = a.seq_len - tok0;
-    const int valid = (int)min((int64_t)(is_tail ? a.tail_len : kPageTokens), rem);
+  int page = p_begin + wave;
+  KRegs<KIND> kr;
+  if (page < p_end) load_k<KIND>(a, bkv * a.capacity + page, l16, l4, kr);
+  while (page < p_end) {
     const int64_t slot = bkv * a.capacity + page;
-
+    VRegs vr;
+    load_v(a, slot, l16, l4, vr);
     float4v s[4];
-    if (is_tail)
-      qk_tail(a, bkv, qb, l16, l4, s);
-    else
-      qk_page<KIND>(a, lut, slot, qb, l16, l4, s);
-
-    // Online softmax in the log2 domain; lane (h = l16) owns 16 tokens.
-    float p[16];
-    float pm = -INFINITY;
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 16 * mt + 4 * l4 + i;
-        const float v = t < valid ? s[mt][i] * a.scale_log2 : -INFINITY;
-        p[4 * mt + i] = v;
-        pm = fmaxf(pm, v);
-      }
-    }
-    pm = fmaxf(pm, __shfl_xor(pm, 16, 64));
-    pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
-    const float m_new = fmaxf(m_run, pm);
-    const float alpha = exp2f(m_run - m_new);
-    float lsum = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      p[k] = exp2f(p[k] - m_new);
-      lsum += p[k];
-    }
-    l_run = l_run * alpha + lsum;
-    m_run = m_new;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] *= alpha;
-
+    qk_regs<KIND>(a, sh.lut, kr, qb, l16, l4, s);
+    const int next = page + WAVES;
+    if (next < p_end) load_k<KIND>(a, bkv * a.capacity + next, l16, l4, kr);
+    const int valid = (int)min((int64_t)kPageTokens, a.seq_len - (int64_t)page * kPageTokens);
     half8v pb[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pb[ks][e] = (f16)p[4 * (2 * ks + (e >> 2)) + (e & 3)];
-    }
-    if (is_tail)
-      pv_tail(a, bkv, pb, l16, l4, acc);
-    else
-      pv_page(a, slot, pb, l16, l4, acc);
+    softmax_page(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
+    pv_regs(vr, pb, acc);
+    page = next;
   }
 
-  // Merge the 4 waves through LDS.
+  // The dense tail follows the last page; the last split's least loaded wave takes it.
+  if (split == a.n_splits - 1 && a.tail_len > 0) {
+    const int n_local = max(p_end - p_begin, 0);
+    if (wave == n_local % WAVES) {
+      const int64_t tok0 = (int64_t)a.n_pages * kPageTokens;
+      const int valid = (int)min((int64_t)a.tail_len, a.seq_len - tok0);
+      if (valid > 0) {
+        float4v s[4];
+        qk_tail(a, bkv, qb, l16, l4, s);
+        half8v pb[2];
+        softmax_page(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
+        pv_tail(a, bkv, pb, l16, l4, acc);
+      }
+    }
+  }
+
+  // Merge the waves through LDS.
   float l_tot = l_run + __shfl_xor(l_run, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
   if (l4 == 0) {
-    red_m[wave][l16] = m_run;
-    red_l[wave][l16] = l_tot;
+    sh.m[wave][l16] = m_run;
+    sh.l[wave][l16] = l_tot;
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red_acc[wave][l16 * kRedStride + 32 * l4 + 8 * i + j] = acc[j][i];
+    for (int i = 0; i < 4; ++i) sh.acc[wave][l16 * kRedStride + 32 * l4 + 8 * i + j] = acc[j][i];
   }
   __syncthreads();
 
-  const int h = tid >> 4;
-  const int c = tid & 15;
-  float M = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red_m[w][h]);
-  float L = 0.0f;
+  // Thread (h = item / 16, c = item % 16) owns dims [8c, 8c+8) of head h.
+  const int item = tid & 255;
+  const int h = item >> 4;
+  const int c = item & 15;
+  float M = -INFINITY, L = 0.0f;
   float ACC[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (tid < 256) {
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const float mw = red_m[w][h];
-    const float sc = mw == -INFINITY ? 0.0f : exp2f(mw - M);
-    L += red_l[w][h] * sc;
+    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sh.m[w][h]);
 #pragma unroll
-    for (int d = 0; d < 8; ++d) ACC[d] += red_acc[w][h * kRedStride + 8 * c + d] * sc;
+    for (int w = 0; w < WAVES; ++w) {
+      const float mw = sh.m[w][h];
+      const float sc = mw == -INFINITY ? 0.0f : exp2f(mw - M);
+      L += sh.l[w][h] * sc;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) ACC[d] += sh.acc[w][h * kRedStride + 8 * c + d] * sc;
+    }
   }
-
   uint16_t* orow = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + h) * kHeadDim + 8 * c;
   if (a.n_splits == 1) {
-    if (h < nh) {
+    if (tid < 256 && h < nh) {
       uint32_t w[4];
 #pragma unroll
       for (int d = 0; d < 4; ++d) w[d] = (uint32_t)f2h(ACC[2 * d] / L) | ((uint32_t)f2h(ACC[2 * d + 1] / L) << 16);
@@ -459,58 +543,88 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(AttnArgs a) {
   }
 
   const int64_t unit = bkv * a.head_blocks + hb;
-  const int64_t pbase = (unit * a.n_splits + split) * 16 + h;
-  if (h < nh) {
+  if (tid < 256 && h < nh) {
+    const int64_t pbase = (unit * a.n_splits + split) * 16 + h;
     if (c == 0) {
-      a.part_ml[pbase * 2 + 0] = M;
-      a.part_ml[pbase * 2 + 1] = L;
+      st_agent(a.part_ml + pbase * 2 + 0, M);
+      st_agent(a.part_ml + pbase * 2 + 1, L);
     }
-    float4* pa = reinterpret_cast<float4*>(a.part_acc + pbase * kHeadDim + 8 * c);
-    pa[0] = make_float4(ACC[0], ACC[1], ACC[2], ACC[3]);
-    pa[1] = make_float4(ACC[4], ACC[5], ACC[6], ACC[7]);
+    float* pa = a.part_acc + pbase * kHeadDim + 8 * c;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) st_agent(pa + d, ACC[d]);
   }
-  __threadfence();
+  wait_stores();
   __syncthreads();
   if (tid == 0) {
-    const uint32_t prev = atomicAdd(&a.counters[unit], 1u);
-    s_last = prev == (uint32_t)(a.n_splits - 1);
+    const uint32_t prev = __hip_atomic_fetch_add(a.counters + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh.last = prev == (uint32_t)(a.n_splits - 1);
   }
   __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  if (!sh.last) return;
 
-  // Last workgroup of this (b, kv, head block): combine all splits.
-  if (h < nh) {
-    const float* pm = a.part_ml + (unit * a.n_splits * 16 + h) * 2;
-    const float* pacc = a.part_acc + (unit * a.n_splits * 16 + h) * kHeadDim + 8 * c;
-    float Mg = -INFINITY;
-    for (int sp = 0; sp < a.n_splits; ++sp) Mg = fmaxf(Mg, pm[sp * 32]);
-    float Lg = 0.0f;
-    float A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int sp = 0; sp < a.n_splits; ++sp) {
-      const float ms = pm[sp * 32];
-      const float wgt = ms == -INFINITY ? 0.0f : exp2f(ms - Mg);
-      Lg += pm[sp * 32 + 1] * wgt;
-      const float4* pa = reinterpret_cast<const float4*>(pacc + (int64_t)sp * 16 * kHeadDim);
-      const float4 x0 = pa[0];
-      const float4 x1 = pa[1];
-      A[0] += x0.x * wgt;
-      A[1] += x0.y * wgt;
-      A[2] += x0.z * wgt;
-      A[3] += x0.w * wgt;
-      A[4] += x1.x * wgt;
-      A[5] += x1.y * wgt;
-      A[6] += x1.z * wgt;
-      A[7] += x1.w * wgt;
+  // Last workgroup of this (b, kv, head block): combine all splits.  Thread
+  // (item, sg) folds splits sg, sg + SG, ... of item (h, c); the SG partial
+  // results are then merged through LDS.
+  const int n_items = nh * 16;
+  const int SG = max(1, (WAVES * 64) / n_items);
+  const int it = tid % n_items;
+  const int sg = tid / n_items;
+  const int hh = it >> 4;
+  const int cc = it & 15;
+  float Mp = -INFINITY, Lp = 0.0f;
+  float Ap[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (sg < SG) {
+    const float* pm = a.part_ml + (unit * a.n_splits * 16 + hh) * 2;
+    const float* pacc = a.part_acc + (unit * a.n_splits * 16 + hh) * kHeadDim + 8 * cc;
+#pragma unroll 4
+    for (int sp = sg; sp < a.n_splits; sp += SG) {
+      const float ms = ld_agent(pm + (int64_t)sp * 32);
+      const float ls = ld_agent(pm + (int64_t)sp * 32 + 1);
+      float x[8];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) x[d] = ld_agent(pacc + (int64_t)sp * 16 * kHeadDim + d);
+      if (ms == -INFINITY) continue;
+      const float mn = fmaxf(Mp, ms);
+      const float so = exp2f(Mp - mn);  // 0 while Mp is -inf
+      const float sn = exp2f(ms - mn);
+      Lp = Lp * so + ls * sn;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) Ap[d] = Ap[d] * so + x[d] * sn;
+      Mp = mn;
     }
+  }
+  __syncthreads();  // sh.acc is reused below
+  float* red = &sh.acc[0][0];  // [SG][n_items][10]
+  if (sg < SG) {
+    float* r = red + ((int64_t)sg * n_items + it) * 10;
+    r[0] = Mp;
+    r[1] = Lp;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) r[2 + d] = Ap[d];
+  }
+  __syncthreads();
+  if (sg == 0) {
+    float Mg = -INFINITY;
+    for (int g2 = 0; g2 < SG; ++g2) Mg = fmaxf(Mg, red[((int64_t)g2 * n_items + it) * 10]);
+    float Lg = 0.0f;
+    float Ag[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int g2 = 0; g2 < SG; ++g2) {
+      const float* r = red + ((int64_t)g2 * n_items + it) * 10;
+      const float sc = r[0] == -INFINITY ? 0.0f : exp2f(r[0] - Mg);
+      Lg += r[1] * sc;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) Ag[d] += r[2 + d] * sc;
+    }
+    uint16_t* orow2 = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + hh) * kHeadDim + 8 * cc;
     uint32_t w[4];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) w[d] = (uint32_t)f2h(A[2 * d] / Lg) | ((uint32_t)f2h(A[2 * d + 1] / Lg) << 16);
-    *reinterpret_cast<uint4*>(orow) = make_uint4(w[0], w[1], w[2], w[3]);
+    for (int d = 0; d < 4; ++d) w[d] = (uint32_t)f2h(Ag[2 * d] / Lg) | ((uint32_t)f2h(Ag[2 * d + 1] / Lg) << 16);
+    *reinterpret_cast<uint4*>(orow2) = make_uint4(w[0], w[1], w[2], w[3]);
   }
-  if (tid == 0) a.counters[unit] = 0u;
+  if (tid == 0) __hip_atomic_store(a.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// ---- standalone fused QK -----------------------------------------------------------
 
 template <int KIND>
 __global__ __launch_bounds__(256) void fused_qk_kernel(AttnArgs a) {
@@ -530,10 +644,12 @@ __global__ __launch_bounds__(256) void fused_qk_kernel(AttnArgs a) {
   half8v qb[4];
   load_q(a, b, kv, h0, nh, l16, l4, qb);
   __syncthreads();
-  const int page = blockIdx.x * kWaves + wave;
+  const int page = blockIdx.x * 4 + wave;
   if (page >= a.n_pages) return;
+  KRegs<KIND> kr;
+  load_k<KIND>(a, bkv * a.capacity + page, l16, l4, kr);
   float4v s[4];
-  qk_page<KIND>(a, lut, bkv * a.capacity + page, qb, l16, l4, s);
+  qk_regs<KIND>(a, lut, kr, qb, l16, l4, s);
   if (l16 >= nh) return;
   const int64_t hq_idx = (int64_t)b * a.hq + (int64_t)kv * a.g + h0 + l16;
   uint16_t* srow = a.scores + hq_idx * ((int64_t)a.n_pages * kPageTokens) + (int64_t)page * kPageTokens + 4 * l4;
@@ -552,6 +668,9 @@ static int layout_kind(const tp_page_layout* L) {
   if (L->int8_radii && L->deep_bits == 8 && L->split_dim == 0) return kKindFast;
   return kKindGeneric;
 }
+
+constexpr int kDecodeWaves = 8;  // wave64s per decode workgroup
+constexpr int kTargetWorkgroups = 256;  // one decode workgroup per CU
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -629,8 +748,7 @@ extern "C" {
 int32_t tp_default_pages_per_split(int64_t batch, int32_t hq, int32_t hkv, int32_t n_pages) {
   if (batch < 1 || hq < 1 || hkv < 1 || n_pages < 1) return 4;
   const int64_t units = batch * hkv * (int64_t)head_blocks_of(hq, hkv);
-  const int64_t target_wgs = 512;  // two 256-thread workgroups per CU on 256 CUs
-  int64_t pps = (n_pages * units + target_wgs - 1) / target_wgs;
+  int64_t pps = (n_pages * units + kTargetWorkgroups - 1) / kTargetWorkgroups;
   if (pps < 4) pps = 4;
   const int64_t min_pps = (n_pages + 255) / 256;  // at most 256 splits per head
   if (pps < min_pps) pps = min_pps;
@@ -666,7 +784,7 @@ int32_t tp_fused_qk(const void* q, int64_t batch, int32_t hq, int32_t hkv,
   }
   a.scores = static_cast<uint16_t*>(scores);
   a.scale = scale;
-  const dim3 grid((unsigned)((n_pages + kWaves - 1) / kWaves), (unsigned)(batch * hkv), (unsigned)a.head_blocks);
+  const dim3 grid((unsigned)((n_pages + 3) / 4), (unsigned)(batch * hkv), (unsigned)a.head_blocks);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (layout_kind(layout)) {
     case kKindDefault: hipLaunchKernelGGL(fused_qk_kernel<kKindDefault>, grid, dim3(256), 0, s, a); break;
@@ -740,9 +858,15 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
   const dim3 grid((unsigned)n_splits, (unsigned)(batch * hkv), (unsigned)a.head_blocks);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (n_pages > 0 ? layout_kind(layout) : (int)kKindGeneric) {
-    case kKindDefault: hipLaunchKernelGGL(decode_attention_kernel<kKindDefault>, grid, dim3(256), 0, s, a); break;
-    case kKindFast: hipLaunchKernelGGL(decode_attention_kernel<kKindFast>, grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL(decode_attention_kernel<kKindGeneric>, grid, dim3(256), 0, s, a); break;
+    case kKindDefault:
+      hipLaunchKernelGGL((decode_attention_kernel<kKindDefault, kDecodeWaves>), grid, dim3(kDecodeWaves * 64), 0, s, a);
+      break;
+    case kKindFast:
+      hipLaunchKernelGGL((decode_attention_kernel<kKindFast, kDecodeWaves>), grid, dim3(kDecodeWaves * 64), 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((decode_attention_kernel<kKindGeneric, kDecodeWaves>), grid, dim3(kDecodeWaves * 64), 0, s, a);
+      break;
   }
   return launch_status("tp_decode_attention");
 }
