@@ -169,8 +169,27 @@ def cpu_baseline(args, layout, caches, budget_s):
     return float(np.median(times)) * 1e6, len(times), err
 
 
+def copy_calibration(nbytes: int, reps: int = 10) -> None:
+    """Plain device-to-device copy of a known size: the reference for scaling
+    rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    # Push the source out of the caches' reach before each copy.
+    flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
+    for _ in range(reps):
+        flush.zero_()
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "reps": reps}))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain copy of BYTES bytes (counter calibration)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
@@ -183,6 +202,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the decode-attention path shards by kv head "
               "across GPUs with no exchange; multi-GPU runs are out of scope here). Use --gpus 1.",

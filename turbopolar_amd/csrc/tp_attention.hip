@@ -85,11 +85,40 @@ __device__ __forceinline__ half2v hi_hi(uint32_t w) {
   return half2v{r, r};
 }
 
-// (cos, sin) of a code's decoded angle, rounded to fp16 and packed.
+// (cos, sin) of a code's decoded angle theta = 2*pi*code/(2^bits-1) - pi
+// (decoder.py:37-55), rounded to fp16 and packed.  v_sin_f32 / v_cos_f32 take
+// revolutions, so theta is passed as code/(2^bits-1) - 1/2.
 __device__ __forceinline__ uint32_t make_cs(uint32_t code, int bits) {
-  const float th = code_angle(code, bits);
-  const half2v cs = {(f16)cosf(th), (f16)sinf(th)};
+  const float x = (float)code / (float)((1 << bits) - 1) - 0.5f;
+  const half2v cs = {(f16)__builtin_amdgcn_cosf(x), (f16)__builtin_amdgcn_sinf(x)};
   return pack_h2(cs);
+}
+
+// Two int8 codes (byte B of `lo` and of `hi`) -> an exact fp16 pair, one SDWA
+// convert per element (sign-extended byte select, word-select destination).
+#define TP_I8PAIR_TO_F16(B)                                                                   \
+  __device__ __forceinline__ uint32_t i8pair_f16_b##B(uint32_t lo, uint32_t hi) {            \
+    uint32_t d;                                                                               \
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_" #B \
+        : "=v"(d)                                                                             \
+        : "v"(lo));                                                                           \
+    asm("v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_" #B \
+        : "=v"(d)                                                                             \
+        : "0"(d), "v"(hi));                                                                   \
+    return d;                                                                                 \
+  }
+TP_I8PAIR_TO_F16(0)
+TP_I8PAIR_TO_F16(1)
+TP_I8PAIR_TO_F16(2)
+TP_I8PAIR_TO_F16(3)
+#undef TP_I8PAIR_TO_F16
+
+template <int B>
+__device__ __forceinline__ uint32_t i8pair_f16(uint32_t lo, uint32_t hi) {
+  if constexpr (B == 0) return i8pair_f16_b0(lo, hi);
+  if constexpr (B == 1) return i8pair_f16_b1(lo, hi);
+  if constexpr (B == 2) return i8pair_f16_b2(lo, hi);
+  return i8pair_f16_b3(lo, hi);
 }
 
 // Four int8 codes -> two exact fp16 pairs: bias the byte into the mantissa of
@@ -106,13 +135,14 @@ __device__ __forceinline__ void i8x4_to_f16(uint32_t w, half2v& lo, half2v& hi) 
 struct Lut {
   uint32_t l1[256];
   uint32_t deep[256];
+  uint2 pair[256];  // 4-bit layouts: (cos, sin) of both nibbles of a code byte
 };
 
 template <int KIND>
 __device__ __forceinline__ void build_lut(Lut& lut, const AttnArgs& a, int tid) {
   const uint32_t c = (uint32_t)tid;
   if constexpr (KIND == kKindDefault) {
-    if (c < 16) lut.deep[c] = make_cs(c, 4);
+    lut.pair[c] = make_uint2(make_cs(c & 15u, 4), make_cs(c >> 4, 4));
   } else if constexpr (KIND == kKindFast) {
     lut.deep[c] = make_cs(c, 8);
   } else {
@@ -202,15 +232,16 @@ __device__ __forceinline__ void qk_regs(const AttnArgs& a, const Lut& lut, const
       float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
+        // Code bytes 2kk and 2kk+1 hold the nibbles of pairs 4kk .. 4kk+3.
+        const uint32_t b0 = (cw[kk >> 1] >> (16 * (kk & 1))) & 0xffu;
+        const uint32_t b1 = (cw[kk >> 1] >> (16 * (kk & 1) + 8)) & 0xffu;
+        const uint2 cs01 = lut.pair[b0];
+        const uint2 cs23 = lut.pair[b1];
         uint32_t e[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = 4 * kk + i;
-          const uint32_t code = (cw[j >> 3] >> (4 * (j & 7))) & 15u;
-          const half2v cs = __builtin_bit_cast(half2v, lut.deep[code]);
-          const half2v rr = (j & 1) ? hi_hi(rw[j >> 1]) : lo_lo(rw[j >> 1]);
-          e[i] = pack_h2(rr * cs);
-        }
+        e[0] = pack_h2(lo_lo(rw[2 * kk]) * __builtin_bit_cast(half2v, cs01.x));
+        e[1] = pack_h2(hi_hi(rw[2 * kk]) * __builtin_bit_cast(half2v, cs01.y));
+        e[2] = pack_h2(lo_lo(rw[2 * kk + 1]) * __builtin_bit_cast(half2v, cs23.x));
+        e[3] = pack_h2(hi_hi(rw[2 * kk + 1]) * __builtin_bit_cast(half2v, cs23.y));
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(e[0], e[1], e[2], e[3]), qb[kk], acc, 0, 0, 0);
       }
       s[mt] = acc;
@@ -295,7 +326,7 @@ __device__ __forceinline__ void qk_tail(const AttnArgs& a, int64_t bkv, const ha
 
 struct VRegs {
   uint2 w[16];
-  uint16_t s[16];
+  half2v s[8];  // scales of tokens (2q, 2q+1) of each k-step
 };
 
 __device__ __forceinline__ int v_token(int ks, int l4, int e) { return 32 * ks + 4 * l4 + (e & 3) + 16 * (e >> 2); }
@@ -309,35 +340,44 @@ __device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16,
     for (int e = 0; e < 8; ++e) {
       const int t = v_token(ks, l4, e);
       v.w[8 * ks + e] = *reinterpret_cast<const uint2*>(vbase + t * kHeadDim);
-      v.s[8 * ks + e] = sbase[t * kVGroups];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f16* sp = reinterpret_cast<const f16*>(sbase);
+      v.s[4 * ks + q] = half2v{sp[v_token(ks, l4, 2 * q) * kVGroups], sp[v_token(ks, l4, 2 * q + 1) * kVGroups]};
     }
   }
 }
 
-// acc[j] += Vhat^T tile j x P, Vhat = f16(code * scale) exactly.
+// acc[j] += Vhat^T tile j x P, Vhat = f16(code * scale) exactly: codes become
+// fp16 pairs (tokens e, e+1) by SDWA converts, then one packed multiply by the
+// pair's scales.
+template <int J>
+__device__ __forceinline__ void pv_tile(const VRegs& v, int ks, const half2v* sp, const half8v& pb,
+                                        float4v& acc) {
+  uint32_t e[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint2 wa = v.w[8 * ks + 2 * q];
+    const uint2 wb = v.w[8 * ks + 2 * q + 1];
+    const uint32_t c = (J < 4) ? i8pair_f16<J & 3>(wa.x, wb.x) : i8pair_f16<J & 3>(wa.y, wb.y);
+    e[q] = pack_h2(__builtin_bit_cast(half2v, c) * sp[q]);
+  }
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(e[0], e[1], e[2], e[3]), pb, acc, 0, 0, 0);
+}
+
 __device__ __forceinline__ void pv_regs(const VRegs& v, const half8v* pb, float4v* acc) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    half2v vals[8][4];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const f16 sv = __builtin_bit_cast(f16, v.s[8 * ks + e]);
-      const half2v s2 = {sv, sv};
-      half2v c0, c1, c2, c3;
-      i8x4_to_f16(v.w[8 * ks + e].x, c0, c1);
-      i8x4_to_f16(v.w[8 * ks + e].y, c2, c3);
-      vals[e][0] = c0 * s2;
-      vals[e][1] = c1 * s2;
-      vals[e][2] = c2 * s2;
-      vals[e][3] = c3 * s2;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      half8v A;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) A[e] = (j & 1) ? vals[e][j >> 1].y : vals[e][j >> 1].x;
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, pb[ks], acc[j], 0, 0, 0);
-    }
+    const half2v* sp = &v.s[4 * ks];
+    pv_tile<0>(v, ks, sp, pb[ks], acc[0]);
+    pv_tile<1>(v, ks, sp, pb[ks], acc[1]);
+    pv_tile<2>(v, ks, sp, pb[ks], acc[2]);
+    pv_tile<3>(v, ks, sp, pb[ks], acc[3]);
+    pv_tile<4>(v, ks, sp, pb[ks], acc[4]);
+    pv_tile<5>(v, ks, sp, pb[ks], acc[5]);
+    pv_tile<6>(v, ks, sp, pb[ks], acc[6]);
+    pv_tile<7>(v, ks, sp, pb[ks], acc[7]);
   }
 }
 
@@ -369,63 +409,155 @@ __device__ __forceinline__ void pv_tail(const AttnArgs& a, int64_t bkv, const ha
 
 // Folds one page of scores into the running (m, l, acc) of the lane's head and
 // returns P (fp16) as the PV B operands.  Scores of tokens >= valid are masked.
+// The running max is raised lazily: only when some head's page max exceeds it
+// by more than kLazyRescale (log2 units), so P stays <= 2^kLazyRescale (exact
+// enough in fp16) and the 32-register accumulator rescale is rare.
+constexpr float kLazyRescale = 8.0f;
+
 __device__ __forceinline__ void softmax_page(const float4v* s, int valid, float scale_log2, int l4,
                                              float& m_run, float& l_run, float4v* acc, half8v* pb) {
-  float p[16];
-  float pm = -INFINITY;
+  float x[16];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * mt + 4 * l4 + i;
-      const float v = t < valid ? s[mt][i] * scale_log2 : -INFINITY;
-      p[4 * mt + i] = v;
-      pm = fmaxf(pm, v);
+    for (int i = 0; i < 4; ++i) x[4 * mt + i] = s[mt][i] * scale_log2;
+  }
+  if (valid < kPageTokens) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (16 * mt + 4 * l4 + i >= valid) x[4 * mt + i] = -INFINITY;
+      }
     }
   }
+  float pm = x[0];
+#pragma unroll
+  for (int k = 1; k < 16; ++k) pm = fmaxf(pm, x[k]);
   pm = fmaxf(pm, __shfl_xor(pm, 16, 64));
   pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
-  const float m_new = fmaxf(m_run, pm);
-  const float alpha = exp2f(m_run - m_new);
+  if (__builtin_amdgcn_ballot_w64(pm > m_run + kLazyRescale)) {
+    const float m_new = fmaxf(m_run, pm);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    l_run *= alpha;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+    m_run = m_new;
+  }
   float lsum = 0.0f;
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
-    p[k] = exp2f(p[k] - m_new);
-    lsum += p[k];
+    x[k] = __builtin_amdgcn_exp2f(x[k] - m_run);
+    lsum += x[k];
   }
-  l_run = l_run * alpha + lsum;
-  m_run = m_new;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+  l_run += lsum;
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) pb[ks][e] = (f16)p[4 * (2 * ks + (e >> 2)) + (e & 3)];
+    for (int e = 0; e < 8; ++e) pb[ks][e] = (f16)x[4 * (2 * ks + (e >> 2)) + (e & 3)];
   }
 }
 
 // ---- cross-workgroup exchange ----------------------------------------------------
 //
-// Partials are written with agent-scope relaxed atomic stores (coherent across
-// the XCDs' L2s without an L2 write-back) and each wave waits for them to be
-// acknowledged before the workgroup barrier; the ticket is an agent-scope
-// atomic; the combining workgroup reads partials with agent-scope loads.
+// Partials are written with sc1 (agent-coherent, write-through) vector stores,
+// so no L2 write-back is needed; each wave waits for its stores to be
+// acknowledged before the workgroup barrier that precedes the ticket atomic.
+// The workgroup that draws the last ticket reads every partial with ordinary
+// loads: the sc1 stores have reached memory before the ticket was taken, and no
+// cache can hold an older copy of a partial line, because nothing reads the
+// partials before the last ticket within a launch and the caches are
+// invalidated at every kernel launch.
 
-__device__ __forceinline__ void st_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void st_agent4(float* p, float4v v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
-__device__ __forceinline__ float ld_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void st_agent2(float* p, float x, float y) {
+  typedef float float2v __attribute__((ext_vector_type(2)));
+  const float2v v = {x, y};
+  asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 constexpr int kRedStride = 132;  // padded LDS row of one head's 128 accumulators
 
+// Softmax-merge state of 8 output dims of one head: running max M (log2
+// units), sum L, and the unnormalised accumulators A.
+struct Fold {
+  float M, L;
+  float A[8];
+};
+
+template <bool kAgent>
+__device__ __forceinline__ float ld_rec(const float* p) {
+  if constexpr (kAgent) return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+
+// Folds up to 8 partial records into `st`.  Record u has (m, l) at
+// ml[u * ml_stride + {0, 1}] and 8 accumulators at acc[u * acc_stride + 0..7].
+// All loads are issued before the first use.  kAgent reads global records
+// written by other workgroups with agent-scope (sc1) loads, which see their
+// sc1 stores without an L2 invalidate.
+template <bool kAgent>
+__device__ __forceinline__ Fold fold_records(Fold st, const float* ml, int ml_stride, const float* acc,
+                                             int acc_stride, int count) {
+  float m[8], l[8], x[8][8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    m[u] = -INFINITY;
+    l[u] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) x[u][d] = 0.0f;
+    if (u < count) {
+      m[u] = ld_rec<kAgent>(ml + u * ml_stride);
+      l[u] = ld_rec<kAgent>(ml + u * ml_stride + 1);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) x[u][d] = ld_rec<kAgent>(acc + u * acc_stride + d);
+    }
+  }
+  float M = st.M;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) M = fmaxf(M, m[u]);
+  Fold out;
+  out.M = M;
+  if (M == -INFINITY) return st;
+  const float w0 = __builtin_amdgcn_exp2f(st.M - M);  // 0 for an empty state
+  out.L = st.L * w0;
+#pragma unroll
+  for (int d = 0; d < 8; ++d) out.A[d] = st.A[d] * w0;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const float w = m[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[u] - M);
+    out.L += l[u] * w;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) out.A[d] += x[u][d] * w;
+  }
+  return out;
+}
+
+__device__ __forceinline__ Fold empty_fold() {
+  Fold f;
+  f.M = -INFINITY;
+  f.L = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 8; ++d) f.A[d] = 0.0f;
+  return f;
+}
+
+// Normalised fp16 output of 8 dims.
+__device__ __forceinline__ void store_out8(uint16_t* orow, const Fold& f) {
+  const float inv = __builtin_amdgcn_rcpf(f.L);
+  uint32_t w[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) w[d] = (uint32_t)f2h(f.A[2 * d] * inv) | ((uint32_t)f2h(f.A[2 * d + 1] * inv) << 16);
+  *reinterpret_cast<uint4*>(orow) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 template <int WAVES>
 struct AttnShared {
   Lut lut;
-  float m[WAVES][16];
-  float l[WAVES][16];
+  float ml[WAVES][16][2];
   float acc[WAVES][16 * kRedStride];
   int last;
 };
@@ -441,18 +573,37 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   const int wave = tid >> 6;
   const int l16 = lane & 15;
   const int l4 = lane >> 4;
-  const int split = blockIdx.x;
-  const int64_t bkv = blockIdx.y;
-  const int hb = blockIdx.z;
+  // 1-D grid, unit-minor: consecutive workgroup ids go to different kv heads,
+  // so with round-robin dispatch over the 8 XCDs every split of one kv head
+  // runs on the same XCD and its partials stay within one L2.
+  const int units_total = (int)(gridDim.x / a.n_splits);
+  const int lin = blockIdx.x;
+  const int unit_id = lin % units_total;
+  const int split = lin / units_total;
+  const int64_t bkv = unit_id / a.head_blocks;
+  const int hb = unit_id % a.head_blocks;
   const int b = (int)(bkv / a.hkv);
   const int kv = (int)(bkv - (int64_t)b * a.hkv);
   const int h0 = hb * 16;
   const int nh = min(16, a.g - h0);
 
-  if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
+  // Compressed pages of this split that hold at least one unmasked token.
+  const int p_begin = split * a.pages_per_split;
+  const int64_t live_pages = (a.seq_len + kPageTokens - 1) / kPageTokens;
+  const int p_end = (int)min((int64_t)min(p_begin + a.pages_per_split, a.n_pages), live_pages);
+
+  // The first page's loads go out before the table build and the barrier.
+  int page = p_begin + wave;
+  KRegs<KIND> kr;
+  VRegs vr;
+  if (page < p_end) {
+    load_k<KIND>(a, bkv * a.capacity + page, l16, l4, kr);
+    load_v(a, bkv * a.capacity + page, l16, l4, vr);
+  }
   half8v qb[4];
   load_q(a, b, kv, h0, nh, l16, l4, qb);
-  __syncthreads();
+  if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
+  lds_barrier();
 
   float m_run = -INFINITY;
   float l_run = 0.0f;
@@ -460,18 +611,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Compressed pages of this split that hold at least one unmasked token.
-  const int p_begin = split * a.pages_per_split;
-  const int64_t live_pages = (a.seq_len + kPageTokens - 1) / kPageTokens;
-  const int p_end = (int)min((int64_t)min(p_begin + a.pages_per_split, a.n_pages), live_pages);
-
-  int page = p_begin + wave;
-  KRegs<KIND> kr;
-  if (page < p_end) load_k<KIND>(a, bkv * a.capacity + page, l16, l4, kr);
+  // Per page: QK on the resident K codes, then the next page's K loads go out,
+  // softmax and PV on the resident V codes, then the next page's V loads.
   while (page < p_end) {
-    const int64_t slot = bkv * a.capacity + page;
-    VRegs vr;
-    load_v(a, slot, l16, l4, vr);
     float4v s[4];
     qk_regs<KIND>(a, sh.lut, kr, qb, l16, l4, s);
     const int next = page + WAVES;
@@ -480,6 +622,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     half8v pb[2];
     softmax_page(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
     pv_regs(vr, pb, acc);
+    if (next < p_end) load_v(a, bkv * a.capacity + next, l16, l4, vr);
     page = next;
   }
 
@@ -503,55 +646,36 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   float l_tot = l_run + __shfl_xor(l_run, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
   if (l4 == 0) {
-    sh.m[wave][l16] = m_run;
-    sh.l[wave][l16] = l_tot;
+    sh.ml[wave][l16][0] = m_run;
+    sh.ml[wave][l16][1] = l_tot;
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) sh.acc[wave][l16 * kRedStride + 32 * l4 + 8 * i + j] = acc[j][i];
   }
-  __syncthreads();
+  lds_barrier();
 
   // Thread (h = item / 16, c = item % 16) owns dims [8c, 8c+8) of head h.
   const int item = tid & 255;
   const int h = item >> 4;
   const int c = item & 15;
-  float M = -INFINITY, L = 0.0f;
-  float ACC[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (tid < 256) {
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sh.m[w][h]);
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) {
-      const float mw = sh.m[w][h];
-      const float sc = mw == -INFINITY ? 0.0f : exp2f(mw - M);
-      L += sh.l[w][h] * sc;
-#pragma unroll
-      for (int d = 0; d < 8; ++d) ACC[d] += sh.acc[w][h * kRedStride + 8 * c + d] * sc;
-    }
-  }
+  Fold f = empty_fold();
+  if (tid < 256)
+    f = fold_records<false>(f, &sh.ml[0][h][0], 32, &sh.acc[0][h * kRedStride + 8 * c], 16 * kRedStride, WAVES);
   uint16_t* orow = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + h) * kHeadDim + 8 * c;
   if (a.n_splits == 1) {
-    if (tid < 256 && h < nh) {
-      uint32_t w[4];
-#pragma unroll
-      for (int d = 0; d < 4; ++d) w[d] = (uint32_t)f2h(ACC[2 * d] / L) | ((uint32_t)f2h(ACC[2 * d + 1] / L) << 16);
-      *reinterpret_cast<uint4*>(orow) = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+    if (tid < 256 && h < nh) store_out8(orow, f);
     return;
   }
 
   const int64_t unit = bkv * a.head_blocks + hb;
   if (tid < 256 && h < nh) {
     const int64_t pbase = (unit * a.n_splits + split) * 16 + h;
-    if (c == 0) {
-      st_agent(a.part_ml + pbase * 2 + 0, M);
-      st_agent(a.part_ml + pbase * 2 + 1, L);
-    }
+    if (c == 0) st_agent2(a.part_ml + pbase * 2, f.M, f.L);
     float* pa = a.part_acc + pbase * kHeadDim + 8 * c;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) st_agent(pa + d, ACC[d]);
+    st_agent4(pa, float4v{f.A[0], f.A[1], f.A[2], f.A[3]});
+    st_agent4(pa + 4, float4v{f.A[4], f.A[5], f.A[6], f.A[7]});
   }
   wait_stores();
   __syncthreads();
@@ -563,63 +687,38 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   if (!sh.last) return;
 
   // Last workgroup of this (b, kv, head block): combine all splits.  Thread
-  // (item, sg) folds splits sg, sg + SG, ... of item (h, c); the SG partial
-  // results are then merged through LDS.
+  // (item, sg) folds splits sg, sg + SG, ... of item (h, c), eight per call,
+  // and the SG results merge through LDS with the same routine.
   const int n_items = nh * 16;
   const int SG = max(1, (WAVES * 64) / n_items);
   const int it = tid % n_items;
   const int sg = tid / n_items;
   const int hh = it >> 4;
   const int cc = it & 15;
-  float Mp = -INFINITY, Lp = 0.0f;
-  float Ap[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  Fold g = empty_fold();
   if (sg < SG) {
-    const float* pm = a.part_ml + (unit * a.n_splits * 16 + hh) * 2;
-    const float* pacc = a.part_acc + (unit * a.n_splits * 16 + hh) * kHeadDim + 8 * cc;
-#pragma unroll 4
-    for (int sp = sg; sp < a.n_splits; sp += SG) {
-      const float ms = ld_agent(pm + (int64_t)sp * 32);
-      const float ls = ld_agent(pm + (int64_t)sp * 32 + 1);
-      float x[8];
-#pragma unroll
-      for (int d = 0; d < 8; ++d) x[d] = ld_agent(pacc + (int64_t)sp * 16 * kHeadDim + d);
-      if (ms == -INFINITY) continue;
-      const float mn = fmaxf(Mp, ms);
-      const float so = exp2f(Mp - mn);  // 0 while Mp is -inf
-      const float sn = exp2f(ms - mn);
-      Lp = Lp * so + ls * sn;
-#pragma unroll
-      for (int d = 0; d < 8; ++d) Ap[d] = Ap[d] * so + x[d] * sn;
-      Mp = mn;
-    }
+    const float* pml = a.part_ml + ((unit * a.n_splits + sg) * 16 + hh) * 2;
+    const float* pac = a.part_acc + ((unit * a.n_splits + sg) * 16 + hh) * kHeadDim + 8 * cc;
+    const int mine = (a.n_splits - sg + SG - 1) / SG;
+    for (int r0 = 0; r0 < mine; r0 += 8)
+      g = fold_records<false>(g, pml + (int64_t)r0 * SG * 32, SG * 32, pac + (int64_t)r0 * SG * 16 * kHeadDim,
+                       SG * 16 * kHeadDim, min(8, mine - r0));
   }
-  __syncthreads();  // sh.acc is reused below
-  float* red = &sh.acc[0][0];  // [SG][n_items][10]
+  float* red = &sh.acc[0][0];  // [SG][n_items][10]: (M, L, A[8]) per thread
   if (sg < SG) {
     float* r = red + ((int64_t)sg * n_items + it) * 10;
-    r[0] = Mp;
-    r[1] = Lp;
+    r[0] = g.M;
+    r[1] = g.L;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) r[2 + d] = Ap[d];
+    for (int d = 0; d < 8; ++d) r[2 + d] = g.A[d];
   }
-  __syncthreads();
+  lds_barrier();
   if (sg == 0) {
-    float Mg = -INFINITY;
-    for (int g2 = 0; g2 < SG; ++g2) Mg = fmaxf(Mg, red[((int64_t)g2 * n_items + it) * 10]);
-    float Lg = 0.0f;
-    float Ag[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int g2 = 0; g2 < SG; ++g2) {
-      const float* r = red + ((int64_t)g2 * n_items + it) * 10;
-      const float sc = r[0] == -INFINITY ? 0.0f : exp2f(r[0] - Mg);
-      Lg += r[1] * sc;
-#pragma unroll
-      for (int d = 0; d < 8; ++d) Ag[d] += r[2 + d] * sc;
-    }
-    uint16_t* orow2 = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + hh) * kHeadDim + 8 * cc;
-    uint32_t w[4];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) w[d] = (uint32_t)f2h(Ag[2 * d] / Lg) | ((uint32_t)f2h(Ag[2 * d + 1] / Lg) << 16);
-    *reinterpret_cast<uint4*>(orow2) = make_uint4(w[0], w[1], w[2], w[3]);
+    Fold t = empty_fold();
+    for (int g0 = 0; g0 < SG; g0 += 8)
+      t = fold_records<false>(t, red + ((int64_t)g0 * n_items + it) * 10, n_items * 10,
+                       red + ((int64_t)g0 * n_items + it) * 10 + 2, n_items * 10, min(8, SG - g0));
+    store_out8(a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + hh) * kHeadDim + 8 * cc, t);
   }
   if (tid == 0) __hip_atomic_store(a.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -855,7 +954,7 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
     ws += align256(units * n_splits * 16 * 2 * sizeof(float));
     a.part_acc = reinterpret_cast<float*>(ws);
   }
-  const dim3 grid((unsigned)n_splits, (unsigned)(batch * hkv), (unsigned)a.head_blocks);
+  const dim3 grid((unsigned)(n_splits * batch * hkv * a.head_blocks));
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (n_pages > 0 ? layout_kind(layout) : (int)kKindGeneric) {
     case kKindDefault:

@@ -147,9 +147,12 @@ __host__ __device__ inline int packed_row_bytes(int n, int bits) {
   return (n + 3) / 4;
 }
 
-template <typename T>
-__device__ __forceinline__ T ldg(const T* p) {
-  return __builtin_nontemporal_load(p);
+// Workgroup barrier that orders LDS only: global loads already in flight stay
+// in flight (a full __syncthreads() would wait for them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 }  // namespace tp
