@@ -1,0 +1,121 @@
+"""The C-ABI library loads, exports every symbol include/turbopolar.h declares,
+and validates its arguments on the host (no GPU needed for these paths)."""
+
+import ctypes
+import re
+
+import pytest
+
+from turbopolar_amd import _lib
+from turbopolar_amd.payload import packed_row_bytes
+
+
+def test_library_exports_every_header_symbol():
+    syms = _lib.header_symbols()
+    assert len(syms) >= 12
+    handle = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [s for s in syms if not hasattr(handle, s)]
+    assert not missing, missing
+    # and the binding declares a signature for each of them
+    assert sorted(_lib._SIGNATURES) == syms
+
+
+def test_header_declares_c_linkage_only():
+    text = _lib.HEADER_PATH.read_text()
+    assert 'extern "C"' in text
+    assert "torch" not in text.lower() and "hipStream_t" not in text
+
+
+def test_version_and_last_error():
+    L = _lib.lib()
+    assert L.tp_version() == 100
+    assert isinstance(L.tp_last_error(), bytes)
+
+
+@pytest.mark.parametrize("l1,deep,split", [(4, 4, 64), (4, 8, 0), (8, 2, 32), (4, 2, 46), (8, 4, 128), (4, 4, 2)])
+def test_row_bytes_match_packing_rule(l1, deep, split):
+    layout = _lib.make_layout(False, l1, deep, split)
+    assert _lib.row_bytes(layout) == (packed_row_bytes(split // 2, l1), packed_row_bytes(64 - split // 2, deep))
+
+
+@pytest.mark.parametrize("l1,deep,split,msg", [
+    (3, 4, 64, "k_angle_bits_level1"),
+    (4, 3, 64, "k_angle_bits_deep"),
+    (4, 4, 63, "split_dim"),
+    (4, 4, 130, "split_dim"),
+])
+def test_layout_rejections(l1, deep, split, msg):
+    with pytest.raises(ValueError, match=msg):
+        _lib.row_bytes(_lib.make_layout(False, l1, deep, split))
+
+
+def _fake_pages(capacity=8):
+    # Aligned, never dereferenced: validation fails before any device access.
+    return _lib.TPPages(4096, 8192, 12288, 16384, 20480, 24576, capacity)
+
+
+def test_encode_argument_validation():
+    L = _lib.lib()
+    lay = _lib.make_layout(False, 4, 4, 64)
+    pages = _fake_pages()
+    st = L.tp_encode_pages(4096, 8192, 2, 1, 64, 0, 64, ctypes.byref(lay), ctypes.byref(pages), 0, None)
+    assert st == _lib.TP_ERR_INVALID and b"in_dtype" in L.tp_last_error()
+    st = L.tp_encode_pages(4096, 8192, 0, 1, 64, 10, 64, ctypes.byref(lay), ctypes.byref(pages), 0, None)
+    assert st == _lib.TP_ERR_INVALID and b"token range" in L.tp_last_error()
+    st = L.tp_encode_pages(4096, 8192, 0, 1, 64 * 20, 0, 64 * 9, ctypes.byref(lay), ctypes.byref(pages), 0, None)
+    assert st == _lib.TP_ERR_INVALID and b"capacity" in L.tp_last_error()
+    st = L.tp_encode_pages(4100, 8192, 0, 1, 64, 0, 64, ctypes.byref(lay), ctypes.byref(pages), 0, None)
+    assert st == _lib.TP_ERR_INVALID and b"aligned" in L.tp_last_error()
+    assert L.tp_encode_pages(4096, 8192, 0, 1, 64, 0, 0, ctypes.byref(lay), ctypes.byref(pages), 0, None) == 0
+
+
+def test_decode_attention_argument_validation():
+    L = _lib.lib()
+    lay = _lib.make_layout(False, 4, 4, 64)
+    pages = _fake_pages()
+
+    def call(**kw):
+        a = dict(q=4096, batch=1, hq=8, hkv=2, n_pages=4, tk=None, tv=None, tail=0, tstride=0, seq=256,
+                 pps=0, ws=None, wsb=0, out=8192)
+        a.update(kw)
+        st = L.tp_decode_attention(a["q"], a["batch"], a["hq"], a["hkv"], ctypes.byref(lay), ctypes.byref(pages),
+                                   a["n_pages"], a["tk"], a["tv"], a["tail"], a["tstride"], a["seq"], 0.088, a["pps"],
+                                   a["ws"], a["wsb"], a["out"], None)
+        return st, L.tp_last_error().decode()
+
+    assert call(hq=7)[0] == _lib.TP_ERR_INVALID
+    assert call(n_pages=9)[0] == _lib.TP_ERR_INVALID
+    st, msg = call(tail=64, tk=4096, tv=4096, tstride=64)
+    assert st == _lib.TP_ERR_INVALID and "tail_len" in msg
+    st, msg = call(seq=257)
+    assert st == _lib.TP_ERR_INVALID and "actual_seq_len" in msg
+    st, msg = call(seq=0)
+    assert st == _lib.TP_ERR_INVALID
+    st, msg = call(n_pages=0)
+    assert st == _lib.TP_ERR_INVALID and "nothing to attend" in msg
+    st, msg = call(pps=1)  # 4 splits need a workspace
+    assert st == _lib.TP_ERR_WORKSPACE and "workspace" in msg
+
+
+def test_workspace_sizes():
+    L = _lib.lib()
+    # Llama-3-8B shape at 32k: one workgroup per CU -> 16 pages per split
+    assert L.tp_default_pages_per_split(1, 32, 8, 512) == 16
+    n = L.tp_decode_workspace_bytes(1, 32, 8, 512, 0, 16)
+    counters = L.tp_decode_counter_bytes(1, 32, 8)
+    assert counters == 256
+    splits = 32
+    assert n == counters + 8 * splits * 16 * 2 * 4 + 8 * splits * 16 * 128 * 4
+    # GQA group > 16 uses two head blocks
+    assert L.tp_decode_counter_bytes(2, 40, 2) == 256
+    assert L.tp_decode_workspace_bytes(1, 40, 2, 2, 0, 1) > L.tp_decode_workspace_bytes(1, 16, 1, 2, 0, 1)
+
+
+def test_product_has_no_oracle_dependency():
+    """The product package never imports the oracle (the oracle checks it)."""
+    import pathlib
+
+    pkg = pathlib.Path(_lib.__file__).parent
+    for f in pkg.glob("*.py"):
+        src = f.read_text()
+        assert not re.search(r"^\s*(import|from)\s+oracle\b", src, re.M), f
