@@ -53,6 +53,26 @@ def gen_q(seed: int, B: int, Hq: int, scale: float = 1.0):
     return (rng.standard_normal((B, Hq, D), dtype=np.float32) * scale).astype(np.float16)
 
 
+def edge_page(dtype):
+    """Axis-aligned pairs, signed zeros, radii at the fp16 x*x overflow edge,
+    exact V quotient ties and an all-zero V group."""
+    k = np.zeros((1, 1, PAGE, 128), dtype=np.float32)
+    v = np.zeros((1, 1, PAGE, 128), dtype=np.float32)
+    specials = [(0, 0), (1, 0), (-1, 0.0), (-1, -0.0), (0, 1), (0, -1), (1, 1), (-1, 1), (3, 4),
+                (255.9, 0), (256, 0), (255, 10), (-300, 2), (1e-7, 1e-7), (65504, 65504), (-0.0, -0.0)]
+    rng = np.random.default_rng(5)
+    for t in range(PAGE):
+        for j in range(64):
+            x, y = specials[(t * 64 + j) % len(specials)] if t < 8 else rng.standard_normal(2) * 4
+            k[0, 0, t, 2 * j], k[0, 0, t, 2 * j + 1] = x, y
+    # V: group 0 all zero; group 1 with many exact half-ties of v / s; group 2 huge range
+    v[0, 0, :, 32:64] = np.arange(32, dtype=np.float32)[None, :] * 0.5 - 8
+    v[0, 0, :, 32] = 127.0
+    v[0, 0, :, 64:96] = rng.standard_normal((PAGE, 32)) * 1000
+    v[0, 0, :, 96:] = rng.standard_normal((PAGE, 32)) * 1e-6
+    return k.astype(dtype), v.astype(dtype)
+
+
 def oracle_pages(k: np.ndarray, v: np.ndarray, layout):
     """Oracle-encode ``[B,H,S*64,D]`` inputs page by page and stack to 5-D."""
     int8, l1b, deepb, split = layout
@@ -94,3 +114,19 @@ def cosine(a, b) -> float:
 # (fp16 output, fp32 accumulation): max-abs 2e-3 and relative L2 1e-3.
 ATOL = 2e-3
 RTOL_L2 = 1e-3
+
+
+GOLDEN_DIR = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+
+
+def load_golden(name: str) -> dict:
+    """A committed fixture file from tests/golden as a dict of arrays."""
+    with np.load(GOLDEN_DIR / name, allow_pickle=False) as f:
+        return {k: f[k] for k in f.files}
+
+
+def within_f16_ulp(got, ref) -> bool:
+    """|got - ref| <= one fp16 ulp of ref, elementwise (fp16 decode outputs)."""
+    ref64 = np.asarray(ref, np.float64)
+    ulp = np.spacing(np.abs(np.asarray(ref, np.float16))).astype(np.float64)
+    return bool(np.all(np.abs(np.asarray(got, np.float64) - ref64) <= ulp + 1e-12))

@@ -95,6 +95,14 @@ def test_decode_attention_argument_validation():
     assert st == _lib.TP_ERR_INVALID and "nothing to attend" in msg
     st, msg = call(pps=1)  # 4 splits need a workspace
     assert st == _lib.TP_ERR_WORKSPACE and "workspace" in msg
+    # The combine's LDS table bounds splits x (query heads per kv head, at most 16) by 6144.
+    big = _fake_pages(capacity=4096)
+    st = L.tp_decode_attention(4096, 1, 8, 2, ctypes.byref(lay), ctypes.byref(big), 1537, None, None, 0, 0,
+                               1537 * 64, 0.088, 1, None, 0, 8192, None)
+    assert st == _lib.TP_ERR_INVALID and b"too many splits" in L.tp_last_error()
+    st = L.tp_decode_attention(4096, 1, 8, 2, ctypes.byref(lay), ctypes.byref(big), 1536, None, None, 0, 0,
+                               1536 * 64, 0.088, 1, None, 0, 8192, None)
+    assert st == _lib.TP_ERR_WORKSPACE  # 1536 x 4 fits; only the missing workspace is reported
 
 
 def test_workspace_sizes():

@@ -157,6 +157,16 @@ def test_split_invariance(device):
     check(outs[0], oracle_out(host, tk, tv, q, seq), "split")
 
 
+def test_max_splits_combine(device):
+    """The split cap (splits x query heads per kv head = 6144): 1536 one-page
+    splits of 4 heads fill the combine's LDS table and run its chunked reloads."""
+    print("[attn-maxsplits] S=1536 pps=1", flush=True)
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], 8, 2, 1536, 9, seed=21)
+    seq = 1536 * PAGE + 9
+    out = run_gpu(device, block, qv, tk, tv, q, seq, pps=1)
+    check(out, oracle_out(host, tk, tv, q, seq), "max splits")
+
+
 def test_page_decode_parity(device):
     """tp_decode_pages: V exactly the dequantised codes; K within one fp16 ulp."""
     for name in ("default", "fast", "deep2", "odd_split"):

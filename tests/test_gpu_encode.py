@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import oracle
-from common import LAYOUTS, PAGE, gen_kv, oracle_pages
+from common import LAYOUTS, PAGE, edge_page, gen_kv, oracle_pages
 from turbopolar_amd import _lib, kernels
 from turbopolar_amd.codecs import PolarQuantEncoder
 from turbopolar_amd.config import TurboPolarConfig
@@ -94,31 +94,11 @@ def test_encode_baseline_distributions(device, kind, layout_name):
     check_against_oracle(k, v, LAYOUTS[layout_name], device)
 
 
-def _edge_page(dtype):
-    """Axis-aligned pairs, signed zeros, radii at the fp16 x*x overflow edge,
-    exact V quotient ties and an all-zero V group."""
-    k = np.zeros((1, 1, PAGE, 128), dtype=np.float32)
-    v = np.zeros((1, 1, PAGE, 128), dtype=np.float32)
-    specials = [(0, 0), (1, 0), (-1, 0.0), (-1, -0.0), (0, 1), (0, -1), (1, 1), (-1, 1), (3, 4),
-                (255.9, 0), (256, 0), (255, 10), (-300, 2), (1e-7, 1e-7), (65504, 65504), (-0.0, -0.0)]
-    rng = np.random.default_rng(5)
-    for t in range(PAGE):
-        for j in range(64):
-            x, y = specials[(t * 64 + j) % len(specials)] if t < 8 else rng.standard_normal(2) * 4
-            k[0, 0, t, 2 * j], k[0, 0, t, 2 * j + 1] = x, y
-    # V: group 0 all zero; group 1 with many exact half-ties of v / s; group 2 huge range
-    v[0, 0, :, 32:64] = np.arange(32, dtype=np.float32)[None, :] * 0.5 - 8
-    v[0, 0, :, 32] = 127.0
-    v[0, 0, :, 64:96] = rng.standard_normal((PAGE, 32)) * 1000
-    v[0, 0, :, 96:] = rng.standard_normal((PAGE, 32)) * 1e-6
-    return k.astype(dtype), v.astype(dtype)
-
-
 @pytest.mark.parametrize("layout_name", ["default", "fast", "deep2", "l1_8bit"])
 @pytest.mark.parametrize("dtype", [np.float16, np.float32])
 def test_encode_edge_page(device, layout_name, dtype):
     print(f"[encode-edge] layout={layout_name} dtype={np.dtype(dtype).name}", flush=True)
-    k, v = _edge_page(dtype)
+    k, v = edge_page(dtype)
     check_against_oracle(k, v, LAYOUTS[layout_name], device)
 
 

@@ -1,12 +1,16 @@
 // tp_attention.hip -- fused dequant.QK and split-K decode attention on gfx950.
 //
 // Work decomposition (decode, batch b, kv head kv, GQA group g <= 16 per head
-// block): a 256-thread workgroup owns `pages_per_split` consecutive pages of one
-// kv head and scores ALL g query heads of that kv head from a single read of the
-// page codes.  Each of its 4 wave64s walks its own pages with a private online
-// softmax; the waves are merged through LDS, then the workgroup's partial
-// (m, l, acc[128]) per head goes to the workspace and the last workgroup of the
-// kv head to arrive (atomic ticket) combines all partials -- one launch per step.
+// block): a 512-thread workgroup (8 wave64s) owns `pages_per_split`
+// consecutive pages of one kv head and scores ALL g query heads of that kv head
+// from a single read of the page codes.  Each wave walks its own pages with a
+// private online softmax; the waves are merged through LDS, then the
+// workgroup's partial (m, l, acc[128]) per head goes to the workspace and the
+// last workgroup of the kv head to arrive (atomic ticket) combines all
+// partials -- one launch per step.  The 1-D grid is unit-minor, so with the
+// hardware's round-robin dispatch over the 8 XCDs every split of one kv head
+// runs on the same XCD (a locality choice only: correctness does not depend
+// on placement).
 //
 // Per page (64 tokens) a wave runs two MFMA chains (v_mfma_f32_16x16x32_f16):
 //   QK: S[t][h] = sum_d Khat[t][d] Q[h][d]; A = Khat decoded in registers from
@@ -182,7 +186,7 @@ template <>
 struct KRegs<kKindFast> {  // int8 log radii + fp16 page scale, 8-bit deep codes, split 0
   uint4 r[4];
   uint4 c[4];
-  float ls;
+  uint32_t ls_bits;  // fp16 page scale, converted at use so its load is not waited on early
 };
 
 template <>
@@ -213,7 +217,7 @@ __device__ __forceinline__ void load_k(const AttnArgs& a, int64_t slot, int l16,
       k.r[mt] = *reinterpret_cast<const uint4*>(rbase + t * kPairs);
       k.c[mt] = *reinterpret_cast<const uint4*>(cbase + t * kPairs);
     }
-    k.ls = h2f(a.radii_scales[slot]);
+    k.ls_bits = a.radii_scales[slot];
   } else {
     k.slot = slot;
   }
@@ -247,6 +251,7 @@ __device__ __forceinline__ void qk_regs(const AttnArgs& a, const Lut& lut, const
       s[mt] = acc;
     }
   } else if constexpr (KIND == kKindFast) {
+    const float ls = h2f((uint16_t)k.ls_bits);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const uint32_t rw[4] = {k.r[mt].x, k.r[mt].y, k.r[mt].z, k.r[mt].w};
@@ -259,7 +264,7 @@ __device__ __forceinline__ void qk_regs(const AttnArgs& a, const Lut& lut, const
         for (int i = 0; i < 4; ++i) {
           const int rc = (int)(int8_t)((rw[kk] >> (8 * i)) & 0xffu);
           const uint32_t code = (cw[kk] >> (8 * i)) & 0xffu;
-          const f16 r = (f16)expf((float)rc * k.ls);
+          const f16 r = (f16)expf((float)rc * ls);
           const half2v cs = __builtin_bit_cast(half2v, lut.deep[code]);
           e[i] = pack_h2(half2v{r, r} * cs);
         }
@@ -330,6 +335,31 @@ struct VRegs {
 };
 
 __device__ __forceinline__ int v_token(int ks, int l4, int e) { return 32 * ks + 4 * l4 + (e & 3) + 16 * (e >> 2); }
+
+// Issues the V code and scale loads of one page; the scales arrive as raw
+// fp16 bits, one token per register, so nothing waits on them here.
+__device__ __forceinline__ void load_v_raw(const AttnArgs& a, int64_t slot, int l16, int l4, VRegs& v,
+                                           uint32_t* sraw) {
+  const int8_t* vbase = a.v_codes + slot * (kPageTokens * kHeadDim) + 8 * l16;
+  const uint16_t* sbase = a.v_scales + slot * (kPageTokens * kVGroups) + (l16 >> 2);
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int t = v_token(ks, l4, e);
+      v.w[8 * ks + e] = *reinterpret_cast<const uint2*>(vbase + t * kHeadDim);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sraw[8 * ks + e] = sbase[v_token(ks, l4, e) * kVGroups];
+  }
+}
+
+// Pairs the raw scales as (token 2q, token 2q+1) per k-step.
+__device__ __forceinline__ void pack_scales(const uint32_t* sraw, VRegs& v) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    v.s[q] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(sraw[2 * q + 1], sraw[2 * q], 0x05040100u));
+}
 
 __device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16, int l4, VRegs& v) {
   const int8_t* vbase = a.v_codes + slot * (kPageTokens * kHeadDim) + 8 * l16;
@@ -479,7 +509,12 @@ __device__ __forceinline__ void st_agent2(float* p, float x, float y) {
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+
 constexpr int kRedStride = 132;  // padded LDS row of one head's 128 accumulators
+// Bound on splits x heads per head block: the combine's (weight, l) table
+// (48 KiB) and its 8 KiB reduction area share the 67.5 KiB accumulator region.
+constexpr int kMaxSplitHeads = 6144;
+
 
 // Softmax-merge state of 8 output dims of one head: running max M (log2
 // units), sum L, and the unnormalised accumulators A.
@@ -488,18 +523,9 @@ struct Fold {
   float A[8];
 };
 
-template <bool kAgent>
-__device__ __forceinline__ float ld_rec(const float* p) {
-  if constexpr (kAgent) return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return *p;
-}
-
-// Folds up to 8 partial records into `st`.  Record u has (m, l) at
-// ml[u * ml_stride + {0, 1}] and 8 accumulators at acc[u * acc_stride + 0..7].
-// All loads are issued before the first use.  kAgent reads global records
-// written by other workgroups with agent-scope (sc1) loads, which see their
-// sc1 stores without an L2 invalidate.
-template <bool kAgent>
+// Folds up to 8 partial records (of the waves of one workgroup, in LDS) into
+// `st`.  Record u has (m, l) at ml[u * ml_stride + {0, 1}] and 8 accumulators
+// at acc[u * acc_stride + 0..7].  All loads are issued before the first use.
 __device__ __forceinline__ Fold fold_records(Fold st, const float* ml, int ml_stride, const float* acc,
                                              int acc_stride, int count) {
   float m[8], l[8], x[8][8];
@@ -510,10 +536,10 @@ __device__ __forceinline__ Fold fold_records(Fold st, const float* ml, int ml_st
 #pragma unroll
     for (int d = 0; d < 8; ++d) x[u][d] = 0.0f;
     if (u < count) {
-      m[u] = ld_rec<kAgent>(ml + u * ml_stride);
-      l[u] = ld_rec<kAgent>(ml + u * ml_stride + 1);
+      m[u] = ml[u * ml_stride];
+      l[u] = ml[u * ml_stride + 1];
 #pragma unroll
-      for (int d = 0; d < 8; ++d) x[u][d] = ld_rec<kAgent>(acc + u * acc_stride + d);
+      for (int d = 0; d < 8; ++d) x[u][d] = acc[u * acc_stride + d];
     }
   }
   float M = st.M;
@@ -592,18 +618,24 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   const int64_t live_pages = (a.seq_len + kPageTokens - 1) / kPageTokens;
   const int p_end = (int)min((int64_t)min(p_begin + a.pages_per_split, a.n_pages), live_pages);
 
-  // The first page's loads go out before the table build and the barrier.
+  // Q and the first page's loads go out before the table build and the
+  // barrier; the first page's V scales are paired only after the barrier, so
+  // no wave waits for memory before it.
+  half8v qb[4];
+  load_q(a, b, kv, h0, nh, l16, l4, qb);
   int page = p_begin + wave;
   KRegs<KIND> kr;
   VRegs vr;
+  uint32_t sraw[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) sraw[e] = 0u;
   if (page < p_end) {
     load_k<KIND>(a, bkv * a.capacity + page, l16, l4, kr);
-    load_v(a, bkv * a.capacity + page, l16, l4, vr);
+    load_v_raw(a, bkv * a.capacity + page, l16, l4, vr, sraw);
   }
-  half8v qb[4];
-  load_q(a, b, kv, h0, nh, l16, l4, qb);
   if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
   lds_barrier();
+  pack_scales(sraw, vr);
 
   float m_run = -INFINITY;
   float l_run = 0.0f;
@@ -662,18 +694,18 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   const int c = item & 15;
   Fold f = empty_fold();
   if (tid < 256)
-    f = fold_records<false>(f, &sh.ml[0][h][0], 32, &sh.acc[0][h * kRedStride + 8 * c], 16 * kRedStride, WAVES);
+    f = fold_records(f, &sh.ml[0][h][0], 32, &sh.acc[0][h * kRedStride + 8 * c], 16 * kRedStride, WAVES);
   uint16_t* orow = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + h) * kHeadDim + 8 * c;
   if (a.n_splits == 1) {
     if (tid < 256 && h < nh) store_out8(orow, f);
     return;
   }
-
   const int64_t unit = bkv * a.head_blocks + hb;
+  const int S = a.n_splits;
+  const int Sp = (S + 1) & ~1;  // (m, l) row length in pairs
   if (tid < 256 && h < nh) {
-    const int64_t pbase = (unit * a.n_splits + split) * 16 + h;
-    if (c == 0) st_agent2(a.part_ml + pbase * 2, f.M, f.L);
-    float* pa = a.part_acc + pbase * kHeadDim + 8 * c;
+    if (c == 0) st_agent2(a.part_ml + ((unit * 16 + h) * Sp + split) * 2, f.M, f.L);
+    float* pa = a.part_acc + ((unit * S + split) * 16 + h) * kHeadDim + 8 * c;
     st_agent4(pa, float4v{f.A[0], f.A[1], f.A[2], f.A[3]});
     st_agent4(pa + 4, float4v{f.A[4], f.A[5], f.A[6], f.A[7]});
   }
@@ -681,44 +713,77 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   __syncthreads();
   if (tid == 0) {
     const uint32_t prev = __hip_atomic_fetch_add(a.counters + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh.last = prev == (uint32_t)(a.n_splits - 1);
+    sh.last = prev == (uint32_t)(S - 1);
   }
   __syncthreads();
   if (!sh.last) return;
 
-  // Last workgroup of this (b, kv, head block): combine all splits.  Thread
-  // (item, sg) folds splits sg, sg + SG, ... of item (h, c), eight per call,
-  // and the SG results merge through LDS with the same routine.
-  const int n_items = nh * 16;
+  // Last workgroup of this (b, kv, head block): combine the n_splits records.
+  // The softmax weight of a (split, head) record is shared by its 128 dims, so
+  // it is computed once: one wave per head turns the head's (m, l) row into
+  // w = 2^(m - M) and 1/L in LDS, while every thread's accumulator loads are
+  // already in flight.  Thread (item = (head hh, 4-dim chunk c4), sg) then
+  // sums w * acc over splits sg, sg + SG, ... and the SG sums meet in LDS.
+  const int n_items = nh * 32;
   const int SG = max(1, (WAVES * 64) / n_items);
   const int it = tid % n_items;
   const int sg = tid / n_items;
-  const int hh = it >> 4;
-  const int cc = it & 15;
-  Fold g = empty_fold();
-  if (sg < SG) {
-    const float* pml = a.part_ml + ((unit * a.n_splits + sg) * 16 + hh) * 2;
-    const float* pac = a.part_acc + ((unit * a.n_splits + sg) * 16 + hh) * kHeadDim + 8 * cc;
-    const int mine = (a.n_splits - sg + SG - 1) / SG;
-    for (int r0 = 0; r0 < mine; r0 += 8)
-      g = fold_records<false>(g, pml + (int64_t)r0 * SG * 32, SG * 32, pac + (int64_t)r0 * SG * 16 * kHeadDim,
-                       SG * 16 * kHeadDim, min(8, mine - r0));
-  }
-  float* red = &sh.acc[0][0];  // [SG][n_items][10]: (M, L, A[8]) per thread
-  if (sg < SG) {
-    float* r = red + ((int64_t)sg * n_items + it) * 10;
-    r[0] = g.M;
-    r[1] = g.L;
+  const int hh = it >> 5;
+  const int c4 = it & 31;
+  const int mine = sg < SG ? (S - sg + SG - 1) / SG : 0;
+  const float* pac = a.part_acc + ((unit * S + sg) * 16 + hh) * kHeadDim + 4 * c4;
+  const int64_t rstride = (int64_t)SG * 16 * kHeadDim;
+  float4v x[8];
 #pragma unroll
-    for (int d = 0; d < 8; ++d) r[2 + d] = g.A[d];
+  for (int u = 0; u < 8; ++u) x[u] = u < mine ? *reinterpret_cast<const float4v*>(pac + u * rstride) : float4v{};
+  float* wml = &sh.acc[0][0];
+  float* inv_l = wml + 2 * nh * S;
+  for (int h2 = wave; h2 < nh; h2 += WAVES) {
+    const float* pml = a.part_ml + (unit * 16 + h2) * Sp * 2;
+    float mx = -INFINITY;
+    for (int sp = lane; sp < S; sp += 64) {
+      const float2 r = *reinterpret_cast<const float2*>(pml + 2 * sp);
+      *reinterpret_cast<float2*>(wml + 2 * (h2 * S + sp)) = r;
+      mx = fmaxf(mx, r.x);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    float lsum = 0.0f;
+    for (int sp = lane; sp < S; sp += 64) {
+      const float2 r = *reinterpret_cast<const float2*>(wml + 2 * (h2 * S + sp));
+      const float w = r.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r.x - mx);
+      wml[2 * (h2 * S + sp)] = w;
+      lsum += w * r.y;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off, 64);
+    if (lane == 0) inv_l[h2] = __builtin_amdgcn_rcpf(lsum);
   }
   lds_barrier();
+  float4v accv = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  const float* wrow = wml + 2 * (hh * S + sg);
+  for (int r0 = 0; r0 < mine; r0 += 8) {
+    if (r0 > 0) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        x[u] = r0 + u < mine ? *reinterpret_cast<const float4v*>(pac + (r0 + u) * rstride) : float4v{};
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (r0 + u < mine) accv += x[u] * wrow[2 * SG * (r0 + u)];
+  }
+  float4v* red = reinterpret_cast<float4v*>(wml + ((2 * nh * S + nh + 3) & ~3));
+  if (SG > 1) {
+    if (sg < SG) red[sg * n_items + it] = accv;
+    lds_barrier();
+    if (sg == 0)
+      for (int g2 = 1; g2 < SG; ++g2) accv += red[g2 * n_items + it];
+  }
   if (sg == 0) {
-    Fold t = empty_fold();
-    for (int g0 = 0; g0 < SG; g0 += 8)
-      t = fold_records<false>(t, red + ((int64_t)g0 * n_items + it) * 10, n_items * 10,
-                       red + ((int64_t)g0 * n_items + it) * 10 + 2, n_items * 10, min(8, SG - g0));
-    store_out8(a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + hh) * kHeadDim + 8 * cc, t);
+    const float inv = inv_l[hh];
+    uint16_t* orow3 = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + hh) * kHeadDim + 4 * c4;
+    *reinterpret_cast<uint2*>(orow3) = make_uint2((uint32_t)f2h(accv[0] * inv) | ((uint32_t)f2h(accv[1] * inv) << 16),
+                                                  (uint32_t)f2h(accv[2] * inv) | ((uint32_t)f2h(accv[3] * inv) << 16));
   }
   if (tid == 0) __hip_atomic_store(a.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -866,7 +931,7 @@ size_t tp_decode_workspace_bytes(int64_t batch, int32_t hq, int32_t hkv, int32_t
   if (pages_per_split <= 0) pages_per_split = tp_default_pages_per_split(batch, hq, hkv, n_pages);
   const size_t units = (size_t)batch * hkv * head_blocks_of(hq, hkv);
   const size_t splits = (size_t)n_splits_of(n_pages, pages_per_split);
-  return tp_decode_counter_bytes(batch, hq, hkv) + align256(units * splits * 16 * 2 * sizeof(float)) +
+  return tp_decode_counter_bytes(batch, hq, hkv) + align256(units * 16 * ((splits + 1) & ~(size_t)1) * 2 * sizeof(float)) +
          align256(units * splits * 16 * kHeadDim * sizeof(float));
 }
 
@@ -926,8 +991,9 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
   }
   if (pages_per_split <= 0) pages_per_split = tp_default_pages_per_split(batch, hq, hkv, n_pages);
   const int32_t n_splits = n_splits_of(n_pages, pages_per_split);
-  if (n_splits > 65535) {
-    set_error("too many splits (%d); raise pages_per_split", n_splits);
+  // The combine keeps a (weight, l) pair per split and head of a head block in LDS.
+  if ((int64_t)n_splits * std::min(16, hq / hkv) > kMaxSplitHeads) {
+    set_error("too many splits (%d) for %d query heads per kv head; raise pages_per_split", n_splits, hq / hkv);
     return TP_ERR_INVALID;
   }
   a.out = static_cast<uint16_t*>(out);
@@ -951,7 +1017,7 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
     a.counters = reinterpret_cast<uint32_t*>(ws);
     ws += tp_decode_counter_bytes(batch, hq, hkv);
     a.part_ml = reinterpret_cast<float*>(ws);
-    ws += align256(units * n_splits * 16 * 2 * sizeof(float));
+    ws += align256(units * 16 * (((size_t)n_splits + 1) & ~(size_t)1) * 2 * sizeof(float));
     a.part_acc = reinterpret_cast<float*>(ws);
   }
   const dim3 grid((unsigned)(n_splits * batch * hkv * a.head_blocks));
