@@ -27,6 +27,25 @@ documented assumptions:
 
 The attention functions compute in float64 by default (``dtype`` argument) on
 the fp16 decoded K and V, which is the "ideal" value of the reference CPU path.
+
+How each function is pinned (tests/test_oracle_pins.py,
+tests/test_oracle_attention.py, tests/test_golden.py):
+
+* pack_4bit / pack_2bit / unpack_* / layout_bytes: closed forms and round trips.
+* encode_block, angle_codes_f16, atan2_cr, log_cr: known answers of the rules in
+  encoder.py:24-98, an independent exact-rational restatement
+  (tests/exact_f16.py) compared bit for bit, fp32-input wrap cases.
+* quantize_block / dequantize_block: known answers (zero group, group max,
+  half-even ties) and the exact-rational restatement.
+* decode_block: radius invariant sqrt(kx^2 + ky^2) ~ r, decode->encode
+  idempotence.
+* softmax_attention, cpu_fused_qk, cpu_online_attention[_dense_tail]: torch
+  float64 scaled_dot_product_attention, brute-force loops on one page, the
+  split-K merge algebra.
+
+Parity unpinned at the MLX boundary (MLX is not installable here): MLX's own
+ulp behaviour for fp16 arctan2 / log, its scalar promotion and rounding mode
+(assumptions 1-4 above), and the reduction order inside mx.sum / mx.softmax.
 """
 
 from __future__ import annotations
