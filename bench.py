@@ -169,6 +169,93 @@ def cpu_baseline(args, layout, caches, budget_s):
     return float(np.median(times)) * 1e6, len(times), err
 
 
+def run_encode(args, layout) -> dict:
+    """Bulk prefill (workload 1): one tp_encode_pages launch
+    encodes ``context`` fp16 tokens of ``hkv`` kv heads into pages.  Input and
+    page sets rotate (> 256 MB in total) so reads and writes go to HBM."""
+    import torch
+
+    from turbopolar_amd import TurboPolarConfig, _lib
+    from turbopolar_amd.codecs import PolarQuantEncoder
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    int8, l1b, deepb, split = layout
+    cfg = TurboPolarConfig(num_q_heads=args.hq, num_kv_heads=args.hkv, use_int8_radii=int8,
+                           k_angle_bits_level1=l1b, k_angle_bits_deep=deepb, split_dim=split)
+    enc = PolarQuantEncoder(cfg)
+    n_pages = args.context // 64
+    g = torch.Generator(device=dev).manual_seed(3)
+    sets = []
+    for _ in range(3):
+        k = torch.randn((1, args.hkv, args.context, 128), generator=g, device=dev).half()
+        v = torch.randn((1, args.hkv, args.context, 128), generator=g, device=dev).half()
+        bufs = enc.alloc_pages(1, args.hkv, n_pages, dev)
+        codes = torch.empty((1, args.hkv, n_pages, 64, 128), dtype=torch.int8, device=dev)
+        scales = torch.empty((1, args.hkv, n_pages, 64, 4), dtype=torch.float16, device=dev)
+        pages = _lib.TPPages(_lib.ptr(bufs["radii"]), _lib.ptr(bufs["radii_scales"]), _lib.ptr(bufs["angle_codes_l1"]),
+                             _lib.ptr(bufs["angle_codes_deep"]), _lib.ptr(codes), _lib.ptr(scales), n_pages)
+        sets.append((k, v, bufs, codes, scales, pages))
+    L = _lib.lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    lay = enc.layout
+
+    def step(i):
+        k, v, _, _, _, pages = sets[i % len(sets)]
+        st = L.tp_encode_pages(k.data_ptr(), v.data_ptr(), 0, args.hkv, args.context, 0, args.context,
+                               ctypes.byref(lay), ctypes.byref(pages), 0, stream)
+        if st:
+            _lib.check(st, "tp_encode_pages")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(args.steps):
+        step(i)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    kv_bytes = 2 * args.hkv * args.context * 128 * 2
+    page_bytes = args.hkv * n_pages * (bench_page_bytes(layout))
+    return {"ms": ms, "read": kv_bytes, "write": page_bytes, "n_pages": n_pages}
+
+
+def bench_page_bytes(layout) -> int:
+    """Compressed bytes of one page of one kv head (K codes + radii + V codes + V scales)."""
+    return algorithmic_bytes(0, 1, 1, layout)
+
+
+def run_append(args, layout, n_appends: int = 4096) -> dict:
+    """Single-token appends (workload 2) through
+    TurboPolarKVCacheRuntime.append: every 64th append encodes a page."""
+    import torch
+
+    from turbopolar_amd import TurboPolarConfig, TurboPolarKVCacheRuntime
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    int8, l1b, deepb, split = layout
+    cfg = TurboPolarConfig(num_q_heads=args.hq, num_kv_heads=args.hkv, use_int8_radii=int8,
+                           k_angle_bits_level1=l1b, k_angle_bits_deep=deepb, split_dim=split)
+    g = torch.Generator(device=dev).manual_seed(3)
+    k = torch.randn((1, args.hkv, n_appends + 64, 128), generator=g, device=dev).half()
+    v = torch.randn((1, args.hkv, n_appends + 64, 128), generator=g, device=dev).half()
+    warm = TurboPolarKVCacheRuntime(cfg)
+    for t in range(128):
+        warm.append(k[:, :, t:t + 1], v[:, :, t:t + 1])
+    torch.cuda.synchronize()
+    rt = TurboPolarKVCacheRuntime(cfg)
+    t0 = time.perf_counter()
+    for t in range(n_appends):
+        rt.append(k[:, :, t:t + 1], v[:, :, t:t + 1])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return {"us_per_append": dt / n_appends * 1e6, "appends": n_appends, "pages": rt.total_blocks}
+
+
 def copy_calibration(nbytes: int, reps: int = 10) -> None:
     """Plain device-to-device copy of a known size: the reference for scaling
     rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes."""
@@ -201,6 +288,8 @@ def main():
     ap.add_argument("--rotate", type=int, default=0, help="independent caches to rotate (0 = auto, >256 MB)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workload", choices=["decode", "encode", "append"], default="decode",
+                    help="decode (the BASELINE metric, default); encode / append: configs[3] workloads")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -213,6 +302,33 @@ def main():
     if args.context % 64:
         sys.exit("--context must be a multiple of 64")
     layout = LAYOUTS[args.layout]
+    if args.workload == "encode":
+        r = run_encode(args, layout)
+        nbytes = r["read"] + r["write"]
+        gbps = nbytes / (r["ms"] * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": "page encode us/step (bulk prefill), Llama-3-8B kv shape",
+            "value": round(r["ms"] * 1e3, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(r["ms"], 6), "higher_is_better": False,
+            "dtype": "f16", "data": "synthetic",
+            "config": {"workload": f"encode {args.context} fp16 tokens x {args.hkv} kv heads into "
+                                   f"{r['n_pages']} pages (BASELINE configs[3])", "layout": args.layout},
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+            "algorithmic_bytes_per_step": {"read": r["read"], "write": r["write"]},
+        }))
+        return
+    if args.workload == "append":
+        r = run_append(args, layout)
+        print(json.dumps({
+            "metric": "single-token append latency, Llama-3-8B kv shape",
+            "value": round(r["us_per_append"], 2), "unit": "us/append", "n_gpus": 1,
+            "higher_is_better": False, "dtype": "f16", "data": "synthetic",
+            "config": {"workload": f"{r['appends']} single-token appends of {args.hkv} kv heads "
+                                   f"through TurboPolarKVCacheRuntime.append, {r['pages']} page encodes "
+                                   f"(BASELINE configs[3])", "layout": args.layout},
+        }))
+        return
     n_pages = args.context // 64
     step_bytes = algorithmic_bytes(args.hq, args.hkv, n_pages, layout)
     if not args.rotate:

@@ -167,6 +167,13 @@ int32_t tp_selftest_f16_tables(uint16_t* sqrt_out, uint16_t* log_out, uint8_t* c
 int32_t tp_selftest_atan2_exhaustive(unsigned long long* mismatches, int32_t x_begin,
                                      int32_t x_count, void* stream);
 
+/* Counts, over positive fp16 scale patterns [s_begin, s_begin+s_count) and all
+ * 65536 value patterns (finite values only), the quotients where the V
+ * quantiser's reciprocal-product fp16 division differs from the correctly
+ * rounded one.  *mismatches is accumulated (atomic add), so zero it first. */
+int32_t tp_selftest_div_f16_exhaustive(unsigned long long* mismatches, int32_t s_begin,
+                                       int32_t s_count, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -160,3 +160,15 @@ def test_atan2_fast_path_exhaustive(device):
         _lib.check(st, "selftest atan2")
     torch.cuda.synchronize()
     assert int(cnt.item()) == 0, f"{int(cnt.item())} fp16 pairs where the fast atan2 differs"
+
+
+def test_v_quotient_fast_path_exhaustive(device):
+    """Reciprocal-product fp16 division + midpoint guard == correctly rounded
+    fp16(v / s) for every positive finite fp16 scale and every finite value."""
+    cnt = torch.zeros(1, dtype=torch.int64, device=device)
+    step = 4096
+    for s0 in range(0, 32768, step):
+        st = _lib.lib().tp_selftest_div_f16_exhaustive(cnt.data_ptr(), s0, step, torch.cuda.current_stream().cuda_stream)
+        _lib.check(st, "selftest div")
+    torch.cuda.synchronize()
+    assert int(cnt.item()) == 0, f"{int(cnt.item())} (v, s) pairs where the fast quotient differs"

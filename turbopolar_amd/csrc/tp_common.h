@@ -42,10 +42,18 @@ constexpr uint16_t kF16VScaleFloor = 0x068E;   // fp16(1e-4)
 constexpr float kF32Pi = 3.14159274101257324f;
 constexpr float kF32TwoPi = 6.28318548202514648f;
 constexpr float kF32OneMinusEps = 0.999998986721038818f;
+// fp32(1 / 6.28125), the reciprocal of fp16(2*pi) (0.5 fp32 ulp from exact).
+constexpr float kF32InvF16TwoPi = 0.159203976392745972f;
 
-// fp32 ulps around an fp16 rounding midpoint inside which the fast atan2/log
-// results are recomputed in float64.
-constexpr int kMidpointGuard = 16;
+// fp32 ulps around an fp16 rounding midpoint inside which a fast fp32 result
+// is not trusted and the exact path decides.  Each guard exceeds the fast
+// path's error: v_sqrt_f32 is within 1 ulp, a v_rcp_f32 product within 2, the
+// fp32 atan2f and logf within a few; the atan2, sqrt, log and angle-code paths
+// are checked over every fp16 input by the self-test kernels.
+constexpr int kGuardAtan2 = 4;
+constexpr int kGuardLog = 16;
+constexpr int kGuardSqrt = 2;
+constexpr int kGuardDiv = 3;
 
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(f16, b); }
 __device__ __forceinline__ uint16_t f2h(float x) { return __builtin_bit_cast(uint16_t, (f16)x); }
@@ -60,29 +68,65 @@ __device__ __forceinline__ uint16_t d2h(double d) {
 
 // True when the fp32 value `v` is too close to an fp16 rounding boundary (or in
 // the fp16 subnormal range) for its rounding to be trusted.
+template <int kGuard>
 __device__ __forceinline__ bool near_f16_midpoint(float v) {
   const uint32_t u = __float_as_uint(v) & 0x7fffffffu;
   const int low = (int)(u & 0x1fffu) - 0x1000;
-  return u < 0x38800000u || (low <= kMidpointGuard && low >= -kMidpointGuard);
+  return u < 0x38800000u || (low <= kGuard && low >= -kGuard);
 }
+
+// fp16 atan2(y, x) for fp16-representable x, y from the fp32 atan2f; *exact
+// is cleared when the result is too close to an fp16 rounding boundary to be
+// trusted (the caller then uses atan2_f16_slow).
+__device__ __forceinline__ uint16_t atan2_f16_fast(float y, float x, bool* exact) {
+  *exact = true;
+  if (y == 0.0f && !__builtin_signbit(x)) return f2h(y);  // exact +-0
+  const float a = atan2f(y, x);
+  *exact = !near_f16_midpoint<kGuardAtan2>(a);
+  return f2h(a);
+}
+__device__ __forceinline__ uint16_t atan2_f16_slow(float y, float x) { return d2h(atan2((double)y, (double)x)); }
 
 // Correctly rounded fp16 atan2(y, x) for fp16-representable x, y.
 __device__ __forceinline__ uint16_t atan2_f16(float y, float x) {
-  if (y == 0.0f && !__builtin_signbit(x)) return f2h(y);  // exact +-0
-  const float a = atan2f(y, x);
-  if (near_f16_midpoint(a)) return d2h(atan2((double)y, (double)x));
-  return f2h(a);
+  bool exact;
+  const uint16_t a = atan2_f16_fast(y, x, &exact);
+  return exact ? a : atan2_f16_slow(y, x);
 }
 
-// Correctly rounded fp16 natural log of a positive fp16 value (or +inf).
-__device__ __forceinline__ uint16_t log_f16(float r) {
+// Correctly rounded fp16 natural log of a positive fp16 value (or +inf); the
+// fast/slow split mirrors atan2_f16.
+__device__ __forceinline__ uint16_t log_f16_fast(float r, bool* exact) {
   const float l = logf(r);
-  if (near_f16_midpoint(l)) return d2h(log((double)r));
+  *exact = !near_f16_midpoint<kGuardLog>(l);
   return f2h(l);
 }
+__device__ __forceinline__ uint16_t log_f16_slow(float r) { return d2h(log((double)r)); }
+__device__ __forceinline__ uint16_t log_f16(float r) {
+  bool exact;
+  const uint16_t l = log_f16_fast(r, &exact);
+  return exact ? l : log_f16_slow(r);
+}
 
-// Correctly rounded fp16 sqrt of a non-negative fp16 value.
-__device__ __forceinline__ uint16_t sqrt_f16(float s) { return f2h(sqrtf(s)); }
+// Correctly rounded fp16 sqrt of a non-negative fp16 value: v_sqrt_f32 (within
+// 1 fp32 ulp) unless that lands near an fp16 rounding boundary, then the
+// correctly rounded fp32 sqrt (which fp16 rounding cannot distinguish from the
+// exact root: 24 >= 2 * 11 + 2 significant bits).
+__device__ __forceinline__ uint16_t sqrt_f16(float s) {
+  const float r = __builtin_amdgcn_sqrtf(s);
+  if (r != 0.0f && near_f16_midpoint<kGuardSqrt>(r)) return f2h(sqrtf(s));
+  return f2h(r);
+}
+
+// fp16(v / s) for fp16-representable v and s > 0 (rs = v_rcp_f32(s)): the
+// reciprocal product is within 2 fp32 ulps of v / s, so its fp16 rounding is
+// the correctly rounded quotient's unless it is near an fp16 rounding
+// boundary; then the correctly rounded fp32 division decides.
+__device__ __forceinline__ float div_f16(float v, float s, float rs) {
+  const float q = v * rs;
+  if (q != 0.0f && near_f16_midpoint<kGuardDiv>(q)) return h2f(f2h(v / s));
+  return h2f(f2h(q));
+}
 
 // encoder.py:33 for fp16 inputs: f16(sqrt(f16(f16(x*x) + f16(y*y)))).
 __device__ __forceinline__ uint16_t radius_f16_in(float x, float y) {
@@ -102,7 +146,7 @@ __device__ __forceinline__ uint16_t radius_f32_in(float x, float y) {
 // float32 product with (2^bits - 1) rounded half-even.
 __device__ __forceinline__ uint32_t angle_code_f16(uint16_t a16, int bits) {
   float n = h2f(f2h(h2f(a16) + h2f(kF16Pi)));
-  n = h2f(f2h(n / h2f(kF16TwoPi)));
+  n = div_f16(n, h2f(kF16TwoPi), kF32InvF16TwoPi);
   n = fminf(fmaxf(n, 0.0f), 1.0f);
   const float lv = (float)((1 << bits) - 1);
   const float c = rintf(n * lv);

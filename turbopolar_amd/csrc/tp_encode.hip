@@ -36,38 +36,36 @@ struct EncodeArgs {
   int64_t page_begin;
 };
 
-// 32 consecutive input values of one token row as floats (zeros past the end:
-// the zero padding of _maybe_encode_partial, turbo_polar_cache.py:280-285).
+// 32 consecutive input values of one token row: issue the loads (raw) first,
+// convert to floats later, so K and V rows are in flight together.  Tokens past
+// the end read as zeros (the zero padding of _maybe_encode_partial,
+// turbo_polar_cache.py:280-285).
 template <bool kF32>
-__device__ __forceinline__ void load_row32(const void* base, int64_t off, bool valid, float* out) {
-  if (!valid) {
+struct RawRow32 {
+  uint4 w[kF32 ? 8 : 4];
+};
+
+template <bool kF32>
+__device__ __forceinline__ void load_row32(const void* base, int64_t off, bool valid, RawRow32<kF32>& r) {
+  constexpr int n = kF32 ? 8 : 4;
+  const uint4* p = kF32 ? reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off)
+                        : reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) out[i] = 0.0f;
-    return;
-  }
-  if constexpr (kF32) {
-    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 w = p[i];
-      out[4 * i + 0] = w.x;
-      out[4 * i + 1] = w.y;
-      out[4 * i + 2] = w.z;
-      out[4 * i + 3] = w.w;
-    }
-  } else {
-    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 w = p[i];
-      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        out[8 * i + 2 * j + 0] = h2f((uint16_t)(ws[j] & 0xffffu));
-        out[8 * i + 2 * j + 1] = h2f((uint16_t)(ws[j] >> 16));
-      }
-    }
-  }
+  for (int i = 0; i < n; ++i) r.w[i] = valid ? p[i] : make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Element i of a raw row, and pair j = elements (2j, 2j+1); for fp16 input a
+// pair is exactly one dword.
+template <bool kF32>
+__device__ __forceinline__ uint32_t raw_word(const RawRow32<kF32>& r, int i) {
+  const uint4 w = r.w[i >> 2];
+  return (i & 3) == 0 ? w.x : (i & 3) == 1 ? w.y : (i & 3) == 2 ? w.z : w.w;
+}
+template <bool kF32>
+__device__ __forceinline__ float raw_val(const RawRow32<kF32>& r, int i) {
+  if constexpr (kF32) return __uint_as_float(raw_word(r, i));
+  const uint32_t w = raw_word(r, i >> 1);
+  return h2f((uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu)));
 }
 
 // Packs the codes of pairs [pair0, pair0 + npairs) of all 64 tokens into rows
@@ -122,14 +120,19 @@ __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
   const int64_t slot = bh * a.capacity + a.page_begin + page;
   const int64_t row = slot * kPageTokens + t;
 
+  RawRow32<kF32> kraw, vraw;
+  if (a.k) load_row32<kF32>(a.k, in_off, valid, kraw);
+
   if (a.k) {
-    float kin[32];
-    load_row32<kF32>(a.k, in_off, valid, kin);
     uint16_t r16[16];
+    // Angles whose fast fp32 atan2 lands too close to an fp16 rounding
+    // boundary are flagged here and recomputed in float64 after the loop, so
+    // the float64 path is one loop body instead of 16 unrolled copies.
+    uint32_t afix = 0;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const float x = kin[2 * j];
-      const float y = kin[2 * j + 1];
+      const float x = raw_val(kraw, 2 * j);
+      const float y = raw_val(kraw, 2 * j + 1);
       const int p = 16 * qq + j;
       const int bits = p < a.split_half ? a.l1_bits : a.deep_bits;
       uint32_t code;
@@ -138,22 +141,53 @@ __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
         code = angle_code_f32((float)atan2((double)y, (double)x), bits);
       } else {
         r16[j] = radius_f16_in(x, y);
-        code = angle_code_f16(atan2_f16(y, x), bits);
+        bool exact;
+        const uint16_t a16 = atan2_f16_fast(y, x, &exact);
+        afix |= exact ? 0u : (1u << j);
+        code = angle_code_f16(a16, bits);
       }
       s_codes[t * kPairs + p] = (uint8_t)code;
+    }
+    if constexpr (!kF32) {
+      const uint16_t* pin = static_cast<const uint16_t*>(a.k) + in_off;
+      while (afix) {
+        const int j = __builtin_ctz(afix);
+        afix &= afix - 1u;
+        const uint32_t xy = *reinterpret_cast<const uint32_t*>(pin + 2 * j);  // flagged pairs are never padding
+        const int p = 16 * qq + j;
+        const int bits = p < a.split_half ? a.l1_bits : a.deep_bits;
+        s_codes[t * kPairs + p] =
+            (uint8_t)angle_code_f16(atan2_f16_slow(h2f((uint16_t)(xy >> 16)), h2f((uint16_t)(xy & 0xffffu))), bits);
+      }
     }
 
     if (a.int8_radii) {
       // encoder.py:34-42: lr = f32(f16 log(max(r, fp16(1e-6)))); per-page scale
-      // f16(max|lr| / 127); codes rint(lr / scale).
+      // f16(max|lr| / 127); codes rint(lr / scale).  Flagged logs are redone in
+      // float64 by one loop body that selects its element into place.
       float lr[16];
-      float mx = 0.0f;
+      uint32_t lfix = 0;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const uint16_t rb = r16[j] > kF16RadiusFloor ? r16[j] : kF16RadiusFloor;
-        lr[j] = h2f(log_f16(h2f(rb)));
-        mx = fmaxf(mx, fabsf(lr[j]));
+        bool exact;
+        lr[j] = h2f(log_f16_fast(h2f(rb), &exact));
+        lfix |= exact ? 0u : (1u << j);
       }
+      while (lfix) {
+        const int j = __builtin_ctz(lfix);
+        lfix &= lfix - 1u;
+        uint16_t rb = 0;
+#pragma unroll
+        for (int k2 = 0; k2 < 16; ++k2) rb = k2 == j ? r16[k2] : rb;
+        rb = rb > kF16RadiusFloor ? rb : kF16RadiusFloor;
+        const float exact_lr = h2f(log_f16_slow(h2f(rb)));
+#pragma unroll
+        for (int k2 = 0; k2 < 16; ++k2) lr[k2] = k2 == j ? exact_lr : lr[k2];
+      }
+      float mx = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(lr[j]));
       mx = wave_max(mx);
       if ((tid & 63) == 0) s_max[tid >> 6] = mx;
       __syncthreads();
@@ -188,21 +222,25 @@ __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
   }
 
   if (a.v) {
+    load_row32<kF32>(a.v, in_off, valid, vraw);
     // v_quant/encoder.py:21-25: s = f16(max|v| / 127) (1e-4 if zero),
     // code = int8(clip(rint(v / s))) with an fp16 quotient for fp16 inputs.
-    float vin[32];
-    load_row32<kF32>(a.v, in_off, valid, vin);
     float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(vin[i]));
+    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(raw_val(vraw, i)));
     uint16_t s16 = f2h(m / 127.0f);
     if ((s16 & 0x7fffu) == 0) s16 = kF16VScaleFloor;
     const float s = h2f(s16);
+    const float rs = __builtin_amdgcn_rcpf(s);
     uint32_t packed[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      float qv = vin[i] / s;
-      if constexpr (!kF32) qv = h2f(f2h(qv));
+      float qv;
+      if constexpr (kF32) {
+        qv = raw_val(vraw, i) / s;
+      } else {
+        qv = div_f16(raw_val(vraw, i), s, rs);
+      }
       packed[i >> 2] |= (uint32_t)(to_int8_rne(qv) & 0xff) << (8 * (i & 3));
     }
     uint4* dst = reinterpret_cast<uint4*>(a.v_codes + row * kHeadDim + 32 * qq);
@@ -236,6 +274,21 @@ __global__ __launch_bounds__(256) void atan2_exhaustive_kernel(unsigned long lon
     const float y = h2f((uint16_t)yb);
     const uint16_t fast = atan2_f16(y, x);
     const uint16_t ref = d2h(atan2((double)y, (double)x));
+    bad = fast != ref ? 1u : 0u;
+  }
+  const unsigned long long ballot = __ballot(bad);
+  if ((threadIdx.x & 63) == 0 && ballot) atomicAdd(mismatches, (unsigned long long)__popcll(ballot));
+}
+
+__global__ __launch_bounds__(256) void div_exhaustive_kernel(unsigned long long* mismatches, int32_t s_begin) {
+  const uint32_t sb = (uint32_t)(s_begin + (int32_t)blockIdx.y) & 0x7fffu;
+  const uint32_t vb = blockIdx.x * 256u + threadIdx.x;
+  uint32_t bad = 0;
+  if (sb != 0 && (sb & 0x7c00u) != 0x7c00u && (vb & 0x7c00u) != 0x7c00u) {
+    const float s = h2f((uint16_t)sb);
+    const float v = h2f((uint16_t)vb);
+    const uint16_t fast = f2h(div_f16(v, s, __builtin_amdgcn_rcpf(s)));
+    const uint16_t ref = f2h(v / s);
     bad = fast != ref ? 1u : 0u;
   }
   const unsigned long long ballot = __ballot(bad);
@@ -354,6 +407,18 @@ int32_t tp_selftest_atan2_exhaustive(unsigned long long* mismatches, int32_t x_b
   hipLaunchKernelGGL(atan2_exhaustive_kernel, dim3(256, (unsigned)x_count), dim3(256), 0,
                      static_cast<hipStream_t>(stream), mismatches, x_begin);
   return launch_status("tp_selftest_atan2_exhaustive");
+}
+
+int32_t tp_selftest_div_f16_exhaustive(unsigned long long* mismatches, int32_t s_begin, int32_t s_count,
+                                       void* stream) {
+  clear_error();
+  if (!mismatches || s_begin < 0 || s_count < 1 || s_begin + s_count > 32768) {
+    set_error("bad self-test range");
+    return TP_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(div_exhaustive_kernel, dim3(256, (unsigned)s_count), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), mismatches, s_begin);
+  return launch_status("tp_selftest_div_f16_exhaustive");
 }
 
 }  // extern "C"
