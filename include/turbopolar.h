@@ -41,7 +41,8 @@ enum {
   TP_ERR_INVALID = 1,     /* bad argument (shape, pointer, size) */
   TP_ERR_UNSUPPORTED = 2, /* layout the kernels do not implement */
   TP_ERR_HIP = 3,         /* HIP launch/runtime error */
-  TP_ERR_WORKSPACE = 4    /* workspace missing or too small */
+  TP_ERR_WORKSPACE = 4,   /* workspace missing or too small */
+  TP_ERR_NONFINITE = 5    /* tp_append_stage: the input holds NaN or inf */
 };
 
 /* Compression layout of the key codes; the fields of TurboPolarConfig that
@@ -150,6 +151,22 @@ int32_t tp_default_pages_per_split(int64_t batch, int32_t hq, int32_t hkv, int32
 int32_t tp_decode_pages(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
                         int64_t page_begin, int32_t n_pages, void* k_out, void* v_out,
                         void* stream);
+
+/* Append staging (replaces the per-input mx.isfinite(...).all() check of
+ * TurboPolarKVCacheRuntime._validate_append_inputs, turbo_polar_cache.py:69,
+ * and the dense-tail concatenation of append, :114-115).
+ *
+ * k, v: [bh][in_tokens][128] of in_dtype (0 fp16, 1 fp32), 16-byte aligned.
+ * Copies tokens [copy_begin, copy_begin + n_copy) of every (b, h) row into
+ * tail_k / tail_v ([bh][tail_tokens][128], same dtype) at token tail_pos.
+ * With check != 0 it also scans every element of k and v; the kernel stores
+ * `epoch` into *flag (caller-owned device memory) if any is NaN or inf, and
+ * this call then synchronises `stream`, reads the flag and returns
+ * TP_ERR_NONFINITE, or TP_OK.  Pass a fresh epoch per call so the flag never
+ * needs clearing.  With check == 0 the call is asynchronous like the others. */
+int32_t tp_append_stage(const void* k, const void* v, int32_t in_dtype, int64_t bh, int64_t in_tokens,
+                        int64_t copy_begin, int64_t n_copy, void* tail_k, void* tail_v, int64_t tail_tokens,
+                        int64_t tail_pos, int32_t check, uint32_t* flag, uint32_t epoch, void* stream);
 
 /* ---- Self-test hooks: no counterpart in the reference.  They evaluate the
  * encoder's scalar fp16 helpers so tests can check them exhaustively. ---- */

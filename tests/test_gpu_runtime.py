@@ -188,3 +188,68 @@ def test_append_rejects_nonfinite_and_changes(device):
     bad[0, 0, 0, 0] = float("inf")
     with pytest.raises(ValueError, match="finite"):
         rt.append(bad, good[:, :, :2])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("where,value", [("k", float("inf")), ("v", float("nan")), ("k", float("-inf"))])
+def test_append_stage_rejects_without_state_change(device, dtype, where, value):
+    """tp_append_stage scans every element: a non-finite value anywhere raises
+    the reference's ValueError and leaves length, tail and storage unchanged."""
+    print(f"[append-stage] dtype={dtype} {where}={value}", flush=True)
+    rt = TurboPolarKVCacheRuntime(_cfg("default", hq=8, hkv=4))
+    base_k = torch.randn((1, 4, 100, 128), device=device).to(dtype)
+    base_v = torch.randn((1, 4, 100, 128), device=device).to(dtype)
+    rt.append(base_k, base_v)  # one page + 36 tail tokens
+    tail_before = rt.partial_k.clone()
+    tel_before = rt.get_io_telemetry()
+    for T, pos in ((1, 0), (30, 29), (200, 137)):
+        k = torch.randn((1, 4, T, 128), device=device).to(dtype)
+        v = torch.randn((1, 4, T, 128), device=device).to(dtype)
+        (k if where == "k" else v)[0, 3, pos, 127] = value
+        with pytest.raises(ValueError, match="finite"):
+            rt.append(k, v)
+        assert rt.actual_seq_len == 100 and rt.total_blocks == 1
+        assert torch.equal(rt.partial_k, tail_before)
+        assert rt.get_io_telemetry() == tel_before
+    # the cache still works afterwards
+    k = torch.randn((1, 4, 28, 128), device=device).to(dtype)
+    rt.append(k, k)
+    assert rt.actual_seq_len == 128 and rt.total_blocks == 2 and rt.partial_k is None
+
+
+def test_append_error_order_matches_reference(device):
+    """Non-finite input together with a changed batch size: the finiteness
+    error comes first, as in turbo_polar_cache.py:69-75."""
+    rt = TurboPolarKVCacheRuntime(_cfg("default", hq=4, hkv=4))
+    x = torch.randn((1, 4, 3, 128), device=device, dtype=torch.float16)
+    rt.append(x, x)
+    y = torch.randn((2, 4, 1, 128), device=device, dtype=torch.float16)
+    y[1, 0, 0, 0] = float("nan")
+    with pytest.raises(ValueError, match="finite"):
+        rt.append(y, y)
+    with pytest.raises(ValueError, match="batch size changed"):
+        rt.append(y.nan_to_num(), y.nan_to_num())
+
+
+def test_single_token_appends_match_bulk(device):
+    """4096 single-token appends (BASELINE configs[3] workload 2, shortened to
+    200 + a page boundary mix) give the storage and tail of one bulk append."""
+    cfg = _cfg("default", hq=8, hkv=2)
+    k = torch.randn((1, 2, 200, 128), device=device, dtype=torch.float16)
+    v = torch.randn((1, 2, 200, 128), device=device, dtype=torch.float16)
+    a = TurboPolarKVCacheRuntime(cfg)
+    for t in range(200):
+        a.append(k[:, :, t:t + 1], v[:, :, t:t + 1])
+    b = TurboPolarKVCacheRuntime(cfg)
+    for lo, hi in ((0, 7), (7, 64), (64, 65), (65, 200)):
+        b.append(k[:, :, lo:hi], v[:, :, lo:hi])
+    c = TurboPolarKVCacheRuntime(cfg)
+    c.append(k, v)
+    for r in (a, b):
+        assert r.actual_seq_len == c.actual_seq_len == 200 and r.total_blocks == c.total_blocks == 3
+        assert torch.equal(r.partial_k, c.partial_k) and torch.equal(r.partial_v, c.partial_v)
+        bk, bv, *_ = r.get_fused_attention_inputs()
+        ck, cv, *_ = c.get_fused_attention_inputs()
+        assert torch.equal(bk.radii, ck.radii) and torch.equal(bk.angle_codes_l1, ck.angle_codes_l1)
+        assert torch.equal(bk.angle_codes_deep, ck.angle_codes_deep)
+        assert torch.equal(bv.codes, cv.codes) and torch.equal(bv.scales, cv.scales)

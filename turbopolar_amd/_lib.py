@@ -22,6 +22,7 @@ TP_ERR_INVALID = 1
 TP_ERR_UNSUPPORTED = 2
 TP_ERR_HIP = 3
 TP_ERR_WORKSPACE = 4
+TP_ERR_NONFINITE = 5
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -78,6 +79,10 @@ _SIGNATURES = {
     "tp_decode_counter_bytes": (c_size, [c_i64, c_i32, c_i32]),
     "tp_default_pages_per_split": (c_i32, [c_i64, c_i32, c_i32, c_i32]),
     "tp_decode_pages": (c_i32, [_P_LAYOUT, _P_PAGES, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp]),
+    "tp_append_stage": (
+        c_i32,
+        [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i32, c_vp, ctypes.c_uint32, c_vp],
+    ),
     "tp_selftest_f16_tables": (c_i32, [c_vp, c_vp, c_vp, c_vp]),
     "tp_selftest_atan2_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
     "tp_selftest_div_f16_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
@@ -115,7 +120,7 @@ def check(status: int, what: str) -> None:
     if status == TP_OK:
         return
     msg = lib().tp_last_error().decode(errors="replace")
-    if status in (TP_ERR_INVALID, TP_ERR_UNSUPPORTED):
+    if status in (TP_ERR_INVALID, TP_ERR_UNSUPPORTED, TP_ERR_NONFINITE):
         raise ValueError(f"{what}: {msg}")
     raise TurboPolarHipError(f"{what}: {msg}")
 

@@ -22,7 +22,7 @@ LIB_NAME = "libturbopolar_hip.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 ARCH = os.environ.get("TP_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["tp_api.hip", "tp_encode.hip", "tp_attention.hip", "tp_decode.hip"]
+SOURCES = ["tp_api.hip", "tp_encode.hip", "tp_attention.hip", "tp_decode.hip", "tp_append.hip"]
 
 # -ffp-contract=off and correctly rounded fp32 divide/sqrt are required for the
 # encoder's bit-exact fp16 rules; packed fp32 VALU ops are disabled.

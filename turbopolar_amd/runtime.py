@@ -53,6 +53,8 @@ class TurboPolarKVCacheRuntime:
         self._tail_k: Optional[torch.Tensor] = None
         self._tail_v: Optional[torch.Tensor] = None
         self._tail_len = 0
+        self._flag: Optional[torch.Tensor] = None  # tp_append_stage verdict (device)
+        self._epoch = 0
 
         self._initialized = False
         self._batch_size: Optional[int] = None
@@ -69,8 +71,8 @@ class TurboPolarKVCacheRuntime:
     def partial_v(self) -> Optional[torch.Tensor]:
         return self._tail_v[:, :, : self._tail_len] if self._tail_len else None
 
-    def _validate_append_inputs(self, k_new, v_new):
-        # turbo_polar_cache.py:55-104, same order and messages.
+    def _validate_shapes(self, k_new, v_new) -> None:
+        # turbo_polar_cache.py:55-68, same order and messages.
         if not isinstance(k_new, torch.Tensor) or not isinstance(v_new, torch.Tensor):
             raise TypeError("append() expects torch.Tensor inputs")
         if k_new.ndim != 4 or v_new.ndim != 4:
@@ -86,39 +88,56 @@ class TurboPolarKVCacheRuntime:
             raise ValueError(f"k_new dtype {k_new.dtype} must match v_new dtype {v_new.dtype}")
         if k_new.dtype not in (torch.float16, torch.float32):
             raise ValueError(f"only float16 and float32 inputs are supported, got {k_new.dtype}")
-        if not bool(torch.isfinite(k_new).all()) or not bool(torch.isfinite(v_new).all()):
-            raise ValueError("append() inputs must contain finite values")
+
+    def _invariant_error(self, k_new) -> Optional[ValueError]:
+        """The error turbo_polar_cache.py:71-104 would raise, without raising it."""
+        B, H_kv, _, D = k_new.shape
         if self._initialized:
             if B != self._batch_size:
-                raise ValueError(
+                return ValueError(
                     f"batch size changed from {self._batch_size} to {B}; "
                     "TurboPolar cache does not support varying batch size."
                 )
             if H_kv != self._num_kv_heads:
-                raise ValueError(
+                return ValueError(
                     f"KV head count changed from {self._num_kv_heads} to {H_kv}; "
                     "TurboPolar cache does not support varying head counts."
                 )
             if D != self._head_dim:
-                raise ValueError(
+                return ValueError(
                     f"head_dim changed from {self._head_dim} to {D}; "
                     "TurboPolar cache does not support varying head dimension."
                 )
             if k_new.dtype != self._input_dtype:
-                raise ValueError(
+                return ValueError(
                     f"input dtype changed from {self._input_dtype} to {k_new.dtype}; "
                     "TurboPolar cache does not support varying dtype."
                 )
         else:
             if H_kv != self.config.num_kv_heads:
-                raise ValueError(f"input has {H_kv} KV heads but config expects {self.config.num_kv_heads}")
+                return ValueError(f"input has {H_kv} KV heads but config expects {self.config.num_kv_heads}")
             if D != self.config.head_dim:
-                raise ValueError(f"input head_dim {D} does not match config {self.config.head_dim}")
+                return ValueError(f"input head_dim {D} does not match config {self.config.head_dim}")
+        return None
+
+    def _commit_invariants(self, k_new) -> None:
+        if not self._initialized:
+            B, H_kv, _, D = k_new.shape
             self._batch_size = B
             self._num_kv_heads = H_kv
             self._head_dim = D
             self._input_dtype = k_new.dtype
             self._initialized = True
+
+    def _validate_append_inputs(self, k_new, v_new):
+        """turbo_polar_cache.py:55-104 in full (shape, finiteness, invariants)."""
+        self._validate_shapes(k_new, v_new)
+        if not bool(torch.isfinite(k_new).all()) or not bool(torch.isfinite(v_new).all()):
+            raise ValueError("append() inputs must contain finite values")
+        err = self._invariant_error(k_new)
+        if err is not None:
+            raise err
+        self._commit_invariants(k_new)
 
     # ------------------------------------------------------------------
     def _page_bytes(self) -> int:
@@ -147,8 +166,66 @@ class TurboPolarKVCacheRuntime:
         self.bytes_written += n_pages * self._page_bytes()
 
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
-        """turbo_polar_cache.py:106-126: extend the tail, flush every full page."""
-        self._validate_append_inputs(k_new, v_new)
+        """turbo_polar_cache.py:106-126: extend the tail, flush every full page.
+
+        On a HIP device one tp_append_stage launch checks the whole input for
+        non-finite values and copies the tokens bound for the dense tail, with
+        a single 4-byte read back (the reference synchronises once per input
+        in mx.isfinite(...).all()).  Errors come in the reference's order and
+        leave the cache unchanged."""
+        self._validate_shapes(k_new, v_new)
+        if not (k_new.is_cuda and v_new.is_cuda) or self._invariant_error(k_new) is not None:
+            self._validate_append_inputs(k_new, v_new)
+            self._append_host_path(k_new, v_new)
+            return
+        B, H, T, D = k_new.shape
+        k_new = k_new.contiguous()
+        v_new = v_new.contiguous()
+        if self._tail_k is not None and self._tail_k.device != k_new.device:
+            raise ValueError(f"append() inputs moved from {self._tail_k.device} to {k_new.device}")
+        if self._tail_k is None:
+            self._tail_k = torch.zeros((B, H, PAGE, D), dtype=k_new.dtype, device=k_new.device)
+            self._tail_v = torch.zeros((B, H, PAGE, D), dtype=k_new.dtype, device=k_new.device)
+        if self._flag is None or self._flag.device != k_new.device:
+            self._flag = torch.zeros(1, dtype=torch.int32, device=k_new.device)
+        if self._tail_len:
+            n_head, head_dst = min(PAGE - self._tail_len, T), self._tail_len
+        elif T < PAGE:
+            n_head, head_dst = T, 0
+        else:
+            n_head, head_dst = 0, 0
+        self._stage(k_new, v_new, 0, n_head, head_dst, check=True)
+        self._commit_invariants(k_new)
+        self.actual_seq_len += T
+        self._tail_len += n_head
+        pos = n_head
+        if self._tail_len == PAGE:
+            self._encode_into_storage(self._tail_k, self._tail_v, 0, 1)
+            self._tail_len = 0
+        n_full = (T - pos) // PAGE
+        if n_full:
+            self._encode_into_storage(k_new, v_new, pos, n_full)
+            pos += n_full * PAGE
+        rem = T - pos
+        if rem:
+            self._stage(k_new, v_new, pos, rem, 0, check=False)
+            self._tail_len = rem
+
+    def _stage(self, k, v, begin: int, n: int, dst: int, check: bool) -> None:
+        B, H, T, _ = k.shape
+        self._epoch = self._epoch % 0xFFFFFFFE + 1
+        with torch.cuda.device(k.device):
+            st = _lib.lib().tp_append_stage(
+                k.data_ptr(), v.data_ptr(), 1 if k.dtype == torch.float32 else 0, B * H, T, begin, n,
+                self._tail_k.data_ptr(), self._tail_v.data_ptr(), PAGE, dst, 1 if check else 0,
+                self._flag.data_ptr(), self._epoch, _lib.stream_of(k.device),
+            )
+        if st == _lib.TP_ERR_NONFINITE:
+            raise ValueError("append() inputs must contain finite values")
+        _lib.check(st, "tp_append_stage")
+
+    def _append_host_path(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+        """Tail bookkeeping with tensor copies (CPU tensors; flushes need HIP)."""
         B, H, T, D = k_new.shape
         self.actual_seq_len += T
         if self._tail_k is None:
