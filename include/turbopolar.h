@@ -119,7 +119,9 @@ int32_t tp_fused_qk(const void* q, int64_t batch, int32_t hq, int32_t hkv,
  * tail_k, tail_v: fp16 [batch][hkv][tail_stride][128] holding tail_len (0..63)
  *   dense tokens that follow the pages (NULL when tail_len == 0).
  * Tokens with global index >= actual_seq_len are masked.
- * pages_per_split: pages per workgroup (0 = library default).
+ * pages_per_split: pages per workgroup (0 = library default); the grid,
+ *   ceil(n_pages / pages_per_split) x batch x hkv x ceil(hq / hkv / 16)
+ *   workgroups, must stay below 2^31.
  * workspace: device memory of at least tp_decode_workspace_bytes(...) bytes.
  *   Its counter area (the first tp_decode_counter_bytes(batch, hq, hkv) bytes)
  *   must be zero before the first call; every call leaves it zero again.  One
@@ -136,7 +138,10 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
 size_t tp_decode_workspace_bytes(int64_t batch, int32_t hq, int32_t hkv, int32_t n_pages,
                                  int32_t tail_len, int32_t pages_per_split);
 
-/* Size of the zero-initialised counter area at the start of the workspace. */
+/* Size of the zero-initialised counter area at the start of the workspace:
+ * 64 KiB for up to 16384 units (batch x hkv x ceil(hq / hkv / 16)), 4 bytes
+ * per unit beyond.  Up to that size it is the same for every shape, so one
+ * workspace, zeroed once, serves calls of any shape. */
 size_t tp_decode_counter_bytes(int64_t batch, int32_t hq, int32_t hkv);
 
 /* Pages per workgroup that tp_decode_attention uses when given 0. */

@@ -95,14 +95,15 @@ def test_decode_attention_argument_validation():
     assert st == _lib.TP_ERR_INVALID and "nothing to attend" in msg
     st, msg = call(pps=1)  # 4 splits need a workspace
     assert st == _lib.TP_ERR_WORKSPACE and "workspace" in msg
-    # The combine's LDS table bounds splits x (query heads per kv head, at most 16) by 6144.
-    big = _fake_pages(capacity=4096)
+    # The grid (splits x units workgroups) must stay below 2^31: 2^30 one-page
+    # splits of 8 kv heads do not fit.
+    big = _fake_pages(capacity=1 << 30)
+    st = L.tp_decode_attention(4096, 1, 8, 8, ctypes.byref(lay), ctypes.byref(big), 1 << 30, None, None, 0, 0,
+                               (1 << 30) * 64, 0.088, 1, None, 0, 8192, None)
+    assert st == _lib.TP_ERR_INVALID and b"grid limit" in L.tp_last_error()
     st = L.tp_decode_attention(4096, 1, 8, 2, ctypes.byref(lay), ctypes.byref(big), 1537, None, None, 0, 0,
                                1537 * 64, 0.088, 1, None, 0, 8192, None)
-    assert st == _lib.TP_ERR_INVALID and b"too many splits" in L.tp_last_error()
-    st = L.tp_decode_attention(4096, 1, 8, 2, ctypes.byref(lay), ctypes.byref(big), 1536, None, None, 0, 0,
-                               1536 * 64, 0.088, 1, None, 0, 8192, None)
-    assert st == _lib.TP_ERR_WORKSPACE  # 1536 x 4 fits; only the missing workspace is reported
+    assert st == _lib.TP_ERR_WORKSPACE  # any number of splits that fits the grid is accepted
 
 
 def test_workspace_sizes():
@@ -111,11 +112,12 @@ def test_workspace_sizes():
     assert L.tp_default_pages_per_split(1, 32, 8, 512) == 16
     n = L.tp_decode_workspace_bytes(1, 32, 8, 512, 0, 16)
     counters = L.tp_decode_counter_bytes(1, 32, 8)
-    assert counters == 256
+    assert counters == 65536  # fixed area: records start at the same offset for every shape
     splits = 32
     assert n == counters + 8 * splits * 16 * 2 * 4 + 8 * splits * 16 * 128 * 4
     # GQA group > 16 uses two head blocks
-    assert L.tp_decode_counter_bytes(2, 40, 2) == 256
+    assert L.tp_decode_counter_bytes(2, 40, 2) == 65536
+    assert L.tp_decode_counter_bytes(4096, 8, 8) == 32768 * 4  # beyond 16384 units the area grows
     assert L.tp_decode_workspace_bytes(1, 40, 2, 2, 0, 1) > L.tp_decode_workspace_bytes(1, 16, 1, 2, 0, 1)
 
 

@@ -94,6 +94,10 @@ CASES = [
     ("odd_split", 8, 4, 3, 9, 2),
     ("int8_default_angles", 4, 2, 2, 0, 1),
     ("default", 40, 2, 2, 11, 1),  # GQA 20 > 16: two head blocks
+    ("default", 6, 2, 3, 5, 1),  # GQA 3: 1 dim per folding thread, 5 split groups
+    ("default", 12, 2, 4, 0, 1),  # GQA 6: 2 dims per folding thread
+    ("default", 24, 2, 3, 9, 1),  # GQA 12: 4 dims per folding thread, 1 split group
+    ("default", 2, 2, 600, 3, 1),  # 600 splits of one head: 16 split groups, chunked reloads
 ]
 
 
@@ -158,13 +162,26 @@ def test_split_invariance(device):
 
 
 def test_max_splits_combine(device):
-    """The split cap (splits x query heads per kv head = 6144): 1536 one-page
-    splits of 4 heads fill the combine's LDS table and run its chunked reloads."""
+    """1536 one-page splits of 4 heads: the combine folds 384 records per
+    thread in chunks of 8 reloads."""
     print("[attn-maxsplits] S=1536 pps=1", flush=True)
     block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], 8, 2, 1536, 9, seed=21)
     seq = 1536 * PAGE + 9
     out = run_gpu(device, block, qv, tk, tv, q, seq, pps=1)
     check(out, oracle_out(host, tk, tv, q, seq), "max splits")
+
+
+def test_workspace_shared_across_shapes(device):
+    """One workspace serves calls whose unit counts (batch x kv heads x head
+    blocks) rise and fall: every call's records land after the fixed counter
+    area, so no call finds an earlier call's records where its counters are."""
+    for i, (hq, hkv, S, tail, pps) in enumerate([(4, 2, 5, 3, 1), (32, 8, 5, 1, 2), (8, 1, 6, 0, 1),
+                                                 (64, 8, 4, 9, 1), (4, 2, 7, 0, 2), (32, 8, 3, 0, 1)]):
+        print(f"[attn-shared-ws] hq={hq} hkv={hkv} S={S} tail={tail} pps={pps}", flush=True)
+        block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], hq, hkv, S, tail, seed=40 + i)
+        seq = S * PAGE + tail
+        out = run_gpu(device, block, qv, tk, tv, q, seq, pps=pps)
+        check(out, oracle_out(host, tk, tv, q, seq), f"shape {i}")
 
 
 def test_page_decode_parity(device):

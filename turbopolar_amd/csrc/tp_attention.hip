@@ -66,6 +66,7 @@ struct AttnArgs {
   float scale_log2;
   int32_t pages_per_split;
   int32_t n_splits;
+  int32_t counter_stride;  // u32 words between the ticket counters of two units
   uint32_t* counters;
   float* part_ml;
   float* part_acc;
@@ -512,75 +513,41 @@ __device__ __forceinline__ void st_agent2(float* p, float x, float y) {
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-
 constexpr int kRedStride = 132;  // padded LDS row of one head's 128 accumulators
-// Bound on splits x heads per head block: the combine's (weight, l) table
-// (48 KiB) and its 8 KiB reduction area share the 67.5 KiB accumulator region.
-constexpr int kMaxSplitHeads = 6144;
-
-
-// Softmax-merge state of 8 output dims of one head: running max M (log2
-// units), sum L, and the unnormalised accumulators A.
-struct Fold {
-  float M, L;
-  float A[8];
-};
-
-// Folds up to 8 partial records (of the waves of one workgroup, in LDS) into
-// `st`.  Record u has (m, l) at ml[u * ml_stride + {0, 1}] and 8 accumulators
-// at acc[u * acc_stride + 0..7].  All loads are issued before the first use.
-__device__ __forceinline__ Fold fold_records(Fold st, const float* ml, int ml_stride, const float* acc,
-                                             int acc_stride, int count) {
-  float m[8], l[8], x[8][8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    m[u] = -INFINITY;
-    l[u] = 0.0f;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) x[u][d] = 0.0f;
-    if (u < count) {
-      m[u] = ml[u * ml_stride];
-      l[u] = ml[u * ml_stride + 1];
-#pragma unroll
-      for (int d = 0; d < 8; ++d) x[u][d] = acc[u * acc_stride + d];
-    }
-  }
-  float M = st.M;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) M = fmaxf(M, m[u]);
-  Fold out;
-  out.M = M;
-  if (M == -INFINITY) return st;
-  const float w0 = __builtin_amdgcn_exp2f(st.M - M);  // 0 for an empty state
-  out.L = st.L * w0;
-#pragma unroll
-  for (int d = 0; d < 8; ++d) out.A[d] = st.A[d] * w0;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const float w = m[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[u] - M);
-    out.L += l[u] * w;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) out.A[d] += x[u][d] * w;
-  }
-  return out;
+// Ticket counters live in a fixed 64 KiB area at the start of the workspace,
+// so its record area starts at the same offset for every shape and a workspace
+// shared by calls of different shapes never finds records where counters
+// belong.  Counters sit 256 bytes apart while the units fit (the tickets of all
+// units arrive within a few microseconds, and one shared cache line serialises
+// them), closer beyond 256 units; beyond 16384 units the area grows.
+constexpr size_t kCounterArea = 65536;
+static inline int32_t counter_stride_of(int64_t units) {
+  int32_t w = 64;
+  while (w > 1 && (size_t)units * w * sizeof(uint32_t) > kCounterArea) w >>= 1;
+  return w;
 }
 
-__device__ __forceinline__ Fold empty_fold() {
-  Fold f;
-  f.M = -INFINITY;
-  f.L = 0.0f;
-#pragma unroll
-  for (int d = 0; d < 8; ++d) f.A[d] = 0.0f;
-  return f;
+// Store of 1, 2 or 4 consecutive floats with sc1 (dpt is wave-uniform).
+__device__ __forceinline__ void st_agent_n(float* p, const float* x, int dpt) {
+  if (dpt == 4) {
+    st_agent4(p, float4v{x[0], x[1], x[2], x[3]});
+  } else if (dpt == 2) {
+    st_agent2(p, x[0], x[1]);
+  } else {
+    asm volatile("global_store_dword %0, %1, off sc1" : : "v"(p), "v"(x[0]) : "memory");
+  }
 }
 
-// Normalised fp16 output of 8 dims.
-__device__ __forceinline__ void store_out8(uint16_t* orow, const Fold& f) {
-  const float inv = __builtin_amdgcn_rcpf(f.L);
-  uint32_t w[4];
-#pragma unroll
-  for (int d = 0; d < 4; ++d) w[d] = (uint32_t)f2h(f.A[2 * d] * inv) | ((uint32_t)f2h(f.A[2 * d + 1] * inv) << 16);
-  *reinterpret_cast<uint4*>(orow) = make_uint4(w[0], w[1], w[2], w[3]);
+// Normalised fp16 output of 1, 2 or 4 consecutive dims.
+__device__ __forceinline__ void store_out_n(uint16_t* orow, const float* x, float inv, int dpt) {
+  if (dpt == 4) {
+    *reinterpret_cast<uint2*>(orow) = make_uint2((uint32_t)f2h(x[0] * inv) | ((uint32_t)f2h(x[1] * inv) << 16),
+                                                 (uint32_t)f2h(x[2] * inv) | ((uint32_t)f2h(x[3] * inv) << 16));
+  } else if (dpt == 2) {
+    *reinterpret_cast<uint32_t*>(orow) = (uint32_t)f2h(x[0] * inv) | ((uint32_t)f2h(x[1] * inv) << 16);
+  } else {
+    *orow = f2h(x[0] * inv);
+  }
 }
 
 template <int WAVES>
@@ -691,42 +658,64 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   }
   lds_barrier();
 
-  // Thread (h = item / 16, c = item % 16) owns dims [8c, 8c+8) of head h.
-  const int item = tid & 255;
-  const int h = item >> 4;
-  const int c = item & 15;
-  Fold f = empty_fold();
-  if (tid < 256)
-    f = fold_records(f, &sh.ml[0][h][0], 32, &sh.acc[0][h * kRedStride + 8 * c], 16 * kRedStride, WAVES);
-  uint16_t* orow = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + h) * kHeadDim + 8 * c;
+  // Fold the waves' records.  Every thread takes part: thread t owns dpt
+  // consecutive dims of head t / (128 / dpt), with dpt = 1, 2 or 4 for up to
+  // 4, 8 or 16 heads, and folds the WAVES records in wave order.
+  const int dpt = nh <= 4 ? 1 : (nh <= 8 ? 2 : 4);
+  const int tph = kHeadDim / dpt;
+  const int h = tid / tph;
+  const int d0 = (tid - h * tph) * dpt;
+  const bool live = h < nh;
+  float M = -INFINITY, L = 0.0f;
+  float A[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (live) {
+    float m[WAVES], l[WAVES], x[WAVES][4];
+#pragma unroll
+    for (int u = 0; u < WAVES; ++u) {
+      m[u] = sh.ml[u][h][0];
+      l[u] = sh.ml[u][h][1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[u][i] = i < dpt ? sh.acc[u][h * kRedStride + d0 + i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < WAVES; ++u) M = fmaxf(M, m[u]);
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int u = 0; u < WAVES; ++u) {
+        const float w = m[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[u] - M);
+        L += l[u] * w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) A[i] += x[u][i] * w;
+      }
+    }
+  }
   if (a.n_splits == 1) {
-    if (tid < 256 && h < nh) store_out8(orow, f);
+    if (live)
+      store_out_n(a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + h) * kHeadDim + d0, A,
+                  __builtin_amdgcn_rcpf(L), dpt);
     return;
   }
   const int64_t unit = bkv * a.head_blocks + hb;
   const int S = a.n_splits;
   const int Sp = (S + 1) & ~1;  // (m, l) row length in pairs
-  if (tid < 256 && h < nh) {
-    if (c == 0) st_agent2(a.part_ml + ((unit * 16 + h) * Sp + split) * 2, f.M, f.L);
-    float* pa = a.part_acc + ((unit * S + split) * 16 + h) * kHeadDim + 8 * c;
-    st_agent4(pa, float4v{f.A[0], f.A[1], f.A[2], f.A[3]});
-    st_agent4(pa + 4, float4v{f.A[4], f.A[5], f.A[6], f.A[7]});
+  if (live) {
+    if (d0 == 0) st_agent2(a.part_ml + ((unit * 16 + h) * Sp + split) * 2, M, L);
+    st_agent_n(a.part_acc + ((unit * S + split) * 16 + h) * kHeadDim + d0, A, dpt);
   }
   wait_stores();
   __syncthreads();
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(a.counters + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(a.counters + unit * a.counter_stride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     sh.last = prev == (uint32_t)(S - 1);
   }
   __syncthreads();
   if (!sh.last) return;
 
   // Last workgroup of this (b, kv, head block): combine the n_splits records.
-  // The softmax weight of a (split, head) record is shared by its 128 dims, so
-  // it is computed once: one wave per head turns the head's (m, l) row into
-  // w = 2^(m - M) and 1/L in LDS, while every thread's accumulator loads are
-  // already in flight.  Thread (item = (head hh, 4-dim chunk c4), sg) then
-  // sums w * acc over splits sg, sg + SG, ... and the SG sums meet in LDS.
+  // Thread (item = (head hh, 4-dim chunk c4), sg) folds splits sg, sg + SG,
+  // ... online (running max, rescaled sums), with all loads of a batch of 8
+  // records in flight together; the SG partial folds then meet in LDS and are
+  // merged in sg order.
   const int n_items = nh * 32;
   const int SG = max(1, (WAVES * 64) / n_items);
   const int it = tid % n_items;
@@ -735,60 +724,66 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   const int c4 = it & 31;
   const int mine = sg < SG ? (S - sg + SG - 1) / SG : 0;
   const float* pac = a.part_acc + ((unit * S + sg) * 16 + hh) * kHeadDim + 4 * c4;
+  const float* pml = a.part_ml + ((unit * 16 + hh) * Sp + sg) * 2;
   const int64_t rstride = (int64_t)SG * 16 * kHeadDim;
-  float4v x[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) x[u] = u < mine ? *reinterpret_cast<const float4v*>(pac + u * rstride) : float4v{};
-  float* wml = &sh.acc[0][0];
-  float* inv_l = wml + 2 * nh * S;
-  for (int h2 = wave; h2 < nh; h2 += WAVES) {
-    const float* pml = a.part_ml + (unit * 16 + h2) * Sp * 2;
-    float mx = -INFINITY;
-    for (int sp = lane; sp < S; sp += 64) {
-      const float2 r = *reinterpret_cast<const float2*>(pml + 2 * sp);
-      *reinterpret_cast<float2*>(wml + 2 * (h2 * S + sp)) = r;
-      mx = fmaxf(mx, r.x);
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    float lsum = 0.0f;
-    for (int sp = lane; sp < S; sp += 64) {
-      const float2 r = *reinterpret_cast<const float2*>(wml + 2 * (h2 * S + sp));
-      const float w = r.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r.x - mx);
-      wml[2 * (h2 * S + sp)] = w;
-      lsum += w * r.y;
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off, 64);
-    if (lane == 0) inv_l[h2] = __builtin_amdgcn_rcpf(lsum);
-  }
-  lds_barrier();
-  float4v accv = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-  const float* wrow = wml + 2 * (hh * S + sg);
+  float Mc = -INFINITY, Lc = 0.0f;
+  float4v Ac = float4v{0.0f, 0.0f, 0.0f, 0.0f};
   for (int r0 = 0; r0 < mine; r0 += 8) {
-    if (r0 > 0) {
+    float2 r[8];
+    float4v x[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        x[u] = r0 + u < mine ? *reinterpret_cast<const float4v*>(pac + (r0 + u) * rstride) : float4v{};
+    for (int u = 0; u < 8; ++u) {
+      const bool ok = r0 + u < mine;
+      r[u] = ok ? *reinterpret_cast<const float2*>(pml + 2 * SG * (r0 + u)) : make_float2(-INFINITY, 0.0f);
+      x[u] = ok ? *reinterpret_cast<const float4v*>(pac + (r0 + u) * rstride) : float4v{};
     }
+    float Mn = Mc;
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (r0 + u < mine) accv += x[u] * wrow[2 * SG * (r0 + u)];
+    for (int u = 0; u < 8; ++u) Mn = fmaxf(Mn, r[u].x);
+    if (Mn != -INFINITY) {
+      const float w0 = __builtin_amdgcn_exp2f(Mc - Mn);  // 0 while Mc is -inf
+      Lc *= w0;
+      Ac *= w0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float w = r[u].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r[u].x - Mn);
+        Lc += r[u].y * w;
+        Ac += x[u] * w;
+      }
+      Mc = Mn;
+    }
   }
-  float4v* red = reinterpret_cast<float4v*>(wml + ((2 * nh * S + nh + 3) & ~3));
   if (SG > 1) {
-    if (sg < SG) red[sg * n_items + it] = accv;
+    float4v* red = reinterpret_cast<float4v*>(&sh.acc[0][0]);
+    float2* redml = reinterpret_cast<float2*>(red + SG * n_items);
+    if (sg < SG) {
+      red[sg * n_items + it] = Ac;
+      redml[sg * n_items + it] = make_float2(Mc, Lc);
+    }
     lds_barrier();
-    if (sg == 0)
-      for (int g2 = 1; g2 < SG; ++g2) accv += red[g2 * n_items + it];
+    if (sg == 0) {
+      float Mx = Mc;
+      for (int g2 = 1; g2 < SG; ++g2) Mx = fmaxf(Mx, redml[g2 * n_items + it].x);
+      if (Mx != -INFINITY) {
+        const float w0 = __builtin_amdgcn_exp2f(Mc - Mx);
+        Lc *= w0;
+        Ac *= w0;
+        for (int g2 = 1; g2 < SG; ++g2) {
+          const float2 r = redml[g2 * n_items + it];
+          const float w = r.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r.x - Mx);
+          Lc += r.y * w;
+          Ac += red[g2 * n_items + it] * w;
+        }
+      }
+    }
   }
   if (sg == 0) {
-    const float inv = inv_l[hh];
+    const float inv = __builtin_amdgcn_rcpf(Lc);
     uint16_t* orow3 = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + hh) * kHeadDim + 4 * c4;
-    *reinterpret_cast<uint2*>(orow3) = make_uint2((uint32_t)f2h(accv[0] * inv) | ((uint32_t)f2h(accv[1] * inv) << 16),
-                                                  (uint32_t)f2h(accv[2] * inv) | ((uint32_t)f2h(accv[3] * inv) << 16));
+    *reinterpret_cast<uint2*>(orow3) = make_uint2((uint32_t)f2h(Ac[0] * inv) | ((uint32_t)f2h(Ac[1] * inv) << 16),
+                                                  (uint32_t)f2h(Ac[2] * inv) | ((uint32_t)f2h(Ac[3] * inv) << 16));
   }
-  if (tid == 0) __hip_atomic_store(a.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(a.counters + unit * a.counter_stride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- standalone fused QK -----------------------------------------------------------
@@ -924,7 +919,8 @@ int32_t tp_default_pages_per_split(int64_t batch, int32_t hq, int32_t hkv, int32
 
 size_t tp_decode_counter_bytes(int64_t batch, int32_t hq, int32_t hkv) {
   if (batch < 1 || hq < 1 || hkv < 1) return 0;
-  return align256((size_t)batch * hkv * head_blocks_of(hq, hkv) * sizeof(uint32_t));
+  const size_t units = (size_t)batch * hkv * head_blocks_of(hq, hkv);
+  return std::max(kCounterArea, align256(units * sizeof(uint32_t)));
 }
 
 size_t tp_decode_workspace_bytes(int64_t batch, int32_t hq, int32_t hkv, int32_t n_pages,
@@ -942,7 +938,7 @@ int32_t tp_fused_qk(const void* q, int64_t batch, int32_t hq, int32_t hkv,
                     const tp_page_layout* layout, const tp_pages* pages, int32_t n_pages, float scale,
                     void* scores, void* stream) {
   clear_error();
-  AttnArgs a;
+  AttnArgs a{};
   if (!fill_common(a, q, batch, hq, hkv, layout, pages, n_pages, false)) return TP_ERR_INVALID;
   if (n_pages == 0) return TP_OK;
   if (!scores || ((uintptr_t)scores & 7u)) {
@@ -968,7 +964,7 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
                             int32_t pages_per_split, void* workspace, size_t workspace_bytes,
                             void* out, void* stream) {
   clear_error();
-  AttnArgs a;
+  AttnArgs a{};
   if (!fill_common(a, q, batch, hq, hkv, layout, pages, n_pages, true)) return TP_ERR_INVALID;
   if (!out || ((uintptr_t)out & 15u)) {
     set_error("out must be a non-NULL 16-byte aligned buffer");
@@ -994,9 +990,9 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
   }
   if (pages_per_split <= 0) pages_per_split = tp_default_pages_per_split(batch, hq, hkv, n_pages);
   const int32_t n_splits = n_splits_of(n_pages, pages_per_split);
-  // The combine keeps a (weight, l) pair per split and head of a head block in LDS.
-  if ((int64_t)n_splits * std::min(16, hq / hkv) > kMaxSplitHeads) {
-    set_error("too many splits (%d) for %d query heads per kv head; raise pages_per_split", n_splits, hq / hkv);
+  const int64_t n_groups = (int64_t)n_splits * batch * hkv * a.head_blocks;
+  if (n_groups > INT32_MAX) {
+    set_error("%lld workgroups exceed the grid limit; raise pages_per_split", (long long)n_groups);
     return TP_ERR_INVALID;
   }
   a.out = static_cast<uint16_t*>(out);
@@ -1018,12 +1014,13 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
     const size_t units = (size_t)batch * hkv * a.head_blocks;
     char* ws = static_cast<char*>(workspace);
     a.counters = reinterpret_cast<uint32_t*>(ws);
+    a.counter_stride = counter_stride_of((int64_t)units);
     ws += tp_decode_counter_bytes(batch, hq, hkv);
     a.part_ml = reinterpret_cast<float*>(ws);
     ws += align256(units * 16 * (((size_t)n_splits + 1) & ~(size_t)1) * 2 * sizeof(float));
     a.part_acc = reinterpret_cast<float*>(ws);
   }
-  const dim3 grid((unsigned)(n_splits * batch * hkv * a.head_blocks));
+  const dim3 grid((unsigned)n_groups);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (n_pages > 0 ? layout_kind(layout) : (int)kKindGeneric) {
     case kKindDefault:
