@@ -46,6 +46,41 @@ def algorithmic_bytes(hq, hkv, n_pages, layout, tail=0):
     return hkv * n_pages * 64 * (kb + 136) + hkv * n_pages * rs + hkv * tail * 512 + hq * 128 * 2 * 2
 
 
+def workload_name(args):
+    shape = {(32, 8): ("llama3-8b-shape", "configs[2]"), (64, 8): ("llama3-70b-shape", "configs[4]")}
+    name, cfg = shape.get((args.hq, args.hkv), (f"{args.hq}q/{args.hkv}kv", "not a BASELINE config"))
+    if (args.hq, args.hkv, args.context) == (32, 8, 4096):
+        name, cfg = "llama3.2-1b-shape", "configs[0]"
+    return f"{name} single-layer decode attention, {args.context} ctx, K {args.kind} (BASELINE {cfg})"
+
+
+def synthetic_k(kind, hkv, tokens, g, dev):
+    """K of the BASELINE configs, fp32 ``[1, hkv, tokens, 128]``: ``outlier``
+    N(0,1) with 4 channels x20 per head; ``loguniform`` N(0,1) x
+    per-channel scales log-uniform in [0.25, 4]; ``studentt``
+    t(3) x per-channel scales log-uniform in [0.1, 10] (configs[4]);
+    ``normal`` N(0,1) (configs[0], [3])."""
+    import torch
+
+    k = torch.randn((1, hkv, tokens, 128), generator=g, device=dev, dtype=torch.float32)
+    if kind == "outlier":
+        for h in range(hkv):
+            ch = torch.randperm(128, generator=g, device=dev)[:4]
+            k[:, h, :, ch] *= 20.0
+    elif kind in ("loguniform", "studentt"):
+        lo, hi = (0.25, 4.0) if kind == "loguniform" else (0.1, 10.0)
+        u = torch.rand((1, hkv, 1, 128), generator=g, device=dev)
+        c = torch.exp(np.log(lo) + u * (np.log(hi) - np.log(lo)))
+        if kind == "studentt":
+            # t(3) = N(0,1) / sqrt(chi2(3) / 3), chi2(3) a sum of three squared normals
+            chi2 = sum(torch.randn(k.shape, generator=g, device=dev) ** 2 for _ in range(3))
+            k = k / torch.sqrt(chi2 / 3.0)
+        k = k * c
+    elif kind != "normal":
+        raise ValueError(kind)
+    return k
+
+
 def build_caches(args, dev, layout):
     import torch
 
@@ -56,12 +91,10 @@ def build_caches(args, dev, layout):
     cfg = TurboPolarConfig(num_q_heads=args.hq, num_kv_heads=args.hkv, use_int8_radii=int8,
                            k_angle_bits_level1=l1b, k_angle_bits_deep=deepb, split_dim=split)
     caches = []
+    kind = getattr(args, "kind", "outlier")
     for r in range(args.rotate):
         g = torch.Generator(device=dev).manual_seed(1000 + r)
-        k = torch.randn((1, args.hkv, args.context, 128), generator=g, device=dev, dtype=torch.float32)
-        for h in range(args.hkv):
-            ch = torch.randperm(128, generator=g, device=dev)[:4]
-            k[:, h, :, ch] *= 20.0
+        k = synthetic_k(kind, args.hkv, args.context, g, dev)
         v = torch.randn((1, args.hkv, args.context, 128), generator=g, device=dev, dtype=torch.float32)
         rt = TurboPolarKVCacheRuntime(cfg)
         rt.append(k.half(), v.half())
@@ -167,6 +200,78 @@ def cpu_baseline(args, layout, caches, budget_s):
     gpu = c["out"].float().cpu().numpy()
     err = float(np.max(np.abs(gpu - out)))
     return float(np.median(times)) * 1e6, len(times), err
+
+
+def run_layers(args, layout) -> dict:
+    """one decode query per layer over ``args.layers``
+    layer caches of ``args.context`` tokens each (K log-uniform per channel);
+    a step launches every layer once, in order, on one stream.  With
+    ``args.graph`` the step's launches are captured once into a HIP graph and a
+    step is one replay."""
+    import torch
+
+    from turbopolar_amd import _lib
+    from turbopolar_amd.kernels import fp16_scale
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    args.rotate = args.layers
+    cfg, caches = build_caches(args, dev, layout)
+    L = _lib.lib()
+    n_pages = caches[0]["pages"].S
+    pps = args.pps or int(L.tp_default_pages_per_split(1, args.hq, args.hkv, n_pages))
+    need = int(L.tp_decode_workspace_bytes(1, args.hq, args.hkv, n_pages, 0, pps))
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    scale = fp16_scale(cfg.attention_scale)
+    fn = L.tp_decode_attention
+
+    def step():
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        for c in caches:
+            ps = c["pages"]
+            st = fn(c["q"].data_ptr(), 1, args.hq, args.hkv, ctypes.byref(ps.layout), ctypes.byref(ps.pages),
+                    n_pages, None, None, 0, 0, c["seq"], scale, pps, ws.data_ptr(), need, c["out"].data_ptr(), stream)
+            if st:
+                _lib.check(st, "tp_decode_attention")
+
+    step()
+    torch.cuda.synchronize()
+    eager = [c["out"].clone() for c in caches]
+    run = step
+    graph_equal = None
+    if args.graph:
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            step()
+        run = graph.replay
+        graph_equal = True
+        for _ in range(3):  # replays interleaved with eager work and syncs must all match eager
+            for c in caches:
+                c["out"].zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            graph_equal &= all(torch.equal(c["out"], e) for c, e in zip(caches, eager))
+            step()
+            torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        run()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    ok = all(bool(torch.isfinite(c["out"]).all()) and torch.equal(c["out"], e) for c, e in zip(caches, eager))
+    return {"ms": ms, "pps": pps, "n_pages": n_pages, "outputs_match_first_step": ok, "graph_equal": graph_equal}
 
 
 def run_encode(args, layout) -> dict:
@@ -288,8 +393,13 @@ def main():
     ap.add_argument("--rotate", type=int, default=0, help="independent caches to rotate (0 = auto, >256 MB)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=["decode", "encode", "append"], default="decode",
-                    help="decode (the BASELINE metric, default); encode / append: configs[3] workloads")
+    ap.add_argument("--workload", choices=["decode", "encode", "append", "layers"], default="decode",
+                    help="decode (the BASELINE metric, default); encode / append: configs[3] workloads; "
+                         "layers: configs[1] (--layers decode launches per step)")
+    ap.add_argument("--kind", choices=["outlier", "loguniform", "studentt", "normal"], default=None,
+                    help="K distribution (default: outlier for decode, loguniform for layers)")
+    ap.add_argument("--layers", type=int, default=16)
+    ap.add_argument("--graph", action="store_true", help="layers: replay the step as one HIP graph")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -302,6 +412,31 @@ def main():
     if args.context % 64:
         sys.exit("--context must be a multiple of 64")
     layout = LAYOUTS[args.layout]
+    if args.kind is None:
+        args.kind = "loguniform" if args.workload == "layers" else "outlier"
+    if args.workload == "layers":
+        r = run_layers(args, layout)
+        n_pages = args.context // 64
+        step_bytes = args.layers * algorithmic_bytes(args.hq, args.hkv, n_pages, layout)
+        us = r["ms"] * 1e3
+        gbps = step_bytes / (r["ms"] * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": f"{args.layers}-layer decode-attention µs/step (sum over layers) + achieved HBM GB/s",
+            "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(r["ms"], 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f16", "data": "synthetic",
+            "config": {"workload": f"{args.layers} layers x {args.context} ctx decode, one query per layer "
+                                   f"(BASELINE configs[1])", "layout": args.layout, "q_heads": args.hq,
+                       "kv_heads": args.hkv, "head_dim": 128, "batch": 1, "k_distribution": args.kind,
+                       "pages_per_split": r["pps"], "hip_graph": bool(args.graph),
+                       "algorithmic_bytes_per_step": step_bytes},
+            "tokens_per_s": round(1e6 / us, 1), "us_per_layer": round(us / args.layers, 3),
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+            "checks": {"outputs_match_first_step": r["outputs_match_first_step"],
+                       "graph_replays_match_eager": r["graph_equal"]},
+        }))
+        return
     if args.workload == "encode":
         r = run_encode(args, layout)
         nbytes = r["read"] + r["write"]
@@ -365,7 +500,7 @@ def main():
         "dtype": "f16",
         "data": "synthetic",
         "config": {
-            "workload": f"llama3-8b-shape single-layer decode attention, {args.context} ctx (BASELINE configs[2])",
+            "workload": workload_name(args),
             "layout": args.layout,
             "q_heads": args.hq,
             "kv_heads": args.hkv,

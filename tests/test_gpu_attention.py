@@ -8,6 +8,8 @@ relative L2 <= 1e-3; fused QK scores (fp16 out) max-abs <= 1e-2 and cosine
 >= 0.999 (tests/benchmarks/test_turbo_polar_kernel_qk.py:57-58 of the reference).
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -151,6 +153,80 @@ def test_north_star_shape_32k(device, layout_name, kind, qscale):
     check(out, oracle_out(host, tk, tv, q, S * PAGE), "32k")
 
 
+def test_config1_shape(device):
+    """Llama-3.2-1B shape (32 q / 8 kv heads), 4096 tokens =
+    64 pages, K, V and q ~ N(0,1) from seed 0, every token visible."""
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], 32, 8, 64, 0, seed=0)
+    out = run_gpu(device, block, qv, tk, tv, q, 64 * PAGE)
+    check(out, oracle_out(host, tk, tv, q, 64 * PAGE), "config 1")
+
+
+@pytest.mark.parametrize("layout_name", ["default", "fast"])
+def test_nonfinite_radii_propagate_like_reference(device, layout_name):
+    """Config 5's K (Student-t(3) x per-channel scales up to 10) overflows the
+    fp16 x*x of some pairs, so those radii are +inf (fast layout: the page
+    scale is inf and the page's codes decode to NaN).  The reference's CPU
+    path then gives NaN for every query head whose scores meet +inf or NaN and
+    a finite output where the inf radii only produce -inf scores.  The kernel
+    must reproduce exactly which outputs are NaN or +-inf, and the finite ones
+    within tolerance, with and without the split-K combine."""
+    hq, hkv, S, tail = 64, 8, 8, 5
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS[layout_name], hq, hkv, S, tail, seed=2,
+                                            kind="studentt", qscale=1.0 / np.sqrt(128.0))
+    seq = S * PAGE + tail
+    rad = host["radii"] if layout_name == "default" else host["radii_scales"].reshape(1, hkv, S)
+    hit = [h for h in range(hkv) if not np.all(np.isfinite(rad[0, h].astype(np.float32)))]
+    assert hit and len(hit) < hkv, f"case must mix affected and clean kv heads, got {hit}"
+    ref = oracle_out(host, tk, tv, q, seq)
+    for pps in (0, 1):
+        out = run_gpu(device, block, qv, tk, tv, q, seq, pps=pps)
+        nan_heads = sorted({int(h) for h in np.nonzero(np.isnan(ref))[1]})
+        print(f"[attn-nonfinite] {layout_name} pps={pps} kv heads with inf radii {hit}, "
+              f"NaN query heads {nan_heads}", flush=True)
+        assert np.array_equal(np.isnan(out), np.isnan(ref)), "NaN positions differ"
+        assert np.array_equal(np.isposinf(out), np.isposinf(ref)), "+inf positions differ"
+        assert np.array_equal(np.isneginf(out), np.isneginf(ref)), "-inf positions differ"
+        fin = np.isfinite(ref)
+        assert fin.any() and (~fin).any()
+        check(out[fin], ref[fin], f"{layout_name} finite outputs")
+
+
+@pytest.mark.parametrize("pps", [0, 1])
+def test_page_of_minus_inf_scores_weighs_zero(device, pps):
+    """Every token of page 1 of kv head 0 has pair 0 = (-300, 0): its radius
+    overflows to +inf and its angle decodes to pi, so K-hat starts (-inf,
+    -inf) and query heads with q0, q1 > 0 score -inf on the whole page.  The
+    reference's softmax gives those tokens weight 0 and a finite output from
+    the other pages; a page whose every score is -inf must not turn the
+    running state into NaN."""
+    from turbopolar_amd.payload import PolarKeyBlock, QuantizedVBlock
+
+    hq, hkv, S, tail = 8, 2, 4, 0
+    k, v = gen_kv(77, 1, hkv, S * PAGE, "normal", np.float16)
+    k[0, 0, PAGE:2 * PAGE, 0] = -300.0
+    k[0, 0, PAGE:2 * PAGE, 1] = 0.0
+    q = gen_q(77, 1, hq)
+    q[0, :2, 0:2] = np.float16(0.5)  # heads 0, 1: q0, q1 > 0 -> -inf scores on page 1
+    q[0, 2, 0], q[0, 2, 1] = np.float16(0.5), np.float16(-0.5)  # head 2: -inf + inf -> NaN scores
+    layout = LAYOUTS["default"]
+    host = encode_gpu(k, v, layout, device)
+    meta = oracle.encode_block(k[:, :, :PAGE], l1_bits=layout[1], deep_bits=layout[2], split_dim=layout[3],
+                               use_int8_radii=layout[0])["metadata"]
+    host["metadata"] = meta
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    block = PolarKeyBlock(radii=t(host["radii"]), angle_codes_l1=t(host["angle_codes_l1"]),
+                          angle_codes_deep=t(host["angle_codes_deep"]), shape=(1, hkv, S * PAGE, 128),
+                          block_size=PAGE, head_dim=128, metadata=meta, radii_scales=None)
+    qv = QuantizedVBlock(codes=t(host["v_codes"]), scales=t(host["v_scales"]), group_size=32)
+    empty = np.zeros((1, hkv, 0, 128), np.float16)
+    ref = oracle_out(host, empty, empty, q, S * PAGE)
+    assert np.all(np.isfinite(ref[0, :2])) and np.all(np.isnan(ref[0, 2])), "case does not exercise -inf / NaN"
+    out = run_gpu(device, block, qv, empty, empty, q, S * PAGE, pps=pps)
+    assert np.array_equal(np.isnan(out), np.isnan(ref)) and np.array_equal(np.isinf(out), np.isinf(ref))
+    fin = np.isfinite(ref)
+    check(out[fin], ref[fin], "-inf page")
+
+
 def test_split_invariance(device):
     """Split-K online softmax equals the one-pass result for every split size."""
     block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], 32, 8, 40, 13, seed=12)
@@ -182,6 +258,57 @@ def test_workspace_shared_across_shapes(device):
         seq = S * PAGE + tail
         out = run_gpu(device, block, qv, tk, tv, q, seq, pps=pps)
         check(out, oracle_out(host, tk, tv, q, seq), f"shape {i}")
+
+
+def test_graph_replay_matches_eager(device):
+    """Three decode launches (6 one-page splits each, so the combine and the
+    ticket reset run inside the graph) captured into one HIP graph: each of
+    three replays, with eager launches and syncs between them, reproduces the
+    eager outputs bit for bit, and the eager outputs match the oracle."""
+    from turbopolar_amd import _lib
+
+    L = _lib.lib()
+    cases = []
+    for seed in (50, 51, 52):
+        block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], 32, 8, 6, 0, seed=seed)
+        cases.append((PageSet(block, qv), torch.from_numpy(q).to(device),
+                      torch.empty((1, 32, 128), dtype=torch.float16, device=device), host, tk, tv, q))
+    seq = 6 * PAGE
+    need = int(L.tp_decode_workspace_bytes(1, 32, 8, 6, 0, 1))
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+
+    def step():
+        stream = torch.cuda.current_stream(device).cuda_stream
+        for ps, qt, out, *_ in cases:
+            st = L.tp_decode_attention(qt.data_ptr(), 1, 32, 8, ctypes.byref(ps.layout), ctypes.byref(ps.pages), 6,
+                                       None, None, 0, 0, seq, SCALE16, 1, ws.data_ptr(), need, out.data_ptr(), stream)
+            assert st == 0, L.tp_last_error()
+
+    step()
+    torch.cuda.synchronize()
+    eager = [c[2].clone() for c in cases]
+    for (ps, qt, out, host, tk, tv, q), e in zip(cases, eager):
+        check(e.float().cpu().numpy(), oracle_out(host, tk, tv, q, seq), "graph eager")
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for rep in range(3):
+        for c in cases:
+            c[2].fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        for c, e in zip(cases, eager):
+            assert torch.equal(c[2], e), f"replay {rep} differs from eager"
+        step()
+        torch.cuda.synchronize()
+        for c, e in zip(cases, eager):
+            assert torch.equal(c[2], e), f"eager launch after replay {rep} differs"
 
 
 def test_page_decode_parity(device):

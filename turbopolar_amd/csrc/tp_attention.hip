@@ -90,12 +90,16 @@ __device__ __forceinline__ half2v hi_hi(uint32_t w) {
   return half2v{r, r};
 }
 
-// (cos, sin) of a code's decoded angle theta = 2*pi*code/(2^bits-1) - pi
-// (decoder.py:37-55), rounded to fp16 and packed.  v_sin_f32 / v_cos_f32 take
-// revolutions, so theta is passed as code/(2^bits-1) - 1/2.
+// (cos, sin) of a code's decoded angle, rounded to fp16 and packed: the
+// reference's fp32 angle (code_angle, decoder.py:37-55) through accurate fp32
+// cosf / sinf.  At half a turn the reference's sin(f32(pi)) is -8.7e-8, whose
+// fp16 rounding -5.96e-8 is not zero, so an inf radius decodes to -inf there
+// as in the reference (decoder.py:57-67); the hardware sine in revolutions
+// returns an exact 0 at half a turn, which would turn that product into NaN.
+// No code of 2, 4 or 8 bits has a cosine or sine that rounds to fp16 zero.
 __device__ __forceinline__ uint32_t make_cs(uint32_t code, int bits) {
-  const float x = (float)code / (float)((1 << bits) - 1) - 0.5f;
-  const half2v cs = {(f16)__builtin_amdgcn_cosf(x), (f16)__builtin_amdgcn_sinf(x)};
+  const float th = code_angle(code, bits);
+  const half2v cs = {(f16)cosf(th), (f16)sinf(th)};
   return pack_h2(cs);
 }
 
@@ -472,16 +476,21 @@ __device__ __forceinline__ void softmax_page(const float4v* s, int valid, float 
   pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
   if (__builtin_amdgcn_ballot_w64(pm > m_run + kLazyRescale)) {
     const float m_new = fmaxf(m_run, pm);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    // From an empty state (m_run = -inf) the factor is 0: l and acc are 0,
+    // or NaN after a page whose scores were all NaN, and NaN must survive.
+    const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
     l_run *= alpha;
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] *= alpha;
     m_run = m_new;
   }
+  // m_run is still -inf only if every score of this page is -inf or NaN: then
+  // -inf scores weigh 0 and NaN scores stay NaN, as in the reference's softmax.
+  const float m_use = m_run == -INFINITY ? 0.0f : m_run;
   float lsum = 0.0f;
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
-    x[k] = __builtin_amdgcn_exp2f(x[k] - m_run);
+    x[k] = __builtin_amdgcn_exp2f(x[k] - m_use);
     lsum += x[k];
   }
   l_run += lsum;
@@ -679,14 +688,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     }
 #pragma unroll
     for (int u = 0; u < WAVES; ++u) M = fmaxf(M, m[u]);
-    if (M != -INFINITY) {
+    // A state with m = -inf weighs 0, so an empty one adds 0 and one that
+    // carries NaN (all of its scores NaN) still makes the fold NaN.
 #pragma unroll
-      for (int u = 0; u < WAVES; ++u) {
-        const float w = m[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[u] - M);
-        L += l[u] * w;
+    for (int u = 0; u < WAVES; ++u) {
+      const float w = m[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[u] - M);
+      L += l[u] * w;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) A[i] += x[u][i] * w;
-      }
+      for (int i = 0; i < 4; ++i) A[i] += x[u][i] * w;
     }
   }
   if (a.n_splits == 1) {
@@ -740,18 +749,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     float Mn = Mc;
 #pragma unroll
     for (int u = 0; u < 8; ++u) Mn = fmaxf(Mn, r[u].x);
-    if (Mn != -INFINITY) {
-      const float w0 = __builtin_amdgcn_exp2f(Mc - Mn);  // 0 while Mc is -inf
-      Lc *= w0;
-      Ac *= w0;
+    // Records and states with m = -inf weigh 0 (NaN they carry survives).
+    const float w0 = Mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mc - Mn);
+    Lc *= w0;
+    Ac *= w0;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float w = r[u].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r[u].x - Mn);
-        Lc += r[u].y * w;
-        Ac += x[u] * w;
-      }
-      Mc = Mn;
+    for (int u = 0; u < 8; ++u) {
+      const float w = r[u].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r[u].x - Mn);
+      Lc += r[u].y * w;
+      Ac += x[u] * w;
     }
+    Mc = Mn;
   }
   if (SG > 1) {
     float4v* red = reinterpret_cast<float4v*>(&sh.acc[0][0]);
@@ -764,16 +772,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     if (sg == 0) {
       float Mx = Mc;
       for (int g2 = 1; g2 < SG; ++g2) Mx = fmaxf(Mx, redml[g2 * n_items + it].x);
-      if (Mx != -INFINITY) {
-        const float w0 = __builtin_amdgcn_exp2f(Mc - Mx);
-        Lc *= w0;
-        Ac *= w0;
-        for (int g2 = 1; g2 < SG; ++g2) {
-          const float2 r = redml[g2 * n_items + it];
-          const float w = r.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r.x - Mx);
-          Lc += r.y * w;
-          Ac += red[g2 * n_items + it] * w;
-        }
+      const float w0 = Mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mc - Mx);
+      Lc *= w0;
+      Ac *= w0;
+      for (int g2 = 1; g2 < SG; ++g2) {
+        const float2 r = redml[g2 * n_items + it];
+        const float w = r.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r.x - Mx);
+        Lc += r.y * w;
+        Ac += red[g2 * n_items + it] * w;
       }
     }
   }
