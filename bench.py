@@ -274,6 +274,65 @@ def run_layers(args, layout) -> dict:
     return {"ms": ms, "pps": pps, "n_pages": n_pages, "outputs_match_first_step": ok, "graph_equal": graph_equal}
 
 
+def run_model(args) -> dict:
+    """§8 f2: decode through a randomly initialised Llama of the configs[1]
+    shape (``args.layers`` layers, ``args.hq`` / ``args.hkv`` heads, head_dim
+    128, float32 weights) with the transformers hook, its caches pre-filled
+    with ``args.context`` synthetic tokens per layer; the same tokens run
+    through the model's own DynamicCache as the dense baseline
+    (run_fast_attention_bench.py:104-121: tokens/s of greedy decode; here the
+    tokens are teacher-forced so both runs see the same inputs)."""
+    import torch
+    from transformers import DynamicCache, LlamaConfig, LlamaForCausalLM
+
+    from turbopolar_amd import llama as tl
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=args.hq * 128, intermediate_size=8192,
+                      num_hidden_layers=args.layers, num_attention_heads=args.hq, num_key_value_heads=args.hkv,
+                      head_dim=128, max_position_embeddings=args.context + 4096, attn_implementation="eager")
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = LlamaForCausalLM(cfg).eval()
+    turbo = tl.make_turbo_cache(model)
+    dense = DynamicCache(config=model.config)
+    g = torch.Generator(device=dev).manual_seed(7)
+    with torch.no_grad():
+        for layer in range(args.layers):
+            k = synthetic_k("loguniform", args.hkv, args.context, g, dev).half()
+            v = torch.randn(k.shape, generator=g, device=dev).half()
+            turbo.fast(layer).runtime.append(k, v)
+            dense.update(k.float(), v.float(), layer)
+            del k, v
+    tokens = torch.randint(0, cfg.vocab_size, (1, args.warmup + args.steps), generator=g, device=dev)
+    res = {}
+    logits = {}
+    for name, cache in (("dense", dense), ("turbo", turbo)):
+        if name == "turbo":
+            tl.patch_llama_attention(model)
+        try:
+            with torch.no_grad():
+                outs = []
+                for i in range(args.warmup):
+                    model(tokens[:, i:i + 1], past_key_values=cache, use_cache=True)
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for i in range(args.warmup, args.warmup + args.steps):
+                    outs.append(model(tokens[:, i:i + 1], past_key_values=cache, use_cache=True).logits[0, -1])
+                torch.cuda.synchronize()
+                res[name] = (time.perf_counter() - t0) / args.steps
+                logits[name] = torch.stack(outs).double()
+        finally:
+            tl.unpatch_llama_attention(model)
+    a, b = logits["turbo"], logits["dense"]
+    cos = torch.nn.functional.cosine_similarity(a, b, dim=-1)
+    top1 = (a.argmax(-1) == b.argmax(-1)).double().mean()
+    return {"turbo_s": res["turbo"], "dense_s": res["dense"], "cos_min": float(cos.min()), "top1": float(top1),
+            "turbo_bytes": int(turbo.nbytes), "dense_bytes": int(sum(x.numel() * x.element_size() for x in (
+                *[layer.keys for layer in dense.layers], *[layer.values for layer in dense.layers])))}
+
+
 def run_encode(args, layout) -> dict:
     """Bulk prefill (workload 1): one tp_encode_pages launch
     encodes ``context`` fp16 tokens of ``hkv`` kv heads into pages.  Input and
@@ -393,9 +452,10 @@ def main():
     ap.add_argument("--rotate", type=int, default=0, help="independent caches to rotate (0 = auto, >256 MB)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=["decode", "encode", "append", "layers"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "encode", "append", "layers", "model"], default="decode",
                     help="decode (the BASELINE metric, default); encode / append: configs[3] workloads; "
-                         "layers: configs[1] (--layers decode launches per step)")
+                         "layers: configs[1] (--layers decode launches per step); "
+                         "model: a configs[1]-shape Llama decoding through the transformers hook")
     ap.add_argument("--kind", choices=["outlier", "loguniform", "studentt", "normal"], default=None,
                     help="K distribution (default: outlier for decode, loguniform for layers)")
     ap.add_argument("--layers", type=int, default=16)
@@ -414,6 +474,23 @@ def main():
     layout = LAYOUTS[args.layout]
     if args.kind is None:
         args.kind = "loguniform" if args.workload == "layers" else "outlier"
+    if args.workload == "model":
+        r = run_model(args)
+        print(json.dumps({
+            "metric": "Llama decode tokens/s through the transformers hook (fused decode attention)",
+            "value": round(1.0 / r["turbo_s"], 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(r["turbo_s"] * 1e3, 3), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32 weights, f16 cache", "data": "synthetic",
+            "config": {"workload": f"random-init Llama, {args.layers} layers, {args.hq} q / {args.hkv} kv heads, "
+                                   f"head_dim 128, {args.context} cached tokens per layer (BASELINE configs[1] "
+                                   f"shape), teacher-forced single-token decode", "layout": "fast (make_turbo_caches)"},
+            "dense_baseline": {"tokens_per_s": round(1.0 / r["dense_s"], 2), "ms_per_token": round(r["dense_s"] * 1e3, 3),
+                               "kv_bytes": r["dense_bytes"], "note": "the model's own DynamicCache (the same fp16 "
+                                                                      "K/V values held as fp32), eager attention"},
+            "turbo_kv_bytes": r["turbo_bytes"],
+            "checks": {"logit_cosine_min_vs_dense": round(r["cos_min"], 6), "top1_agreement_vs_dense": r["top1"]},
+        }))
+        return
     if args.workload == "layers":
         r = run_layers(args, layout)
         n_pages = args.context // 64

@@ -1,0 +1,183 @@
+"""PyTorch Llama integration of the fused decode path.
+
+Mirrors the reference's mlx_lm hook (benchmarks/turbopolar_fast_attention.py:
+232-298: ``_is_standard_causal_mask``, ``_turbo_attention_call``,
+``patch_llama_attention``, ``unpatch_llama_attention``) for Hugging Face
+``transformers`` Llama models:
+
+* ``TurboPolarCache`` is a ``transformers`` ``Cache`` whose layers are
+  ``TurboPolarFastCache`` objects (one per decoder layer), so the model sees the
+  cached length (positions, masks) as with its own caches.  Its ``update`` is
+  the prefill path: append, then decompress on read
+  (``TurboPolarFastCache.update_and_fetch``), followed by the model's own
+  attention over the decompressed history, as mlx_lm does with the
+  reference's cache.
+* ``patch_llama_attention`` swaps ``LlamaAttention.forward`` for one that sends
+  single-token decode steps with a standard causal mask through
+  ``TurboPolarFastCache.decode_attention`` (the fused HIP kernel over the
+  compressed pages) and everything else through the original forward.
+
+The model's weights are untouched; any Llama checkpoint loaded from a local
+path works, and tests use randomly initialised models.
+"""
+
+from __future__ import annotations
+
+from typing import List, Optional, Sequence
+
+import torch
+
+from .config import TurboPolarConfig
+from .fast_attention import TurboPolarFastCache, make_turbo_caches
+
+try:  # transformers is an optional dependency of this module only
+    from transformers.cache_utils import Cache, CacheLayerMixin
+    from transformers.models.llama import modeling_llama as _llama
+except ImportError as exc:  # pragma: no cover - exercised only without transformers
+    raise ImportError("turbopolar_amd.llama needs the transformers package") from exc
+
+__all__ = [
+    "TurboPolarCache",
+    "TurboPolarLayer",
+    "make_turbo_cache",
+    "patch_llama_attention",
+    "unpatch_llama_attention",
+    "is_patched",
+]
+
+
+class TurboPolarLayer(CacheLayerMixin):
+    """One decoder layer's cache: a ``TurboPolarFastCache``."""
+
+    is_compileable = False
+    is_sliding = False
+
+    def __init__(self, fast: TurboPolarFastCache):
+        super().__init__()
+        self.fast = fast
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        self.is_initialized = True
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs):
+        """Prefill path: append and return the decompressed history (K, V)."""
+        self.is_initialized = True
+        return self.fast.update_and_fetch(key_states, value_states)
+
+    def get_mask_sizes(self, query_length: int) -> tuple:
+        # Called before the new tokens are appended: the keys the queries see are
+        # the cached ones plus themselves, starting at position 0.
+        return self.fast.offset + query_length, 0
+
+    def get_seq_length(self) -> int:
+        return self.fast.offset
+
+    def get_max_length(self) -> int:
+        return -1
+
+    def reset(self) -> None:
+        self.fast = TurboPolarFastCache(self.fast.config)
+        self.is_initialized = False
+
+
+class TurboPolarCache(Cache):
+    """``transformers`` cache over one ``TurboPolarFastCache`` per decoder layer."""
+
+    def __init__(self, fast_caches: Sequence[TurboPolarFastCache]):
+        super().__init__(layers=[TurboPolarLayer(c) for c in fast_caches])
+
+    def fast(self, layer_idx: int) -> TurboPolarFastCache:
+        return self.layers[layer_idx].fast
+
+    @property
+    def nbytes(self) -> int:
+        return sum(layer.fast.nbytes for layer in self.layers)
+
+
+def make_turbo_cache(model, config: Optional[TurboPolarConfig] = None) -> TurboPolarCache:
+    """A ``TurboPolarCache`` sized for ``model``: the reference's fast layout
+    (``make_turbo_caches``, turbopolar_fast_attention.py:207-229) unless a
+    ``TurboPolarConfig`` is given."""
+    cfg = model.config
+    n_layers = cfg.num_hidden_layers
+    n_heads = cfg.num_attention_heads
+    n_kv = getattr(cfg, "num_key_value_heads", None) or n_heads
+    head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // n_heads
+    if config is None:
+        return TurboPolarCache(make_turbo_caches(n_layers, n_heads, n_kv, head_dim))
+    return TurboPolarCache([TurboPolarFastCache(config) for _ in range(n_layers)])
+
+
+def _is_standard_causal_mask(mask: Optional[torch.Tensor], seq_len: int, cache_len: int) -> bool:
+    """True for no mask or the full-history causal mask ``[1, 1, seq_len, cache_len]``
+    (turbopolar_fast_attention.py:235-244), boolean (True = attend) or additive
+    (0 = attend).  Query i (at position cache_len - seq_len + i) sees keys
+    0 .. cache_len - seq_len + i."""
+    if mask is None:
+        return True
+    if tuple(mask.shape) != (1, 1, seq_len, cache_len):
+        return False
+    allowed = mask[0, 0] if mask.dtype == torch.bool else mask[0, 0] == 0
+    expected = torch.ones((seq_len, cache_len), dtype=torch.bool, device=mask.device).tril(cache_len - seq_len)
+    return bool(torch.equal(allowed, expected))
+
+
+_orig_llama_attention_forward = None
+
+
+def _turbo_llama_attention_forward(
+    self,
+    hidden_states: torch.Tensor,
+    position_embeddings=None,
+    attention_mask: Optional[torch.Tensor] = None,
+    past_key_values=None,
+    **kwargs,
+):
+    """``_turbo_attention_call`` (turbopolar_fast_attention.py:247-280) for
+    ``transformers``' ``LlamaAttention``: a single-token step on a
+    ``TurboPolarCache`` runs the fused decode kernel; anything else runs the
+    original forward (prefill appends and decompresses through the cache)."""
+    if isinstance(past_key_values, TurboPolarCache) and hidden_states.shape[1] == 1:
+        fast = past_key_values.fast(self.layer_idx)
+        B, L, _ = hidden_states.shape
+        q = self.q_proj(hidden_states).view(B, L, -1, self.head_dim).transpose(1, 2)
+        k = self.k_proj(hidden_states).view(B, L, -1, self.head_dim).transpose(1, 2)
+        v = self.v_proj(hidden_states).view(B, L, -1, self.head_dim).transpose(1, 2)
+        if q.shape[1] % k.shape[1] != 0:
+            raise ValueError("TurboPolar fused decode requires GQA ratio to divide evenly.")
+        if not _is_standard_causal_mask(attention_mask, L, fast.offset + L):
+            raise NotImplementedError("TurboPolar fused decode only supports standard causal full-history masks.")
+        cos, sin = position_embeddings
+        q, k = _llama.apply_rotary_pos_emb(q, k, cos, sin)
+        out = fast.decode_attention(q, k, v, self.scaling)  # [B, H_q, D] fp16
+        out = out.to(hidden_states.dtype).reshape(B, L, -1)
+        return self.o_proj(out), None
+    return _orig_llama_attention_forward(
+        self, hidden_states, position_embeddings, attention_mask, past_key_values, **kwargs
+    )
+
+
+def patch_llama_attention(model=None) -> None:
+    """Route Llama decode steps on a ``TurboPolarCache`` through the fused kernel
+    (turbopolar_fast_attention.py:283-290).  Patches the class, like the
+    reference; ``model`` is accepted for the same signature."""
+    global _orig_llama_attention_forward
+    if _orig_llama_attention_forward is None:
+        _orig_llama_attention_forward = _llama.LlamaAttention.forward
+    _llama.LlamaAttention.forward = _turbo_llama_attention_forward
+
+
+def unpatch_llama_attention(model=None) -> None:
+    """Restore the original forward (turbopolar_fast_attention.py:293-298)."""
+    global _orig_llama_attention_forward
+    if _orig_llama_attention_forward is not None:
+        _llama.LlamaAttention.forward = _orig_llama_attention_forward
+        _orig_llama_attention_forward = None
+
+
+def is_patched() -> bool:
+    return _llama.LlamaAttention.forward is _turbo_llama_attention_forward
+
+
+def caches_of(cache: TurboPolarCache) -> List[TurboPolarFastCache]:
+    return [layer.fast for layer in cache.layers]
