@@ -184,8 +184,9 @@ int32_t tp_selftest_f16_tables(uint16_t* sqrt_out, uint16_t* log_out, uint8_t* c
 
 /* Counts, over x bit patterns [x_begin, x_begin+x_count) and all 65536 y
  * patterns (finite values only), the pairs where the encoder's fast fp16
- * atan2 differs from the float64 reference path.  *mismatches is accumulated
- * (atomic add), so zero it first. */
+ * atan2 differs from the float64 reference path, or where the 4- or 8-bit
+ * angle code of the specialised fp16 encoder differs from the code of the
+ * float64 angle.  *mismatches is accumulated (atomic add), so zero it first. */
 int32_t tp_selftest_atan2_exhaustive(unsigned long long* mismatches, int32_t x_begin,
                                      int32_t x_count, void* stream);
 
@@ -195,6 +196,14 @@ int32_t tp_selftest_atan2_exhaustive(unsigned long long* mismatches, int32_t x_b
  * rounded one.  *mismatches is accumulated (atomic add), so zero it first. */
 int32_t tp_selftest_div_f16_exhaustive(unsigned long long* mismatches, int32_t s_begin,
                                        int32_t s_count, void* stream);
+
+/* Counts, over positive finite fp16 scale patterns [s_begin, s_begin+s_count)
+ * and all finite fp16 values, the int8 V codes where the fast encoder's path
+ * (reciprocal-product quotient, biased byte conversion, exact redo near an
+ * fp16 midpoint) differs from int8(clip(rint(fp16(v / s)), -128, 127)).
+ * *mismatches is accumulated (atomic add), so zero it first. */
+int32_t tp_selftest_vcode_exhaustive(unsigned long long* mismatches, int32_t s_begin,
+                                     int32_t s_count, void* stream);
 
 #ifdef __cplusplus
 }

@@ -152,7 +152,9 @@ def test_f16_tables_exhaustive(device):
 
 
 def test_atan2_fast_path_exhaustive(device):
-    """Fast fp32 atan2 + midpoint guard == float64 path for every finite fp16 pair."""
+    """Fast fp32 atan2 + midpoint guard == float64 path, and the specialised
+    encoder's 4- and 8-bit angle codes == the codes of the float64 angle, for
+    every finite fp16 pair."""
     cnt = torch.zeros(1, dtype=torch.int64, device=device)
     step = 4096
     for x0 in range(0, 65536, step):
@@ -172,3 +174,17 @@ def test_v_quotient_fast_path_exhaustive(device):
         _lib.check(st, "selftest div")
     torch.cuda.synchronize()
     assert int(cnt.item()) == 0, f"{int(cnt.item())} (v, s) pairs where the fast quotient differs"
+
+
+def test_v_code_fast_path_exhaustive(device):
+    """The specialised fp16 encoder's V codes (reciprocal-product quotient,
+    biased byte conversion that rounds half to even and saturates, exact redo
+    near an fp16 midpoint) == int8(clip(rint(fp16(v / s)), -128, 127)) for
+    every positive finite fp16 scale and every finite value."""
+    cnt = torch.zeros(1, dtype=torch.int64, device=device)
+    step = 4096
+    for s0 in range(0, 32768, step):
+        st = _lib.lib().tp_selftest_vcode_exhaustive(cnt.data_ptr(), s0, step, torch.cuda.current_stream().cuda_stream)
+        _lib.check(st, "selftest vcode")
+    torch.cuda.synchronize()
+    assert int(cnt.item()) == 0, f"{int(cnt.item())} (v, s) pairs where the fast V code differs"

@@ -86,6 +86,7 @@ _SIGNATURES = {
     "tp_selftest_f16_tables": (c_i32, [c_vp, c_vp, c_vp, c_vp]),
     "tp_selftest_atan2_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
     "tp_selftest_div_f16_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
+    "tp_selftest_vcode_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
 }
 
 _lib = None

@@ -66,6 +66,16 @@ __device__ __forceinline__ uint16_t d2h(double d) {
   return f2h(f);
 }
 
+// True when the fp32 value `v` is within kGuard fp32 ulps of an fp16 rounding
+// midpoint, for a value that only feeds the round-half-even of a code: below
+// the fp16 normal range (|v| < 2^-14) every code candidate rounds to 0, so no
+// subnormal test is needed.  ((u - 0x1000 + kGuard) mod 2^13) <= 2 kGuard is
+// |low 13 bits - 0x1000| <= kGuard.
+template <int kGuard>
+__device__ __forceinline__ bool near_f16_midpoint_code(float v) {
+  return ((__float_as_uint(v) + (uint32_t)(kGuard - 0x1000)) & 0x1fffu) <= (uint32_t)(2 * kGuard);
+}
+
 // True when the fp32 value `v` is too close to an fp16 rounding boundary (or in
 // the fp16 subnormal range) for its rounding to be trusted.
 template <int kGuard>
@@ -87,7 +97,8 @@ __device__ __forceinline__ float atan2_poly(float y, float x) {
   const float ay = fabsf(y);
   const float mx = fmaxf(ax, ay);
   const float mn = fminf(ax, ay);
-  const float t = mx == 0.0f ? 0.0f : mn * __builtin_amdgcn_rcpf(mx);
+  // mx >= 2^-24 for any non-zero fp16 input; for x = y = 0 the clamp keeps t = 0.
+  const float t = mn * __builtin_amdgcn_rcpf(fmaxf(mx, 0x1p-30f));
   const float u = t * t;
   float p = -0.0017539079999551177f;
   p = __builtin_fmaf(p, u, 0.010726844891905785f);
@@ -179,12 +190,13 @@ __device__ __forceinline__ uint16_t radius_f32_in(float x, float y) {
 // encoder.py:47-55 for an fp16 angle: fp16 shift and divide, clip, then the
 // float32 product with (2^bits - 1) rounded half-even.
 __device__ __forceinline__ uint32_t angle_code_f16(uint16_t a16, int bits) {
-  float n = h2f(f2h(h2f(a16) + h2f(kF16Pi)));
-  n = div_f16(n, h2f(kF16TwoPi), kF32InvF16TwoPi);
-  n = fminf(fmaxf(n, 0.0f), 1.0f);
-  const float lv = (float)((1 << bits) - 1);
-  const float c = rintf(n * lv);
-  return (uint32_t)fminf(fmaxf(c, 0.0f), lv);
+  const float s1 = h2f(f2h(h2f(a16) + h2f(kF16Pi)));
+  const float q = s1 * kF32InvF16TwoPi;
+  const float n16 = near_f16_midpoint_code<kGuardDiv>(q) ? h2f(f2h(s1 / h2f(kF16TwoPi))) : h2f(f2h(q));
+  const float n = fminf(fmaxf(n16, 0.0f), 1.0f);  // NaN -> 0
+  // n * (2^bits - 1) lies in [0, 2^bits - 1]: the byte conversion rounds half
+  // to even (the reference's mx.round) and saturation never triggers.
+  return __builtin_amdgcn_cvt_pk_u8_f32(n * (float)((1 << bits) - 1), 0u, 0u);
 }
 
 // encoder.py:47-55 for an fp32 angle: fp32 ops, and the near-one wrap to 0.

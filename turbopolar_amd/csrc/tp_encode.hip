@@ -250,6 +250,265 @@ __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
   }
 }
 
+// ---- fp16 fast path for the runtime's two layouts ----------------------------
+//
+// encode_pages_kernel serves every layout and input type.  fp16 input in the
+// default layout (4-bit l1 and deep angles, split_dim 64, fp16 radii) or the
+// fast layout (8-bit deep angles, split_dim 0, int8 log radii) takes this
+// kernel instead: the code widths and the pair -> row mapping are compile-time
+// constants, each thread packs its 16 codes in registers and stores them
+// directly (thread q of a token owns pairs [16q, 16q+16), which are bytes
+// [8q, 8q+8) of the token's l1 / deep rows in the default layout and bytes
+// [16q, 16q+16) of its deep row in the fast layout), and the byte conversion
+// v_cvt_pk_u8_f32 rounds half to even, saturates and places the byte in one
+// instruction.  Every fp32 step whose fp16 rounding is in doubt only sets a
+// per-lane flag; flagged pairs and value groups are redone exactly after the
+// main loop, so the output is bit-identical to encode_pages_kernel's.
+
+constexpr int kEncDefault = 0;
+constexpr int kEncFast = 1;
+
+// fp16 (a16 + pi) as fp32, the numerator of the angle code (encoder.py:46-50).
+__device__ __forceinline__ float code_numerator(uint16_t a16) { return h2f(f2h(h2f(a16) + h2f(kF16Pi))); }
+
+// Code of an angle numerator from its fp16 quotient n16 (clamped, NaN -> 0).
+template <int kBits>
+__device__ __forceinline__ float code_arg(float n16) {
+  return fminf(fmaxf(n16, 0.0f), 1.0f) * (float)((1 << kBits) - 1);
+}
+
+// The fast path's angle code of pair (x, y), as the argument of the byte
+// conversion, and whether it cannot be trusted: the fp32 atan2 or the fp32
+// quotient lies near an fp16 rounding midpoint.  An angle below 2^-14 leaves
+// fp16(a + pi) = fp16(pi) whichever way it rounds, so neither guard needs the
+// subnormal test, and atan2(+-0, x >= 0) = +-0 comes out of atan2_poly exactly.
+template <int kBits>
+__device__ __forceinline__ float angle_arg_fast(float x, float y, bool* flag) {
+  const float a = atan2_poly(y, x);
+  const float q = code_numerator(f2h(a)) * kF32InvF16TwoPi;
+  *flag = near_f16_midpoint_code<kGuardAtan2>(a) | near_f16_midpoint_code<kGuardDiv>(q);
+  return code_arg<kBits>(h2f(f2h(q)));
+}
+
+// Exact angle code of pair (x, y): correctly rounded fp16 atan2, except that
+// the float64 atan2 runs only when the two fp16 candidates around the fast
+// result's rounding midpoint give different codes.
+template <int kBits>
+__device__ __forceinline__ uint32_t exact_angle_code(float y, float x) {
+  bool exact;
+  const uint16_t a16 = atan2_f16_fast(y, x, &exact);
+  const uint32_t c0 = angle_code_f16(a16, kBits);
+  if (exact) return c0;
+  // The fast fp32 angle lies within kGuardAtan2 ulps of the midpoint between
+  // a16 and the neighbour on its side; the correctly rounded value is one of
+  // the two.
+  const float a = atan2_poly(y, x);
+  const float d = a - h2f(a16);
+  const uint16_t nb = (uint16_t)(a16 + ((d > 0.0f) == !(a16 & 0x8000u) ? 1 : -1));
+  if ((a16 & 0x7fffu) == 0 || angle_code_f16(nb, kBits) != c0) return angle_code_f16(atan2_f16_slow(y, x), kBits);
+  return c0;
+}
+
+// Biased byte (code + 128) of value v with scale s = 1/rs by the fast path,
+// written into byte `sel` of `old`, and whether the fp32 quotient is too close
+// to an fp16 midpoint to trust.
+__device__ __forceinline__ uint32_t vcode_fast_byte(float v, float rs, uint32_t sel, uint32_t old, bool* near) {
+  const float q = v * rs;
+  *near = near_f16_midpoint_code<kGuardDiv>(q);
+  return __builtin_amdgcn_cvt_pk_u8_f32(h2f(f2h(q)) + 128.0f, sel, old);
+}
+// The same byte from the correctly rounded quotient, NaN -> code 0.
+__device__ __forceinline__ uint32_t vcode_exact_byte(float v, float s) {
+  const float qn = h2f(f2h(v / s));
+  return __builtin_amdgcn_cvt_pk_u8_f32((qn == qn ? qn : 0.0f) + 128.0f, 0u, 0u);
+}
+
+template <int L>
+__global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
+  constexpr bool kFastLayout = L == kEncFast;
+  constexpr int kBits = kFastLayout ? 8 : 4;
+  __shared__ float s_max[4];
+
+  const int page = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int t = tid >> 2;
+  const int qq = tid & 3;
+  const int64_t local_tok = (int64_t)page * kPageTokens + t;
+  const bool valid = local_tok < a.n_tokens;
+  const int64_t in_off = (bh * a.in_tokens + a.token_begin + local_tok) * kHeadDim + 32 * qq;
+  const int64_t slot = bh * a.capacity + a.page_begin + page;
+  const int64_t row = slot * kPageTokens + t;
+
+  RawRow32<false> kraw;
+  load_row32<false>(a.k, in_off, valid, kraw);
+  uint16_t r16[16];
+  float ss16[16];  // fp16 x*x + y*y, kept for an exact sqrt
+  uint32_t cw[kFastLayout ? 4 : 2];
+#pragma unroll
+  for (int i = 0; i < (kFastLayout ? 4 : 2); ++i) cw[i] = 0u;
+  uint32_t fixr = 0;  // pairs whose radius the fast path cannot vouch for
+  uint32_t fixa = 0;  // pairs whose angle code the fast path cannot vouch for
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t w = raw_word(kraw, j);
+    const half2v xy = __builtin_bit_cast(half2v, w);
+    const half2v sq = xy * xy;  // fp16 products, as the reference squares in fp16 (no FMA)
+    const float ss = (float)(f16)(sq[0] + sq[1]);
+    ss16[j] = ss;
+    const float r = __builtin_amdgcn_sqrtf(ss);
+    fixr |= ((r != 0.0f) & near_f16_midpoint<kGuardSqrt>(r)) ? (1u << j) : 0u;
+    r16[j] = f2h(r);
+    bool flag;
+    const float arg = angle_arg_fast<kBits>((float)xy[0], (float)xy[1], &flag);
+    fixa |= flag ? (1u << j) : 0u;
+    if constexpr (kFastLayout) {
+      cw[j >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(arg, (uint32_t)(j & 3), cw[j >> 2]);
+    } else {
+      cw[j >> 3] |= __builtin_amdgcn_cvt_pk_u8_f32(arg, 0u, 0u) << (4 * (j & 7));
+    }
+  }
+  // Exact redo of the flagged radii and codes (padding tokens are never flagged).
+  while (fixr) {
+    const int j = __builtin_ctz(fixr);
+    fixr &= fixr - 1u;
+    float ss = 0.0f;
+#pragma unroll
+    for (int k2 = 0; k2 < 16; ++k2) ss = k2 == j ? ss16[k2] : ss;
+    const uint16_t rj = sqrt_f16(ss);
+#pragma unroll
+    for (int k2 = 0; k2 < 16; ++k2) r16[k2] = k2 == j ? rj : r16[k2];
+  }
+  while (fixa) {
+    const int j = __builtin_ctz(fixa);
+    fixa &= fixa - 1u;
+    uint32_t w = 0;
+#pragma unroll
+    for (int k2 = 0; k2 < 16; ++k2) w = k2 == j ? raw_word(kraw, k2) : w;
+    const uint32_t c = exact_angle_code<kBits>(h2f((uint16_t)(w >> 16)), h2f((uint16_t)(w & 0xffffu)));
+    if constexpr (kFastLayout) {
+      const uint32_t sh = 8u * (uint32_t)(j & 3);
+#pragma unroll
+      for (int k2 = 0; k2 < 4; ++k2)
+        cw[k2] = k2 == (j >> 2) ? (cw[k2] & ~(0xffu << sh)) | (c << sh) : cw[k2];
+    } else {
+      const uint32_t sh = 4u * (uint32_t)(j & 7);
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2)
+        cw[k2] = k2 == (j >> 3) ? (cw[k2] & ~(0xfu << sh)) | (c << sh) : cw[k2];
+    }
+  }
+
+  if constexpr (kFastLayout) {
+    // encoder.py:34-42: lr = f32(f16 log(max(r, fp16(1e-6)))); per-page scale
+    // f16(max|lr| / 127); codes rint(lr / scale).
+    float lr[16];
+    uint32_t lfix = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint16_t rb = r16[j] > kF16RadiusFloor ? r16[j] : kF16RadiusFloor;
+      bool exact;
+      lr[j] = h2f(log_f16_fast(h2f(rb), &exact));
+      lfix |= exact ? 0u : (1u << j);
+    }
+    while (lfix) {
+      const int j = __builtin_ctz(lfix);
+      lfix &= lfix - 1u;
+      uint16_t rb = 0;
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) rb = k2 == j ? r16[k2] : rb;
+      rb = rb > kF16RadiusFloor ? rb : kF16RadiusFloor;
+      const float exact_lr = h2f(log_f16_slow(h2f(rb)));
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) lr[k2] = k2 == j ? exact_lr : lr[k2];
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(lr[j]));
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) s_max[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    const float ls = mx == 0.0f ? 1e-6f : mx;
+    const uint16_t ls16 = f2h(ls / 127.0f);
+    const float lsf = h2f(ls16);
+    uint32_t packed[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t c = (uint32_t)(to_int8_rne(lr[j] / lsf) & 0xff);
+      packed[j >> 2] |= c << (8 * (j & 3));
+    }
+    *reinterpret_cast<uint4*>(static_cast<int8_t*>(a.radii) + row * kPairs + 16 * qq) =
+        make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    if (tid == 0) a.radii_scales[slot] = ls16;
+    *reinterpret_cast<uint4*>(a.angle_deep + row * kPairs + 16 * qq) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+  } else {
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = (uint32_t)r16[2 * i] | ((uint32_t)r16[2 * i + 1] << 16);
+    uint4* dst = reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.radii) + row * kPairs + 16 * qq);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    uint8_t* crow = (qq < 2 ? a.angle_l1 : a.angle_deep) + row * 16 + 8 * (qq & 1);
+    *reinterpret_cast<uint2*>(crow) = make_uint2(cw[0], cw[1]);
+  }
+
+  // Values (v_quant/encoder.py:21-25): s = f16(max|v| / 127) (1e-4 if zero),
+  // code = int8(clip(rint(f16(v / s)), -128, 127)).  The group maximum is an
+  // integer maximum of the |v| bit patterns, which orders finite fp16 values
+  // like fmaxf and exceeds 0x7c00 exactly when the group holds a NaN.
+  RawRow32<false> vraw;
+  load_row32<false>(a.v, in_off, valid, vraw);
+  uint32_t mbits = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t w = raw_word(vraw, i) & 0x7fff7fffu;
+    mbits = max(mbits, max(w & 0xffffu, w >> 16));
+  }
+  // inf or NaN in the group: exact path (v / inf and NaN quotients give code 0).
+  const bool nonfinite = mbits >= 0x7c00u;
+  uint32_t mb = mbits;
+  if (mbits > 0x7c00u) {  // a NaN: the scale comes from the largest non-NaN |v|, as with fmaxf
+    mb = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const uint32_t hb = (raw_word(vraw, i >> 1) >> (16 * (i & 1))) & 0x7fffu;
+      mb = hb <= 0x7c00u ? max(mb, hb) : mb;
+    }
+  }
+  uint16_t s16 = f2h(h2f((uint16_t)mb) / 127.0f);
+  if ((s16 & 0x7fffu) == 0) s16 = kF16VScaleFloor;
+  const float s = h2f(s16);
+  const float rs = __builtin_amdgcn_rcpf(s);
+  uint32_t vw[8];
+  uint32_t vfix = nonfinite ? 0xffffffffu : 0u;  // values whose quotient the fast path cannot vouch for
+#pragma unroll
+  for (int i = 0; i < 8; ++i) vw[i] = 0u;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    bool near;
+    vw[i >> 2] = vcode_fast_byte(raw_val(vraw, i), rs, (uint32_t)(i & 3), vw[i >> 2], &near);
+    vfix |= near ? (1u << i) : 0u;
+  }
+  while (vfix) {  // exact quotients of the flagged values
+    const int i = __builtin_ctz(vfix);
+    vfix &= vfix - 1u;
+    float vi = 0.0f;
+#pragma unroll
+    for (int k2 = 0; k2 < 32; ++k2) vi = k2 == i ? raw_val(vraw, k2) : vi;
+    const uint32_t b = vcode_exact_byte(vi, s);
+    const uint32_t sh = 8u * (uint32_t)(i & 3);
+#pragma unroll
+    for (int k2 = 0; k2 < 8; ++k2) vw[k2] = k2 == (i >> 2) ? (vw[k2] & ~(0xffu << sh)) | (b << sh) : vw[k2];
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) vw[i] ^= 0x80808080u;  // biased bytes -> int8
+  uint4* vdst = reinterpret_cast<uint4*>(a.v_codes + row * kHeadDim + 32 * qq);
+  vdst[0] = make_uint4(vw[0], vw[1], vw[2], vw[3]);
+  vdst[1] = make_uint4(vw[4], vw[5], vw[6], vw[7]);
+  a.v_scales[row * kVGroups + qq] = s16;
+}
+
 // ---- self-test kernels -------------------------------------------------------
 
 __global__ __launch_bounds__(256) void f16_tables_kernel(uint16_t* sqrt_out, uint16_t* log_out,
@@ -275,6 +534,16 @@ __global__ __launch_bounds__(256) void atan2_exhaustive_kernel(unsigned long lon
     const uint16_t fast = atan2_f16(y, x);
     const uint16_t ref = d2h(atan2((double)y, (double)x));
     bad = fast != ref ? 1u : 0u;
+    // The specialised encoder's codes: the fast path where it vouches for its
+    // result, else exact_angle_code (which skips the float64 atan2 when both
+    // fp16 candidates give one code).
+    bool f4, f8;
+    const float g4 = angle_arg_fast<4>(x, y, &f4);
+    const float g8 = angle_arg_fast<8>(x, y, &f8);
+    const uint32_t c4 = f4 ? exact_angle_code<4>(y, x) : __builtin_amdgcn_cvt_pk_u8_f32(g4, 0u, 0u);
+    const uint32_t c8 = f8 ? exact_angle_code<8>(y, x) : __builtin_amdgcn_cvt_pk_u8_f32(g8, 0u, 0u);
+    bad |= c4 != angle_code_f16(ref, 4) ? 1u : 0u;
+    bad |= c8 != angle_code_f16(ref, 8) ? 1u : 0u;
   }
   const unsigned long long ballot = __ballot(bad);
   if ((threadIdx.x & 63) == 0 && ballot) atomicAdd(mismatches, (unsigned long long)__popcll(ballot));
@@ -290,6 +559,25 @@ __global__ __launch_bounds__(256) void div_exhaustive_kernel(unsigned long long*
     const uint16_t fast = f2h(div_f16(v, s, __builtin_amdgcn_rcpf(s)));
     const uint16_t ref = f2h(v / s);
     bad = fast != ref ? 1u : 0u;
+  }
+  const unsigned long long ballot = __ballot(bad);
+  if ((threadIdx.x & 63) == 0 && ballot) atomicAdd(mismatches, (unsigned long long)__popcll(ballot));
+}
+
+// Every finite value v against one positive finite scale per blockIdx.y: the
+// fast V code byte (with its exact fallback) against the exact one.
+__global__ __launch_bounds__(256) void vcode_exhaustive_kernel(unsigned long long* mismatches, int32_t s_begin) {
+  const uint32_t sb = (uint32_t)(s_begin + (int32_t)blockIdx.y) & 0x7fffu;
+  const uint32_t vb = blockIdx.x * 256u + threadIdx.x;
+  uint32_t bad = 0;
+  if (sb != 0 && (sb & 0x7c00u) != 0x7c00u && (vb & 0x7c00u) != 0x7c00u) {
+    const float s = h2f((uint16_t)sb);
+    const float v = h2f((uint16_t)vb);
+    bool near;
+    uint32_t fast = vcode_fast_byte(v, __builtin_amdgcn_rcpf(s), 0u, 0u, &near);
+    if (near) fast = vcode_exact_byte(v, s);
+    const int32_t ref = to_int8_rne(h2f(f2h(v / s)));
+    bad = (int32_t)(int8_t)(uint8_t)(fast ^ 0x80u) != ref ? 1u : 0u;
   }
   const unsigned long long ballot = __ballot(bad);
   if ((threadIdx.x & 63) == 0 && ballot) atomicAdd(mismatches, (unsigned long long)__popcll(ballot));
@@ -378,7 +666,16 @@ int32_t tp_encode_pages(const void* k, const void* v, int32_t in_dtype, int64_t 
   a.page_begin = page_begin;
   const dim3 grid((unsigned)n_pages, (unsigned)bh);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (in_dtype == 1)
+  // fp16 K and V in the runtime's two layouts take the specialised kernel.
+  const bool is_default = !layout->int8_radii && layout->l1_bits == 4 && layout->deep_bits == 4 &&
+                          layout->split_dim == 64 && !(((uintptr_t)pages->angle_l1 | (uintptr_t)pages->angle_deep) & 7u);
+  const bool is_fast = layout->int8_radii && layout->deep_bits == 8 && layout->split_dim == 0 &&
+                       !((uintptr_t)pages->angle_deep & 15u);
+  if (in_dtype == 0 && k && v && is_default)
+    hipLaunchKernelGGL(encode_f16_kernel<kEncDefault>, grid, dim3(256), 0, s, a);
+  else if (in_dtype == 0 && k && v && is_fast)
+    hipLaunchKernelGGL(encode_f16_kernel<kEncFast>, grid, dim3(256), 0, s, a);
+  else if (in_dtype == 1)
     hipLaunchKernelGGL(encode_pages_kernel<true>, grid, dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL(encode_pages_kernel<false>, grid, dim3(256), 0, s, a);
@@ -407,6 +704,18 @@ int32_t tp_selftest_atan2_exhaustive(unsigned long long* mismatches, int32_t x_b
   hipLaunchKernelGGL(atan2_exhaustive_kernel, dim3(256, (unsigned)x_count), dim3(256), 0,
                      static_cast<hipStream_t>(stream), mismatches, x_begin);
   return launch_status("tp_selftest_atan2_exhaustive");
+}
+
+int32_t tp_selftest_vcode_exhaustive(unsigned long long* mismatches, int32_t s_begin, int32_t s_count,
+                                     void* stream) {
+  clear_error();
+  if (!mismatches || s_begin < 0 || s_count < 1 || s_begin + s_count > 32768 || s_count > 65535) {
+    set_error("bad self-test range");
+    return TP_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(vcode_exhaustive_kernel, dim3(256, (unsigned)s_count), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), mismatches, s_begin);
+  return launch_status("tp_selftest_vcode_exhaustive");
 }
 
 int32_t tp_selftest_div_f16_exhaustive(unsigned long long* mismatches, int32_t s_begin, int32_t s_count,
