@@ -47,12 +47,11 @@ constexpr float kF32InvF16TwoPi = 0.159203976392745972f;
 
 // fp32 ulps around an fp16 rounding midpoint inside which a fast fp32 result
 // is not trusted and the exact path decides.  Each guard exceeds the fast
-// path's error: v_sqrt_f32 is within 1 ulp, a v_rcp_f32 product within 2,
-// atan2_poly and logf within a few; the atan2, sqrt, log and angle-code paths
-// are checked over every fp16 input by the self-test kernels.
+// path's error: a v_rcp_f32 product is within 2 ulps, atan2_poly and logf
+// within a few; the atan2, log, quotient and angle-code paths are checked over
+// every fp16 input by the self-test kernels.
 constexpr int kGuardAtan2 = 6;
 constexpr int kGuardLog = 16;
-constexpr int kGuardSqrt = 2;
 constexpr int kGuardDiv = 3;
 
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(f16, b); }
@@ -153,14 +152,12 @@ __device__ __forceinline__ uint16_t log_f16(float r) {
   return exact ? l : log_f16_slow(r);
 }
 
-// Correctly rounded fp16 sqrt of a non-negative fp16 value: v_sqrt_f32 (within
-// 1 fp32 ulp) unless that lands near an fp16 rounding boundary, then the
-// correctly rounded fp32 sqrt (which fp16 rounding cannot distinguish from the
-// exact root: 24 >= 2 * 11 + 2 significant bits).
+// Correctly rounded fp16 sqrt of a non-negative fp16 value s: v_sqrt_f16, which
+// on gfx950 returns the correctly rounded root for every non-negative fp16
+// input (tp_selftest_f16_tables checks all of them against the fp16 rounding of
+// the correctly rounded fp32 root, itself exact to fp16: 24 >= 2 * 11 + 2).
 __device__ __forceinline__ uint16_t sqrt_f16(float s) {
-  const float r = __builtin_amdgcn_sqrtf(s);
-  if (r != 0.0f && near_f16_midpoint<kGuardSqrt>(r)) return f2h(sqrtf(s));
-  return f2h(r);
+  return __builtin_bit_cast(uint16_t, __builtin_sqrtf16((f16)s));
 }
 
 // fp16(v / s) for fp16-representable v and s > 0 (rs = v_rcp_f32(s)): the

@@ -295,14 +295,13 @@ __device__ __forceinline__ float angle_arg_fast(float x, float y, bool* flag) {
 // result's rounding midpoint give different codes.
 template <int kBits>
 __device__ __forceinline__ uint32_t exact_angle_code(float y, float x) {
-  bool exact;
-  const uint16_t a16 = atan2_f16_fast(y, x, &exact);
+  const float a = atan2_poly(y, x);
+  const uint16_t a16 = f2h(a);
   const uint32_t c0 = angle_code_f16(a16, kBits);
-  if (exact) return c0;
+  if (!near_f16_midpoint_code<kGuardAtan2>(a)) return c0;
   // The fast fp32 angle lies within kGuardAtan2 ulps of the midpoint between
   // a16 and the neighbour on its side; the correctly rounded value is one of
   // the two.
-  const float a = atan2_poly(y, x);
   const float d = a - h2f(a16);
   const uint16_t nb = (uint16_t)(a16 + ((d > 0.0f) == !(a16 & 0x8000u) ? 1 : -1));
   if ((a16 & 0x7fffu) == 0 || angle_code_f16(nb, kBits) != c0) return angle_code_f16(atan2_f16_slow(y, x), kBits);
@@ -343,22 +342,16 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
   RawRow32<false> kraw;
   load_row32<false>(a.k, in_off, valid, kraw);
   uint16_t r16[16];
-  float ss16[16];  // fp16 x*x + y*y, kept for an exact sqrt
   uint32_t cw[kFastLayout ? 4 : 2];
 #pragma unroll
   for (int i = 0; i < (kFastLayout ? 4 : 2); ++i) cw[i] = 0u;
-  uint32_t fixr = 0;  // pairs whose radius the fast path cannot vouch for
   uint32_t fixa = 0;  // pairs whose angle code the fast path cannot vouch for
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const uint32_t w = raw_word(kraw, j);
     const half2v xy = __builtin_bit_cast(half2v, w);
     const half2v sq = xy * xy;  // fp16 products, as the reference squares in fp16 (no FMA)
-    const float ss = (float)(f16)(sq[0] + sq[1]);
-    ss16[j] = ss;
-    const float r = __builtin_amdgcn_sqrtf(ss);
-    fixr |= ((r != 0.0f) & near_f16_midpoint<kGuardSqrt>(r)) ? (1u << j) : 0u;
-    r16[j] = f2h(r);
+    r16[j] = __builtin_bit_cast(uint16_t, __builtin_sqrtf16((f16)(sq[0] + sq[1])));  // correctly rounded
     bool flag;
     const float arg = angle_arg_fast<kBits>((float)xy[0], (float)xy[1], &flag);
     fixa |= flag ? (1u << j) : 0u;
@@ -368,23 +361,12 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
       cw[j >> 3] |= __builtin_amdgcn_cvt_pk_u8_f32(arg, 0u, 0u) << (4 * (j & 7));
     }
   }
-  // Exact redo of the flagged radii and codes (padding tokens are never flagged).
-  while (fixr) {
-    const int j = __builtin_ctz(fixr);
-    fixr &= fixr - 1u;
-    float ss = 0.0f;
-#pragma unroll
-    for (int k2 = 0; k2 < 16; ++k2) ss = k2 == j ? ss16[k2] : ss;
-    const uint16_t rj = sqrt_f16(ss);
-#pragma unroll
-    for (int k2 = 0; k2 < 16; ++k2) r16[k2] = k2 == j ? rj : r16[k2];
-  }
-  while (fixa) {
+  // Exact redo of the flagged codes (padding tokens are never flagged).
+  const uint32_t* kin = reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.k) + in_off);
+  while (fixa) {  // flagged pairs are never padding: reload the pair
     const int j = __builtin_ctz(fixa);
     fixa &= fixa - 1u;
-    uint32_t w = 0;
-#pragma unroll
-    for (int k2 = 0; k2 < 16; ++k2) w = k2 == j ? raw_word(kraw, k2) : w;
+    const uint32_t w = kin[j];
     const uint32_t c = exact_angle_code<kBits>(h2f((uint16_t)(w >> 16)), h2f((uint16_t)(w & 0xffffu)));
     if constexpr (kFastLayout) {
       const uint32_t sh = 8u * (uint32_t)(j & 3);
@@ -432,12 +414,33 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
     const float ls = mx == 0.0f ? 1e-6f : mx;
     const uint16_t ls16 = f2h(ls / 127.0f);
     const float lsf = h2f(ls16);
+    // code = int8(clip(rint(f32(lr / ls)))): a reciprocal product is within 2
+    // ulps of the correctly rounded quotient, and |quotient| <= 128, so rint
+    // agrees unless the product is within 2^-13 of a half-integer; those are
+    // redone with the division.  NaN quotients (0 / 0 scale) give code 0.
+    const float rl = __builtin_amdgcn_rcpf(lsf);
     uint32_t packed[4] = {0u, 0u, 0u, 0u};
+    uint32_t dfix = 0;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const uint32_t c = (uint32_t)(to_int8_rne(lr[j] / lsf) & 0xff);
-      packed[j >> 2] |= c << (8 * (j & 3));
+      const float qd = lr[j] * rl;
+      dfix |= fabsf(qd - floorf(qd) - 0.5f) <= 0x1p-13f ? (1u << j) : 0u;
+      packed[j >> 2] = __builtin_amdgcn_cvt_pk_u8_f32((qd == qd ? qd : 0.0f) + 128.0f, (uint32_t)(j & 3), packed[j >> 2]);
     }
+    while (dfix) {
+      const int j = __builtin_ctz(dfix);
+      dfix &= dfix - 1u;
+      float lj = 0.0f;
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) lj = k2 == j ? lr[k2] : lj;
+      const float qd = lj / lsf;
+      const uint32_t b = __builtin_amdgcn_cvt_pk_u8_f32((qd == qd ? qd : 0.0f) + 128.0f, 0u, 0u);
+      const uint32_t sh = 8u * (uint32_t)(j & 3);
+#pragma unroll
+      for (int k2 = 0; k2 < 4; ++k2) packed[k2] = k2 == (j >> 2) ? (packed[k2] & ~(0xffu << sh)) | (b << sh) : packed[k2];
+    }
+#pragma unroll
+    for (int k2 = 0; k2 < 4; ++k2) packed[k2] ^= 0x80808080u;  // biased bytes -> int8
     *reinterpret_cast<uint4*>(static_cast<int8_t*>(a.radii) + row * kPairs + 16 * qq) =
         make_uint4(packed[0], packed[1], packed[2], packed[3]);
     if (tid == 0) a.radii_scales[slot] = ls16;
@@ -490,13 +493,11 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
     vw[i >> 2] = vcode_fast_byte(raw_val(vraw, i), rs, (uint32_t)(i & 3), vw[i >> 2], &near);
     vfix |= near ? (1u << i) : 0u;
   }
-  while (vfix) {  // exact quotients of the flagged values
+  const uint16_t* vin = static_cast<const uint16_t*>(a.v) + in_off;
+  while (vfix) {  // exact quotients of the flagged values, reloaded (never padding)
     const int i = __builtin_ctz(vfix);
     vfix &= vfix - 1u;
-    float vi = 0.0f;
-#pragma unroll
-    for (int k2 = 0; k2 < 32; ++k2) vi = k2 == i ? raw_val(vraw, k2) : vi;
-    const uint32_t b = vcode_exact_byte(vi, s);
+    const uint32_t b = vcode_exact_byte(h2f(vin[i]), s);
     const uint32_t sh = 8u * (uint32_t)(i & 3);
 #pragma unroll
     for (int k2 = 0; k2 < 8; ++k2) vw[k2] = k2 == (i >> 2) ? (vw[k2] & ~(0xffu << sh)) | (b << sh) : vw[k2];
