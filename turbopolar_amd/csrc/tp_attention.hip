@@ -571,6 +571,9 @@ struct AttnShared {
 
 template <int KIND, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a) {
+  // The fold maps 512 threads onto up to 16 heads x 128 dims at 1, 2 or 4 dims
+  // per thread, and the combine sizes its split groups for 512 threads.
+  static_assert(WAVES == 8, "decode_attention_kernel assumes 8 waves per workgroup");
   __shared__ AttnShared<WAVES> sh;
 
   const int tid = threadIdx.x;
