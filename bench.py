@@ -333,6 +333,48 @@ def run_model(args) -> dict:
                 *[layer.keys for layer in dense.layers], *[layer.values for layer in dense.layers])))}
 
 
+def run_decompress(args, layout) -> dict:
+    """§8 f1 decompress-on-read: one tp_decode_pages launch per step turns
+    every page of a 32k cache (8 kv heads, 512 pages) back into dense fp16 K
+    and V [1, 8, 32768, 128], as update_and_fetch does before prefill
+    attention.  Three rotating caches, so the reads come from HBM."""
+    import torch
+
+    from turbopolar_amd import _lib
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    args.rotate = 3
+    _, caches = build_caches(args, dev, layout)
+    L = _lib.lib()
+    n_pages = caches[0]["pages"].S
+    k_out = torch.empty((1, args.hkv, n_pages * 64, 128), dtype=torch.float16, device=dev)
+    v_out = torch.empty_like(k_out)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def step(i):
+        ps = caches[i % len(caches)]["pages"]
+        st = L.tp_decode_pages(ctypes.byref(ps.layout), ctypes.byref(ps.pages), args.hkv, 0, n_pages,
+                               k_out.data_ptr(), v_out.data_ptr(), stream)
+        if st:
+            _lib.check(st, "tp_decode_pages")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(args.steps):
+        step(i)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    read = algorithmic_bytes(args.hq, args.hkv, n_pages, layout) - args.hq * 128 * 4
+    write = 2 * k_out.numel() * 2
+    return {"ms": ms, "read": read, "write": write, "n_pages": n_pages}
+
+
 def run_encode(args, layout) -> dict:
     """Bulk prefill (workload 1): one tp_encode_pages launch
     encodes ``context`` fp16 tokens of ``hkv`` kv heads into pages.  Input and
@@ -452,10 +494,12 @@ def main():
     ap.add_argument("--rotate", type=int, default=0, help="independent caches to rotate (0 = auto, >256 MB)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=["decode", "encode", "append", "layers", "model"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "encode", "append", "layers", "model", "decompress"],
+                    default="decode",
                     help="decode (the BASELINE metric, default); encode / append: configs[3] workloads; "
                          "layers: configs[1] (--layers decode launches per step); "
-                         "model: a configs[1]-shape Llama decoding through the transformers hook")
+                         "model: a configs[1]-shape Llama decoding through the transformers hook; "
+                         "decompress: tp_decode_pages of a whole cache (prefill decompress-on-read)")
     ap.add_argument("--kind", choices=["outlier", "loguniform", "studentt", "normal"], default=None,
                     help="K distribution (default: outlier for decode, loguniform for layers)")
     ap.add_argument("--layers", type=int, default=16)
@@ -474,6 +518,22 @@ def main():
     layout = LAYOUTS[args.layout]
     if args.kind is None:
         args.kind = "loguniform" if args.workload == "layers" else "outlier"
+    if args.workload == "decompress":
+        r = run_decompress(args, layout)
+        nbytes = r["read"] + r["write"]
+        gbps = nbytes / (r["ms"] * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": "page decompress us/step (decompress-on-read of a whole cache), Llama-3-8B kv shape",
+            "value": round(r["ms"] * 1e3, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(r["ms"], 6), "higher_is_better": False,
+            "dtype": "f16", "data": "synthetic",
+            "config": {"workload": f"tp_decode_pages: {r['n_pages']} pages x {args.hkv} kv heads -> dense fp16 K "
+                                   f"and V ({args.context} tokens)", "layout": args.layout},
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+            "algorithmic_bytes_per_step": {"read": r["read"], "write": r["write"]},
+        }))
+        return
     if args.workload == "model":
         r = run_model(args)
         print(json.dumps({

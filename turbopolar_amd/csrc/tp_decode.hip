@@ -8,6 +8,11 @@
 //
 // One 256-thread workgroup per page; thread (t = tid/4, q = tid%4) writes key
 // pairs [16q, 16q+16) and value group q of token t (64 contiguous bytes each).
+// The page's code rows are staged in LDS, and the fp32 cos / sin of every code
+// angle (and, for int8 log radii, exp(code * scale) of every code) are built
+// once per workgroup into LDS tables, so a pair costs two lookups and two fp32
+// multiplies; the table entries are the same fp32 values the per-pair
+// expressions give, so the output is unchanged.
 #include "tp_common.h"
 
 namespace tp {
@@ -33,6 +38,11 @@ struct DecodeArgs {
 };
 
 __global__ __launch_bounds__(256) void decode_pages_kernel(DecodeArgs a) {
+  __shared__ float2 s_cs_l1[256];
+  __shared__ float2 s_cs_deep[256];
+  __shared__ float s_exp[256];
+  __shared__ uint32_t s_l1[kPageTokens * 64 / 4];
+  __shared__ uint32_t s_deep[kPageTokens * 64 / 4];
   const int page = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const int tid = threadIdx.x;
@@ -43,28 +53,49 @@ __global__ __launch_bounds__(256) void decode_pages_kernel(DecodeArgs a) {
   const int64_t out_off = ((bh * a.n_pages + page) * kPageTokens + t) * kHeadDim + 32 * qq;
 
   if (a.k_out) {
-    const float ls = a.int8_radii ? h2f(a.radii_scales[slot]) : 0.0f;
-    const uint8_t* l1row = a.angle_l1 + row * a.l1_row;
-    const uint8_t* deeprow = a.angle_deep + row * a.deep_row;
+    // Tables: (cos, sin) of each l1 / deep code angle (decoder.py:37-55) and
+    // exp(code * scale) of each int8 log-radius code (decoder.py:57-62).
+    if (tid < (1 << a.l1_bits) && a.split_half > 0) {
+      const float th = code_angle((uint32_t)tid, a.l1_bits);
+      s_cs_l1[tid] = make_float2(cosf(th), sinf(th));
+    }
+    if (tid < (1 << a.deep_bits)) {
+      const float th = code_angle((uint32_t)tid, a.deep_bits);
+      s_cs_deep[tid] = make_float2(cosf(th), sinf(th));
+    }
+    if (a.int8_radii) s_exp[tid] = expf((float)(tid - 128) * h2f(a.radii_scales[slot]));
+    // The page's code rows: 64 rows of l1_row / deep_row bytes each, contiguous.
+    const uint32_t* l1src = reinterpret_cast<const uint32_t*>(a.angle_l1 + slot * kPageTokens * a.l1_row);
+    for (int i = tid; i < 16 * a.l1_row; i += 256) s_l1[i] = l1src[i];
+    const uint32_t* deepsrc = reinterpret_cast<const uint32_t*>(a.angle_deep + slot * kPageTokens * a.deep_row);
+    for (int i = tid; i < 16 * a.deep_row; i += 256) s_deep[i] = deepsrc[i];
+    // Radii of the thread's 16 pairs: 32 bytes (fp16) or 16 bytes (int8 codes).
+    uint4 rv[2];
+    if (a.int8_radii) {
+      rv[0] = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(a.radii) + row * kPairs + 16 * qq);
+      rv[1] = make_uint4(0u, 0u, 0u, 0u);
+    } else {
+      const uint4* rp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.radii) + row * kPairs + 16 * qq);
+      rv[0] = rp[0];
+      rv[1] = rp[1];
+    }
+    __syncthreads();
+    const uint8_t* l1row = reinterpret_cast<const uint8_t*>(s_l1) + t * a.l1_row;
+    const uint8_t* deeprow = reinterpret_cast<const uint8_t*>(s_deep) + t * a.deep_row;
+    const uint32_t rw[8] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w, rv[1].x, rv[1].y, rv[1].z, rv[1].w};
     uint32_t w[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int p = 16 * qq + j;
       float r;
       if (a.int8_radii) {
-        const int rc = static_cast<const int8_t*>(a.radii)[row * kPairs + p];
-        r = expf((float)rc * ls);
+        r = s_exp[((rw[j >> 2] >> (8 * (j & 3))) + 128u) & 0xffu];
       } else {
-        r = h2f(static_cast<const uint16_t*>(a.radii)[row * kPairs + p]);
+        r = h2f((uint16_t)(rw[j >> 1] >> (16 * (j & 1))));
       }
-      float th;
-      if (p < a.split_half)
-        th = code_angle(packed_code(l1row, p, a.l1_bits), a.l1_bits);
-      else
-        th = code_angle(packed_code(deeprow, p - a.split_half, a.deep_bits), a.deep_bits);
-      const float kx = r * cosf(th);
-      const float ky = r * sinf(th);
-      w[j] = (uint32_t)f2h(kx) | ((uint32_t)f2h(ky) << 16);
+      const float2 cs = p < a.split_half ? s_cs_l1[packed_code(l1row, p, a.l1_bits)]
+                                         : s_cs_deep[packed_code(deeprow, p - a.split_half, a.deep_bits)];
+      w[j] = (uint32_t)f2h(r * cs.x) | ((uint32_t)f2h(r * cs.y) << 16);
     }
     uint4* dst = reinterpret_cast<uint4*>(a.k_out + out_off);
 #pragma unroll
@@ -109,8 +140,10 @@ extern "C" int32_t tp_decode_pages(const tp_page_layout* layout, const tp_pages*
   if (n_pages == 0 || (!k_out && !v_out)) return TP_OK;
   if (k_out && (!pages->radii || (l1_row > 0 && !pages->angle_l1) ||
                 (deep_row > 0 && !pages->angle_deep) ||
-                (layout->int8_radii && !pages->radii_scales) || ((uintptr_t)k_out & 15u))) {
-    set_error("key page buffers missing or k_out misaligned");
+                (layout->int8_radii && !pages->radii_scales) || ((uintptr_t)k_out & 15u) ||
+                ((uintptr_t)pages->radii & 15u) || ((uintptr_t)pages->angle_l1 & 3u) ||
+                ((uintptr_t)pages->angle_deep & 3u))) {
+    set_error("key page buffers missing or misaligned (radii 16-byte, codes 4-byte), or k_out misaligned");
     return TP_ERR_INVALID;
   }
   if (v_out && (!pages->v_codes || !pages->v_scales || ((uintptr_t)v_out & 15u) ||
