@@ -129,3 +129,21 @@ def test_product_has_no_oracle_dependency():
     for f in pkg.glob("*.py"):
         src = f.read_text()
         assert not re.search(r"^\s*(import|from)\s+oracle\b", src, re.M), f
+
+
+def test_append_stage_argument_validation():
+    L = _lib.lib()
+    args = dict(k=4096, v=8192, dt=0, bh=8, tok=1, cb=0, n=1, tk=12288, tv=16384, tt=64, tp=0)
+
+    def call(check, flag):
+        a = args
+        st = L.tp_append_stage(a["k"], a["v"], a["dt"], a["bh"], a["tok"], a["cb"], a["n"], a["tk"], a["tv"],
+                               a["tt"], a["tp"], check, flag, 1, None)
+        return st, L.tp_last_error().decode()
+
+    for check in (-1, 3):
+        st, msg = call(check, 20480)
+        assert st == _lib.TP_ERR_INVALID and "check must be" in msg
+    for check in (1, 2):
+        st, msg = call(check, None)
+        assert st == _lib.TP_ERR_INVALID and "flag" in msg

@@ -253,3 +253,31 @@ def test_single_token_appends_match_bulk(device):
         assert torch.equal(bk.radii, ck.radii) and torch.equal(bk.angle_codes_l1, ck.angle_codes_l1)
         assert torch.equal(bk.angle_codes_deep, ck.angle_codes_deep)
         assert torch.equal(bv.codes, cv.codes) and torch.equal(bv.scales, cv.scales)
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_append_stage_flag_modes(device, mode):
+    """tp_append_stage's verdict through a device flag (check 1, read back with
+    a copy) and through a pinned host flag (check 2, written by the kernel):
+    both report a NaN, both pass finite input, and a stale epoch in the flag
+    never reads as a new verdict."""
+    from turbopolar_amd import _lib
+
+    L = _lib.lib()
+    flag = torch.zeros(1, dtype=torch.int32, device=device) if mode == 1 else torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    tail_k = torch.zeros((8, 64, 128), dtype=torch.float16, device=device)
+    tail_v = torch.zeros_like(tail_k)
+    k = torch.randn((8, 1, 128), dtype=torch.float16, device=device)
+    v = torch.randn_like(k)
+    stream = torch.cuda.current_stream(device).cuda_stream
+
+    def stage(kk, epoch):
+        return L.tp_append_stage(kk.data_ptr(), v.data_ptr(), 0, 8, 1, 0, 1, tail_k.data_ptr(), tail_v.data_ptr(),
+                                 64, 0, mode, flag.data_ptr(), epoch, stream)
+
+    assert stage(k, 1) == _lib.TP_OK
+    bad = k.clone()
+    bad[3, 0, 77] = float("nan")
+    assert stage(bad, 2) == _lib.TP_ERR_NONFINITE
+    assert stage(k, 3) == _lib.TP_OK  # the flag still holds epoch 2
+    assert torch.equal(tail_k[:, 0], k[:, 0])

@@ -64,7 +64,12 @@ __global__ __launch_bounds__(256) void append_stage_kernel(AppendArgs a) {
       reinterpret_cast<uint4*>(a.tail_v)[dst] = vw;
     }
   }
-  if (bad) *a.flag = a.epoch;  // every writer stores the same value
+  if (bad) {  // every writer stores the same value
+    if (a.check == 2)
+      __hip_atomic_store(a.flag, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);  // pinned host flag
+    else
+      *a.flag = a.epoch;
+  }
 }
 
 }  // namespace tp
@@ -92,8 +97,8 @@ int32_t tp_append_stage(const void* k, const void* v, int32_t in_dtype, int64_t 
               (long long)tail_tokens);
     return TP_ERR_INVALID;
   }
-  if (check && !flag) {
-    set_error("a verdict flag is required when checking");
+  if (check < 0 || check > 2 || (check && !flag)) {
+    set_error("check must be 0, 1 (device flag) or 2 (pinned host flag), with a flag when checking");
     return TP_ERR_INVALID;
   }
   const uintptr_t al = (uintptr_t)k | (uintptr_t)v | (uintptr_t)tail_k | (uintptr_t)tail_v;
@@ -125,8 +130,14 @@ int32_t tp_append_stage(const void* k, const void* v, int32_t in_dtype, int64_t 
   int32_t st = launch_status("tp_append_stage");
   if (st != TP_OK || !check) return st;
   uint32_t verdict = 0;
-  if (hipMemcpyAsync(&verdict, flag, sizeof(verdict), hipMemcpyDeviceToHost, s) != hipSuccess ||
-      hipStreamSynchronize(s) != hipSuccess) {
+  if (check == 2) {  // the kernel wrote the host flag directly: one synchronisation, no copy
+    if (hipStreamSynchronize(s) != hipSuccess) {
+      set_error("tp_append_stage: synchronising the stream failed");
+      return TP_ERR_HIP;
+    }
+    verdict = *reinterpret_cast<volatile uint32_t*>(flag);
+  } else if (hipMemcpyAsync(&verdict, flag, sizeof(verdict), hipMemcpyDeviceToHost, s) != hipSuccess ||
+             hipStreamSynchronize(s) != hipSuccess) {
     set_error("tp_append_stage: reading the verdict failed");
     return TP_ERR_HIP;
   }

@@ -53,7 +53,7 @@ class TurboPolarKVCacheRuntime:
         self._tail_k: Optional[torch.Tensor] = None
         self._tail_v: Optional[torch.Tensor] = None
         self._tail_len = 0
-        self._flag: Optional[torch.Tensor] = None  # tp_append_stage verdict (device)
+        self._flag: Optional[torch.Tensor] = None  # tp_append_stage verdict (pinned host memory)
         self._epoch = 0
 
         self._initialized = False
@@ -186,8 +186,10 @@ class TurboPolarKVCacheRuntime:
         if self._tail_k is None:
             self._tail_k = torch.zeros((B, H, PAGE, D), dtype=k_new.dtype, device=k_new.device)
             self._tail_v = torch.zeros((B, H, PAGE, D), dtype=k_new.dtype, device=k_new.device)
-        if self._flag is None or self._flag.device != k_new.device:
-            self._flag = torch.zeros(1, dtype=torch.int32, device=k_new.device)
+        if self._flag is None:
+            # Written by the staging kernel and read after one synchronisation,
+            # with no device-to-host copy.
+            self._flag = torch.zeros(1, dtype=torch.int32, pin_memory=True)
         if self._tail_len:
             n_head, head_dst = min(PAGE - self._tail_len, T), self._tail_len
         elif T < PAGE:
@@ -217,7 +219,7 @@ class TurboPolarKVCacheRuntime:
         with torch.cuda.device(k.device):
             st = _lib.lib().tp_append_stage(
                 k.data_ptr(), v.data_ptr(), 1 if k.dtype == torch.float32 else 0, B * H, T, begin, n,
-                self._tail_k.data_ptr(), self._tail_v.data_ptr(), PAGE, dst, 1 if check else 0,
+                self._tail_k.data_ptr(), self._tail_v.data_ptr(), PAGE, dst, 2 if check else 0,
                 self._flag.data_ptr(), self._epoch, _lib.stream_of(k.device),
             )
         if st == _lib.TP_ERR_NONFINITE:
