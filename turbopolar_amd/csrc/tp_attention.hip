@@ -339,17 +339,17 @@ __device__ __forceinline__ void qk_tail(const AttnArgs& a, int64_t bkv, const ha
 
 struct VRegs {
   uint2 w[16];
-  half2v s[8];  // scales of tokens (2q, 2q+1) of each k-step
+  uint32_t sd[2];  // dwords `lane` and `lane + 64` of the page's 128-dword scale block
 };
 
 __device__ __forceinline__ int v_token(int ks, int l4, int e) { return 32 * ks + 4 * l4 + (e & 3) + 16 * (e >> 2); }
 
-// Issues the V code and scale loads of one page; the scales arrive as raw
-// fp16 bits, one token per register, so nothing waits on them here.
-__device__ __forceinline__ void load_v_raw(const AttnArgs& a, int64_t slot, int l16, int l4, VRegs& v,
-                                           uint32_t* sraw) {
+// Issues the V code loads of one page and loads its 512 bytes of scales as
+// two coalesced dwords per lane (the scale of token t, group g is half g & 1
+// of dword 2t + g / 2); PV gathers each lane's scales from these with lane
+// permutes, so the scales hold two registers, not one per token.
+__device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16, int l4, int lane, VRegs& v) {
   const int8_t* vbase = a.v_codes + slot * (kPageTokens * kHeadDim) + 8 * l16;
-  const uint16_t* sbase = a.v_scales + slot * (kPageTokens * kVGroups) + (l16 >> 2);
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
@@ -357,34 +357,10 @@ __device__ __forceinline__ void load_v_raw(const AttnArgs& a, int64_t slot, int 
       const int t = v_token(ks, l4, e);
       v.w[8 * ks + e] = *reinterpret_cast<const uint2*>(vbase + t * kHeadDim);
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sraw[8 * ks + e] = sbase[v_token(ks, l4, e) * kVGroups];
   }
-}
-
-// Pairs the raw scales as (token 2q, token 2q+1) per k-step.
-__device__ __forceinline__ void pack_scales(const uint32_t* sraw, VRegs& v) {
-#pragma unroll
-  for (int q = 0; q < 8; ++q)
-    v.s[q] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(sraw[2 * q + 1], sraw[2 * q], 0x05040100u));
-}
-
-__device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16, int l4, VRegs& v) {
-  const int8_t* vbase = a.v_codes + slot * (kPageTokens * kHeadDim) + 8 * l16;
-  const uint16_t* sbase = a.v_scales + slot * (kPageTokens * kVGroups) + (l16 >> 2);
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int t = v_token(ks, l4, e);
-      v.w[8 * ks + e] = *reinterpret_cast<const uint2*>(vbase + t * kHeadDim);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f16* sp = reinterpret_cast<const f16*>(sbase);
-      v.s[4 * ks + q] = half2v{sp[v_token(ks, l4, 2 * q) * kVGroups], sp[v_token(ks, l4, 2 * q + 1) * kVGroups]};
-    }
-  }
+  const uint32_t* sbase = reinterpret_cast<const uint32_t*>(a.v_scales + slot * (kPageTokens * kVGroups));
+  v.sd[0] = sbase[lane];
+  v.sd[1] = sbase[lane + 64];
 }
 
 // acc[j] += Vhat^T tile j x P, Vhat = f16(code * scale) exactly: codes become
@@ -404,10 +380,24 @@ __device__ __forceinline__ void pv_tile(const VRegs& v, int ks, const half2v* sp
   acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(e[0], e[1], e[2], e[3]), pb, acc, 0, 0, 0);
 }
 
-__device__ __forceinline__ void pv_regs(const VRegs& v, const half8v* pb, float4v* acc) {
+// sbase4: byte index of the lane holding the scale dword of token 4*l4 of the
+// lane's group (4 * (8*l4 + g/2)); ssel: v_perm selector taking half g & 1 of
+// two dwords.
+__device__ __forceinline__ void pv_regs(const VRegs& v, int sbase4, uint32_t ssel, const half8v* pb,
+                                        float4v* acc) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    const half2v* sp = &v.s[4 * ks];
+    // Scales of tokens (2q, 2q+1) of this k-step as fp16 pairs: tokens
+    // 4*l4 + t0 and 4*l4 + t0 + 1 (t0 = 0, 2, 16, 18) sit in the dwords of
+    // lanes 8*l4 + g/2 + 2*t0 and two lanes further, in register ks.
+    half2v sp[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int t0 = (2 * q & 3) + 16 * (q >> 1);
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(sbase4 + 8 * t0, (int)v.sd[ks]);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(sbase4 + 8 * t0 + 8, (int)v.sd[ks]);
+      sp[q] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(hi, lo, ssel));
+    }
     pv_tile<0>(v, ks, sp, pb[ks], acc[0]);
     pv_tile<1>(v, ks, sp, pb[ks], acc[1]);
     pv_tile<2>(v, ks, sp, pb[ks], acc[2]);
@@ -562,8 +552,8 @@ __device__ __forceinline__ void store_out_n(uint16_t* orow, const float* x, floa
 template <int WAVES>
 struct AttnShared {
   Lut lut;
-  float ml[WAVES][16][2];
-  float acc[WAVES][16 * kRedStride];
+  float2 ml[WAVES][16];
+  alignas(16) float acc[WAVES][16 * kRedStride];
   int last;
 };
 
@@ -578,7 +568,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int l16 = lane & 15;
   const int l4 = lane >> 4;
   // 1-D grid, unit-minor: consecutive workgroup ids go to different kv heads,
@@ -601,24 +591,32 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   const int p_end = (int)min((int64_t)min(p_begin + a.pages_per_split, a.n_pages), live_pages);
 
   // Q and the first page's loads go out before the table build and the
-  // barrier; the first page's V scales are paired only after the barrier, so
-  // no wave waits for memory before it.
+  // barrier, and nothing before the barrier uses them.
   half8v qb[4];
   load_q(a, b, kv, h0, nh, l16, l4, qb);
   int page = p_begin + wave;
   KRegs<KIND> kr;
   VRegs vr;
-  uint32_t sraw[16];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) sraw[e] = 0u;
-  if (page < p_end) {
-    load_k<KIND>(a, bkv * a.capacity + page, l16, l4, kr);
-    load_v_raw(a, bkv * a.capacity + page, l16, l4, vr, sraw);
+  if constexpr (KIND == kKindGeneric) {  // also the launch for a call without pages
+    if (page < p_end) {
+      load_k<KIND>(a, bkv * a.capacity + page, l16, l4, kr);
+      load_v(a, bkv * a.capacity + page, l16, l4, lane, vr);
+    }
+  } else {
+    // The specialised layouts always have pages (p_begin < n_pages), and a
+    // wave without a page of its own loads the split's first page instead of
+    // branching around its loads: a load under a branch would make the
+    // compiler's wait counting treat Q as the newest load, so every QK would
+    // wait for all loads in flight.  The duplicate read hits in the cache.
+    const int p_load = page < p_end ? page : p_begin;
+    load_k<KIND>(a, bkv * a.capacity + p_load, l16, l4, kr);
+    load_v(a, bkv * a.capacity + p_load, l16, l4, lane, vr);
   }
   if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
   lds_barrier();
-  pack_scales(sraw, vr);
 
+  const int sbase4 = 4 * (8 * l4 + (l16 >> 3));
+  const uint32_t ssel = (l16 & 4) ? 0x07060302u : 0x05040100u;
   float m_run = -INFINITY;
   float l_run = 0.0f;
   float4v acc[8];
@@ -627,17 +625,26 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
 
   // Per page: QK on the resident K codes, then the next page's K loads go out,
   // softmax and PV on the resident V codes, then the next page's V loads.
-  while (page < p_end) {
+  // The wave's last page is peeled off, so the loads inside the loop are
+  // unconditional and every wait covers only the loads it needs: QK waits for
+  // the page's K codes while its V codes may still be in flight.  A page with
+  // a successor is fully valid (only the last live page can be partial).
+  for (; page + WAVES < p_end; page += WAVES) {
     float4v s[4];
     qk_regs<KIND>(a, sh.lut, kr, qb, l16, l4, s);
-    const int next = page + WAVES;
-    if (next < p_end) load_k<KIND>(a, bkv * a.capacity + next, l16, l4, kr);
+    load_k<KIND>(a, bkv * a.capacity + page + WAVES, l16, l4, kr);
+    half8v pb[2];
+    softmax_page(s, kPageTokens, a.scale_log2, l4, m_run, l_run, acc, pb);
+    pv_regs(vr, sbase4, ssel, pb, acc);
+    load_v(a, bkv * a.capacity + page + WAVES, l16, l4, lane, vr);
+  }
+  if (page < p_end) {
+    float4v s[4];
+    qk_regs<KIND>(a, sh.lut, kr, qb, l16, l4, s);
     const int valid = (int)min((int64_t)kPageTokens, a.seq_len - (int64_t)page * kPageTokens);
     half8v pb[2];
     softmax_page(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
-    pv_regs(vr, pb, acc);
-    if (next < p_end) load_v(a, bkv * a.capacity + next, l16, l4, vr);
-    page = next;
+    pv_regs(vr, sbase4, ssel, pb, acc);
   }
 
   // The dense tail follows the last page; the last split's least loaded wave takes it.
@@ -659,14 +666,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   // Merge the waves through LDS.
   float l_tot = l_run + __shfl_xor(l_run, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
-  if (l4 == 0) {
-    sh.ml[wave][l16][0] = m_run;
-    sh.ml[wave][l16][1] = l_tot;
-  }
+  if (l4 == 0) sh.ml[wave][l16] = make_float2(m_run, l_tot);
+  // The lane holds dims 32*l4 + 8*i + j (acc[j][i]) of head l16: eight 16-byte
+  // writes of 4 consecutive dims each; with the 132-float row stride the 8
+  // lanes of each write phase cover all banks once.
+  float* arow = &sh.acc[wave][l16 * kRedStride + 32 * l4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sh.acc[wave][l16 * kRedStride + 32 * l4 + 8 * i + j] = acc[j][i];
+  for (int q = 0; q < 8; ++q) {
+    const int i = q >> 1, j0 = 4 * (q & 1);
+    *reinterpret_cast<float4v*>(arow + 4 * q) = float4v{acc[j0][i], acc[j0 + 1][i], acc[j0 + 2][i], acc[j0 + 3][i]};
   }
   lds_barrier();
 
@@ -684,8 +692,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     float m[WAVES], l[WAVES], x[WAVES][4];
 #pragma unroll
     for (int u = 0; u < WAVES; ++u) {
-      m[u] = sh.ml[u][h][0];
-      l[u] = sh.ml[u][h][1];
+      const float2 ml = sh.ml[u][h];
+      m[u] = ml.x;
+      l[u] = ml.y;
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[u][i] = i < dpt ? sh.acc[u][h * kRedStride + d0 + i] : 0.0f;
     }
@@ -743,11 +752,20 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   for (int r0 = 0; r0 < mine; r0 += 8) {
     float2 r[8];
     float4v x[8];
+    // Unconditional loads (a record past `mine` rereads the last one and is
+    // then given weight 0), so all 16 are in flight before the first use.
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const bool ok = r0 + u < mine;
-      r[u] = ok ? *reinterpret_cast<const float2*>(pml + 2 * SG * (r0 + u)) : make_float2(-INFINITY, 0.0f);
-      x[u] = ok ? *reinterpret_cast<const float4v*>(pac + (r0 + u) * rstride) : float4v{};
+      const int ru = min(r0 + u, mine - 1);
+      r[u] = *reinterpret_cast<const float2*>(pml + 2 * SG * ru);
+      x[u] = *reinterpret_cast<const float4v*>(pac + ru * rstride);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (r0 + u >= mine) {
+        r[u] = make_float2(-INFINITY, 0.0f);
+        x[u] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+      }
     }
     float Mn = Mc;
 #pragma unroll
@@ -802,7 +820,7 @@ __global__ __launch_bounds__(256) void fused_qk_kernel(AttnArgs a) {
   __shared__ Lut lut;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int l16 = lane & 15;
   const int l4 = lane >> 4;
   const int64_t bkv = blockIdx.y;
