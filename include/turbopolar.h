@@ -55,7 +55,10 @@ typedef struct tp_page_layout {
   int32_t split_dim;  /* even, 0..128 */
 } tp_page_layout;
 
-/* Device pointers of one page store (see the layout above). */
+/* Device pointers of one page store (see the layout above).  The attention
+ * entry points read radii, angle_deep and v_codes in 16-byte, angle_l1 in
+ * 8-byte and v_scales in 4-byte units, and reject buffers aligned less (any
+ * device allocation, and any page slot of one, is aligned enough). */
 typedef struct tp_pages {
   void* radii;
   void* radii_scales;

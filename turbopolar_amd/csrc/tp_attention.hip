@@ -549,6 +549,67 @@ __device__ __forceinline__ void store_out_n(uint16_t* orow, const float* x, floa
   }
 }
 
+// Folds the 8 wave states of DPT consecutive dims (from d0) of head h, in
+// wave order.  A state with m = -inf weighs 0, so an empty one adds 0 and one
+// that carries NaN (all of its scores NaN) still makes the fold NaN.
+template <int DPT, class Shared>
+__device__ __forceinline__ void fold_waves(const Shared& sh, int h, int d0, float& M, float& L, float* A) {
+  constexpr int W = sizeof(sh.ml) / sizeof(sh.ml[0]);
+  float m[W], l[W], x[W][DPT];
+#pragma unroll
+  for (int u = 0; u < W; ++u) {
+    const float2 ml = sh.ml[u][h];
+    m[u] = ml.x;
+    l[u] = ml.y;
+    const float* src = &sh.acc[u][h * kRedStride + d0];
+    if constexpr (DPT == 4) {
+      const float4v v = *reinterpret_cast<const float4v*>(src);
+      x[u][0] = v[0], x[u][1] = v[1], x[u][2] = v[2], x[u][3] = v[3];
+    } else if constexpr (DPT == 2) {
+      const float2 v = *reinterpret_cast<const float2*>(src);
+      x[u][0] = v.x, x[u][1] = v.y;
+    } else {
+      x[u][0] = src[0];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < W; ++u) M = fmaxf(M, m[u]);
+#pragma unroll
+  for (int u = 0; u < W; ++u) {
+    const float w = m[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[u] - M);
+    L += l[u] * w;
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) A[i] += x[u][i] * w;
+  }
+}
+
+// Merges the partial folds of split groups 1 .. SG-1 of item `it` (LDS slot
+// (g << ish) + it) into group 0's state, in group order.
+template <int SG>
+__device__ __forceinline__ void merge_groups(const float4v* red, const float2* redml, int it, int ish, float& Mc,
+                                             float& Lc, float4v& Ac) {
+  float2 r[SG];
+  float4v x[SG];
+#pragma unroll
+  for (int g2 = 1; g2 < SG; ++g2) {
+    r[g2] = redml[(g2 << ish) + it];
+    x[g2] = red[(g2 << ish) + it];
+  }
+  float Mx = Mc;
+#pragma unroll
+  for (int g2 = 1; g2 < SG; ++g2) Mx = fmaxf(Mx, r[g2].x);
+  const float w0 = Mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mc - Mx);
+  Lc *= w0;
+  Ac *= w0;
+#pragma unroll
+  for (int g2 = 1; g2 < SG; ++g2) {
+    const float w = r[g2].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r[g2].x - Mx);
+    Lc += r[g2].y * w;
+    Ac += x[g2] * w;
+  }
+  Mc = Mx;
+}
+
 template <int WAVES>
 struct AttnShared {
   Lut lut;
@@ -681,34 +742,20 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   // Fold the waves' records.  Every thread takes part: thread t owns dpt
   // consecutive dims of head t / (128 / dpt), with dpt = 1, 2 or 4 for up to
   // 4, 8 or 16 heads, and folds the WAVES records in wave order.
-  const int dpt = nh <= 4 ? 1 : (nh <= 8 ? 2 : 4);
-  const int tph = kHeadDim / dpt;
-  const int h = tid / tph;
-  const int d0 = (tid - h * tph) * dpt;
+  const int ldpt = nh <= 4 ? 0 : (nh <= 8 ? 1 : 2);  // log2(dpt)
+  const int dpt = 1 << ldpt;
+  const int h = tid >> (7 - ldpt);
+  const int d0 = (tid & ((kHeadDim >> ldpt) - 1)) << ldpt;
   const bool live = h < nh;
   float M = -INFINITY, L = 0.0f;
   float A[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (live) {
-    float m[WAVES], l[WAVES], x[WAVES][4];
-#pragma unroll
-    for (int u = 0; u < WAVES; ++u) {
-      const float2 ml = sh.ml[u][h];
-      m[u] = ml.x;
-      l[u] = ml.y;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x[u][i] = i < dpt ? sh.acc[u][h * kRedStride + d0 + i] : 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < WAVES; ++u) M = fmaxf(M, m[u]);
-    // A state with m = -inf weighs 0, so an empty one adds 0 and one that
-    // carries NaN (all of its scores NaN) still makes the fold NaN.
-#pragma unroll
-    for (int u = 0; u < WAVES; ++u) {
-      const float w = m[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[u] - M);
-      L += l[u] * w;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) A[i] += x[u][i] * w;
-    }
+    if (ldpt == 0)
+      fold_waves<1>(sh, h, d0, M, L, A);
+    else if (ldpt == 1)
+      fold_waves<2>(sh, h, d0, M, L, A);
+    else
+      fold_waves<4>(sh, h, d0, M, L, A);
   }
   if (a.n_splits == 1) {
     if (live)
@@ -733,17 +780,21 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   if (!sh.last) return;
 
   // Last workgroup of this (b, kv, head block): combine the n_splits records.
-  // Thread (item = (head hh, 4-dim chunk c4), sg) folds splits sg, sg + SG,
-  // ... online (running max, rescaled sums), with all loads of a batch of 8
-  // records in flight together; the SG partial folds then meet in LDS and are
-  // merged in sg order.
+  // Items are (head hh, 4-dim chunk c4), nh * 32 of them, padded to a power
+  // of two 2^ish; thread (item, sg), sg < SG = 512 / 2^ish, folds splits
+  // sg, sg + SG, ... online (running max, rescaled sums), with all loads of a
+  // batch of 8 records in flight together; the SG partial folds then meet in
+  // LDS and are merged in sg order.
   const int n_items = nh * 32;
-  const int SG = max(1, (WAVES * 64) / n_items);
-  const int it = tid % n_items;
-  const int sg = tid / n_items;
+  const int ish = n_items <= 32 ? 5 : (n_items <= 64 ? 6 : (n_items <= 128 ? 7 : (n_items <= 256 ? 8 : 9)));
+  const int lsg = 9 - ish;
+  const int SG = 1 << lsg;
+  const int it = tid & ((1 << ish) - 1);
+  const int sg = tid >> ish;
+  const bool item = it < n_items;
   const int hh = it >> 5;
   const int c4 = it & 31;
-  const int mine = sg < SG ? (S - sg + SG - 1) / SG : 0;
+  const int mine = item ? (S - sg + SG - 1) >> lsg : 0;
   const float* pac = a.part_acc + ((unit * S + sg) * 16 + hh) * kHeadDim + 4 * c4;
   const float* pml = a.part_ml + ((unit * 16 + hh) * Sp + sg) * 2;
   const int64_t rstride = (int64_t)SG * 16 * kHeadDim;
@@ -784,27 +835,24 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   }
   if (SG > 1) {
     float4v* red = reinterpret_cast<float4v*>(&sh.acc[0][0]);
-    float2* redml = reinterpret_cast<float2*>(red + SG * n_items);
-    if (sg < SG) {
-      red[sg * n_items + it] = Ac;
-      redml[sg * n_items + it] = make_float2(Mc, Lc);
+    float2* redml = reinterpret_cast<float2*>(red + (WAVES * 64));
+    if (item) {
+      red[tid] = Ac;
+      redml[tid] = make_float2(Mc, Lc);
     }
     lds_barrier();
-    if (sg == 0) {
-      float Mx = Mc;
-      for (int g2 = 1; g2 < SG; ++g2) Mx = fmaxf(Mx, redml[g2 * n_items + it].x);
-      const float w0 = Mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mc - Mx);
-      Lc *= w0;
-      Ac *= w0;
-      for (int g2 = 1; g2 < SG; ++g2) {
-        const float2 r = redml[g2 * n_items + it];
-        const float w = r.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r.x - Mx);
-        Lc += r.y * w;
-        Ac += red[g2 * n_items + it] * w;
-      }
+    if (sg == 0 && item) {
+      if (lsg == 1)
+        merge_groups<2>(red, redml, it, ish, Mc, Lc, Ac);
+      else if (lsg == 2)
+        merge_groups<4>(red, redml, it, ish, Mc, Lc, Ac);
+      else if (lsg == 3)
+        merge_groups<8>(red, redml, it, ish, Mc, Lc, Ac);
+      else
+        merge_groups<16>(red, redml, it, ish, Mc, Lc, Ac);
     }
   }
-  if (sg == 0) {
+  if (sg == 0 && item) {
     const float inv = __builtin_amdgcn_rcpf(Lc);
     uint16_t* orow3 = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + hh) * kHeadDim + 4 * c4;
     *reinterpret_cast<uint2*>(orow3) = make_uint2((uint32_t)f2h(Ac[0] * inv) | ((uint32_t)f2h(Ac[1] * inv) << 16),
@@ -895,7 +943,7 @@ static bool fill_common(AttnArgs& a, const void* q, int64_t batch, int32_t hq, i
     }
     if (((uintptr_t)pages->radii & 15u) || (need_v && ((uintptr_t)pages->v_codes & 15u)) ||
         ((uintptr_t)pages->angle_l1 & 7u) || ((uintptr_t)pages->angle_deep & 15u) ||
-        ((uintptr_t)pages->v_scales & 1u)) {
+        (need_v && ((uintptr_t)pages->v_scales & 3u))) {
       set_error("page buffers are not aligned");
       return false;
     }
