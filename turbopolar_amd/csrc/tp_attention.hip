@@ -664,14 +664,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
       load_v(a, bkv * a.capacity + page, l16, l4, lane, vr);
     }
   } else {
-    // The specialised layouts always have pages (p_begin < n_pages), and a
-    // wave without a page of its own loads the split's first page instead of
-    // branching around its loads: a load under a branch would make the
+    // The specialised layouts always have pages (p_begin < n_pages).  A wave
+    // without a page of its own issues the same loads with every lane on the
+    // first bytes of the split's first page (one cache line per load) instead
+    // of branching around them: a load under a branch would make the
     // compiler's wait counting treat Q as the newest load, so every QK would
-    // wait for all loads in flight.  The duplicate read hits in the cache.
-    const int p_load = page < p_end ? page : p_begin;
-    load_k<KIND>(a, bkv * a.capacity + p_load, l16, l4, kr);
-    load_v(a, bkv * a.capacity + p_load, l16, l4, lane, vr);
+    // wait for all loads in flight.
+    const bool has_page = page < p_end;
+    const int p_load = has_page ? page : p_begin;
+    const int lane_e = has_page ? lane : 0;
+    load_k<KIND>(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, kr);
+    load_v(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
   }
   if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
   lds_barrier();
