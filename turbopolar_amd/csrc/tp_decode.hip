@@ -122,6 +122,123 @@ __global__ __launch_bounds__(256) void decode_pages_kernel(DecodeArgs a) {
   }
 }
 
+// ---- specialised layouts ------------------------------------------------------
+//
+// The default layout (fp16 radii, 4-bit l1 and deep codes, split 64) and the
+// fast layout (int8 log radii with an fp16 page scale, 8-bit deep codes,
+// split 0) get their own kernel, one page per workgroup.  Thread T decodes
+// the 8-dim chunk c = T % 16 (pairs 4c .. 4c+3, V group c / 4) of tokens
+// T / 16 + 16 k, k = 0..3, so every load and store instruction of a wave
+// covers consecutive bytes (a wave's 16-byte output stores fill 1 KiB runs).
+// All loads are issued first; the (cos, sin) table (16 or 256 entries) and,
+// for the fast layout, the page's exp table are built in LDS while they are in
+// flight, and V is decoded and stored before the barrier that guards the
+// tables.  V is dequantised as fp16 pairs, f16(code * scale) with one
+// rounding of the exact product, as the f32 expression rounds it.  Outputs
+// are the generic kernel's, bit for bit.
+enum DecodeKind { kDecDefault = 0, kDecFast = 1 };
+
+__device__ __forceinline__ uint32_t i8pair_to_h2(uint32_t w, int first) {
+  // Bytes `first` and `first + 1` of w (int8) as an exact fp16 pair.
+  const f16 lo = (f16)(int)(int8_t)(w >> (8 * first));
+  const f16 hi = (f16)(int)(int8_t)(w >> (8 * first + 8));
+  return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
+  constexpr bool kFast = KIND == kDecFast;
+  constexpr int kCodes = kFast ? 256 : 16;
+  constexpr int kTok = 4;  // tokens per thread
+  __shared__ float2 s_cs[kCodes];
+  __shared__ float s_exp[kFast ? 256 : 1];
+  const int tid = threadIdx.x;
+  const int c = tid & 15;    // 8-dim chunk
+  const int t0 = tid >> 4;   // first token; the others are t0 + 16 k
+  const int64_t bh = blockIdx.y;
+  const int page = blockIdx.x;
+  const int64_t slot = bh * a.capacity + a.page_begin + page;
+  const int64_t row0 = slot * kPageTokens;
+  const int64_t out0 = (bh * a.n_pages + page) * kPageTokens;
+  const bool want_k = a.k_out != nullptr;
+  const bool want_v = a.v_out != nullptr;
+
+  // All loads first.
+  uint32_t rw[kTok][kFast ? 1 : 2];  // radii of pairs 4c..4c+3
+  uint32_t cw[kTok];                 // their angle codes (low 16 bits for 4-bit codes)
+  uint16_t ls16 = 0;
+  if (want_k) {
+#pragma unroll
+    for (int k = 0; k < kTok; ++k) {
+      const int64_t row = row0 + t0 + 16 * k;
+      if constexpr (kFast) {
+        rw[k][0] = *reinterpret_cast<const uint32_t*>(static_cast<const int8_t*>(a.radii) + row * kPairs + 4 * c);
+        cw[k] = *reinterpret_cast<const uint32_t*>(a.angle_deep + row * kPairs + 4 * c);
+      } else {
+        const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.radii) + row * kPairs + 4 * c);
+        rw[k][0] = r.x, rw[k][1] = r.y;
+        cw[k] = *reinterpret_cast<const uint16_t*>((c < 8 ? a.angle_l1 : a.angle_deep) + row * 16 + 2 * (c & 7));
+      }
+    }
+    if constexpr (kFast) ls16 = a.radii_scales[slot];
+  }
+  uint2 vc[kTok];
+  uint16_t vs16[kTok];
+  if (want_v) {
+#pragma unroll
+    for (int k = 0; k < kTok; ++k) {
+      const int64_t row = row0 + t0 + 16 * k;
+      vc[k] = *reinterpret_cast<const uint2*>(a.v_codes + row * kHeadDim + 8 * c);
+      vs16[k] = a.v_scales[row * kVGroups + (c >> 2)];
+    }
+  }
+
+  // Tables (decoder.py:37-62) while the loads are in flight.
+  if (want_k && tid < kCodes) {
+    const float th = code_angle((uint32_t)tid, kFast ? 8 : 4);
+    s_cs[tid] = make_float2(cosf(th), sinf(th));
+  }
+
+  // V (v_quant/encoder.py:32-38).
+  if (want_v) {
+#pragma unroll
+    for (int k = 0; k < kTok; ++k) {
+      const half2v sp = __builtin_bit_cast(half2v, (uint32_t)vs16[k] | ((uint32_t)vs16[k] << 16));
+      uint32_t w[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const half2v h = __builtin_bit_cast(half2v, i8pair_to_h2(q < 2 ? vc[k].x : vc[k].y, 2 * (q & 1)));
+        w[q] = __builtin_bit_cast(uint32_t, h * sp);
+      }
+      *reinterpret_cast<uint4*>(a.v_out + (out0 + t0 + 16 * k) * kHeadDim + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  if (!want_k) return;
+  if constexpr (kFast) s_exp[tid] = expf((float)(tid - 128) * h2f(ls16));
+  __syncthreads();
+
+  // K (decoder.py:57-67).
+#pragma unroll
+  for (int k = 0; k < kTok; ++k) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float r;
+      uint32_t code;
+      if constexpr (kFast) {
+        r = s_exp[((rw[k][0] >> (8 * j)) + 128u) & 0xffu];
+        code = (cw[k] >> (8 * j)) & 0xffu;
+      } else {
+        r = h2f((uint16_t)(rw[k][j >> 1] >> (16 * (j & 1))));
+        code = (cw[k] >> (4 * j)) & 0xfu;
+      }
+      const float2 cs = s_cs[code];
+      w[j] = (uint32_t)f2h(r * cs.x) | ((uint32_t)f2h(r * cs.y) << 16);
+    }
+    *reinterpret_cast<uint4*>(a.k_out + (out0 + t0 + 16 * k) * kHeadDim + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 }  // namespace tp
 
 using namespace tp;
@@ -169,7 +286,19 @@ extern "C" int32_t tp_decode_pages(const tp_page_layout* layout, const tp_pages*
   a.deep_row = deep_row;
   a.k_out = static_cast<uint16_t*>(k_out);
   a.v_out = static_cast<uint16_t*>(v_out);
-  hipLaunchKernelGGL(decode_pages_kernel, dim3((unsigned)n_pages, (unsigned)bh), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool is_default = !layout->int8_radii && layout->l1_bits == 4 && layout->deep_bits == 4 && layout->split_dim == 64;
+  const bool is_fast = layout->int8_radii && layout->deep_bits == 8 && layout->split_dim == 0;
+  const bool aligned = (!k_out || (is_default ? ((uintptr_t)pages->angle_l1 & 1u) == 0 && ((uintptr_t)pages->angle_deep & 1u) == 0
+                                              : ((uintptr_t)pages->angle_deep & 3u) == 0 &&
+                                                    ((uintptr_t)pages->radii & 3u) == 0)) &&
+                       (!v_out || ((uintptr_t)pages->v_codes & 7u) == 0);
+  const dim3 grid((unsigned)n_pages, (unsigned)bh);
+  if (is_default && aligned)
+    hipLaunchKernelGGL(decode_pages_spec_kernel<kDecDefault>, grid, dim3(256), 0, s, a);
+  else if (is_fast && aligned)
+    hipLaunchKernelGGL(decode_pages_spec_kernel<kDecFast>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(decode_pages_kernel, grid, dim3(256), 0, s, a);
   return launch_status("tp_decode_pages");
 }
