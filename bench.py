@@ -447,16 +447,21 @@ def run_append(args, layout, n_appends: int = 4096) -> dict:
     cfg = TurboPolarConfig(num_q_heads=args.hq, num_kv_heads=args.hkv, use_int8_radii=int8,
                            k_angle_bits_level1=l1b, k_angle_bits_deep=deepb, split_dim=split)
     g = torch.Generator(device=dev).manual_seed(3)
-    k = torch.randn((1, args.hkv, n_appends + 64, 128), generator=g, device=dev).half()
-    v = torch.randn((1, args.hkv, n_appends + 64, 128), generator=g, device=dev).half()
+    k = torch.randn((1, args.hkv, n_appends + 128, 128), generator=g, device=dev).half()
+    v = torch.randn((1, args.hkv, n_appends + 128, 128), generator=g, device=dev).half()
+    # One contiguous [1, hkv, 1, 128] tensor per step, as a decode loop hands
+    # over each step's projected K and V (a strided slice of one big tensor
+    # would add a copy kernel to every append).
+    ks = [k[:, :, t:t + 1].contiguous() for t in range(n_appends + 128)]
+    vs = [v[:, :, t:t + 1].contiguous() for t in range(n_appends + 128)]
     warm = TurboPolarKVCacheRuntime(cfg)
     for t in range(128):
-        warm.append(k[:, :, t:t + 1], v[:, :, t:t + 1])
+        warm.append(ks[t], vs[t])
     torch.cuda.synchronize()
     rt = TurboPolarKVCacheRuntime(cfg)
     t0 = time.perf_counter()
     for t in range(n_appends):
-        rt.append(k[:, :, t:t + 1], v[:, :, t:t + 1])
+        rt.append(ks[128 + t], vs[128 + t])
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     return {"us_per_append": dt / n_appends * 1e6, "appends": n_appends, "pages": rt.total_blocks}

@@ -170,11 +170,15 @@ int32_t tp_decode_pages(const tp_page_layout* layout, const tp_pages* pages, int
  * With check != 0 it also scans every element of k and v; the kernel stores
  * `epoch` into *flag if any is NaN or inf, and this call then synchronises
  * `stream`, reads the flag and returns TP_ERR_NONFINITE, or TP_OK.  check == 1:
- * flag is caller-owned device memory, read back with a 4-byte copy; check == 2:
- * flag is caller-owned pinned host memory from hipHostMalloc (device-visible),
- * written by the kernel with a system-scope store and read directly after the
- * synchronisation.  Pass a fresh epoch per call so the flag never needs
- * clearing.  With check == 0 the call is asynchronous like the others. */
+ * flag is caller-owned device memory, read back with a 4-byte copy.  check == 2:
+ * flag is caller-owned pinned host memory from hipHostMalloc (device-visible)
+ * and epoch must be even; the kernel writes epoch + 1 there on a non-finite
+ * value with system-scope stores, and when the launch is a single workgroup
+ * (up to 16 token rows of 128 fp16 or 8 of fp32) it also reports completion
+ * itself (epoch or epoch + 1), so the call polls the flag instead of
+ * synchronising the stream (bounded, then synchronising).  Pass a fresh epoch
+ * per call so the flag never needs clearing.  With check == 0 the call is
+ * asynchronous like the others. */
 int32_t tp_append_stage(const void* k, const void* v, int32_t in_dtype, int64_t bh, int64_t in_tokens,
                         int64_t copy_begin, int64_t n_copy, void* tail_k, void* tail_v, int64_t tail_tokens,
                         int64_t tail_pos, int32_t check, uint32_t* flag, uint32_t epoch, void* stream);

@@ -147,3 +147,5 @@ def test_append_stage_argument_validation():
     for check in (1, 2):
         st, msg = call(check, None)
         assert st == _lib.TP_ERR_INVALID and "flag" in msg
+    L.tp_append_stage(4096, 8192, 0, 8, 1, 0, 1, 12288, 16384, 64, 0, 2, 20480, 3, None)
+    assert "even epoch" in L.tp_last_error().decode()  # check 2 takes even epochs

@@ -256,28 +256,32 @@ def test_single_token_appends_match_bulk(device):
 
 
 @pytest.mark.parametrize("mode", [1, 2])
-def test_append_stage_flag_modes(device, mode):
+@pytest.mark.parametrize("tokens", [1, 300])
+def test_append_stage_flag_modes(device, mode, tokens):
     """tp_append_stage's verdict through a device flag (check 1, read back with
-    a copy) and through a pinned host flag (check 2, written by the kernel):
-    both report a NaN, both pass finite input, and a stale epoch in the flag
-    never reads as a new verdict."""
+    a copy) and through a pinned host flag (check 2, written by the kernel;
+    one workgroup reports completion itself and the host polls, several are
+    synchronised): both report a NaN, both pass finite input, and a stale
+    value in the flag never reads as a new verdict."""
     from turbopolar_amd import _lib
 
     L = _lib.lib()
     flag = torch.zeros(1, dtype=torch.int32, device=device) if mode == 1 else torch.zeros(1, dtype=torch.int32, pin_memory=True)
     tail_k = torch.zeros((8, 64, 128), dtype=torch.float16, device=device)
     tail_v = torch.zeros_like(tail_k)
-    k = torch.randn((8, 1, 128), dtype=torch.float16, device=device)
+    k = torch.randn((8, tokens, 128), dtype=torch.float16, device=device)
     v = torch.randn_like(k)
     stream = torch.cuda.current_stream(device).cuda_stream
 
     def stage(kk, epoch):
-        return L.tp_append_stage(kk.data_ptr(), v.data_ptr(), 0, 8, 1, 0, 1, tail_k.data_ptr(), tail_v.data_ptr(),
+        return L.tp_append_stage(kk.data_ptr(), v.data_ptr(), 0, 8, tokens, 0, 1, tail_k.data_ptr(), tail_v.data_ptr(),
                                  64, 0, mode, flag.data_ptr(), epoch, stream)
 
-    assert stage(k, 1) == _lib.TP_OK
+    assert stage(k, 2) == _lib.TP_OK
     bad = k.clone()
-    bad[3, 0, 77] = float("nan")
-    assert stage(bad, 2) == _lib.TP_ERR_NONFINITE
-    assert stage(k, 3) == _lib.TP_OK  # the flag still holds epoch 2
+    bad[3, tokens - 1, 77] = float("nan")
+    assert stage(bad, 4) == _lib.TP_ERR_NONFINITE
+    assert stage(k, 6) == _lib.TP_OK  # the flag still holds the last verdict
+    assert stage(bad, 8) == _lib.TP_ERR_NONFINITE
+    assert stage(k, 10) == _lib.TP_OK
     assert torch.equal(tail_k[:, 0], k[:, 0])

@@ -137,6 +137,12 @@ def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def raw_stream(device_index: int) -> int:
+    """The current stream of a device as a raw handle, without building a
+    torch Stream object (the hot append path calls this once per token)."""
+    return torch._C._cuda_getCurrentRawStream(device_index)
+
+
 def require_hip(t: torch.Tensor, name: str) -> None:
     if not t.is_cuda:
         raise RuntimeError(

@@ -64,9 +64,16 @@ __global__ __launch_bounds__(256) void append_stage_kernel(AppendArgs a) {
       reinterpret_cast<uint4*>(a.tail_v)[dst] = vw;
     }
   }
-  if (bad) {  // every writer stores the same value
+  if (a.check == 2 && gridDim.x == 1) {
+    // One workgroup: it reports completion itself, epoch (all finite) or
+    // epoch + 1, once every thread's copies are issued and its verdict known;
+    // the host polls the pinned word instead of synchronising the stream.
+    const bool any_bad = __syncthreads_or(bad);
+    if (threadIdx.x == 0)
+      __hip_atomic_store(a.flag, any_bad ? a.epoch + 1u : a.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  } else if (bad) {  // every writer stores the same value
     if (a.check == 2)
-      __hip_atomic_store(a.flag, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);  // pinned host flag
+      __hip_atomic_store(a.flag, a.epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);  // pinned host flag
     else
       *a.flag = a.epoch;
   }
@@ -97,8 +104,8 @@ int32_t tp_append_stage(const void* k, const void* v, int32_t in_dtype, int64_t 
               (long long)tail_tokens);
     return TP_ERR_INVALID;
   }
-  if (check < 0 || check > 2 || (check && !flag)) {
-    set_error("check must be 0, 1 (device flag) or 2 (pinned host flag), with a flag when checking");
+  if (check < 0 || check > 2 || (check && !flag) || (check == 2 && (epoch & 1u))) {
+    set_error("check must be 0, 1 (device flag) or 2 (pinned host flag, even epoch), with a flag when checking");
     return TP_ERR_INVALID;
   }
   const uintptr_t al = (uintptr_t)k | (uintptr_t)v | (uintptr_t)tail_k | (uintptr_t)tail_v;
@@ -129,15 +136,34 @@ int32_t tp_append_stage(const void* k, const void* v, int32_t in_dtype, int64_t 
     hipLaunchKernelGGL(append_stage_kernel<false>, dim3(blocks), dim3(256), 0, s, a);
   int32_t st = launch_status("tp_append_stage");
   if (st != TP_OK || !check) return st;
-  uint32_t verdict = 0;
-  if (check == 2) {  // the kernel wrote the host flag directly: one synchronisation, no copy
-    if (hipStreamSynchronize(s) != hipSuccess) {
-      set_error("tp_append_stage: synchronising the stream failed");
-      return TP_ERR_HIP;
+  if (check == 2) {  // the kernel writes the pinned host flag directly, no copy
+    volatile uint32_t* vf = reinterpret_cast<volatile uint32_t*>(flag);
+    uint32_t verdict = 0;
+    bool done = false;
+    if (blocks == 1) {
+      // Poll for the workgroup's completion word (bounded; a launch that has
+      // not reported by then is waited for the ordinary way).
+      for (int spin = 0; spin < (1 << 22) && !done; ++spin) {
+        verdict = *vf;
+        done = verdict == epoch || verdict == epoch + 1u;
+      }
     }
-    verdict = *reinterpret_cast<volatile uint32_t*>(flag);
-  } else if (hipMemcpyAsync(&verdict, flag, sizeof(verdict), hipMemcpyDeviceToHost, s) != hipSuccess ||
-             hipStreamSynchronize(s) != hipSuccess) {
+    if (!done) {
+      if (hipStreamSynchronize(s) != hipSuccess) {
+        set_error("tp_append_stage: synchronising the stream failed");
+        return TP_ERR_HIP;
+      }
+      verdict = *vf;
+    }
+    if (verdict == epoch + 1u) {
+      set_error("append() inputs must contain finite values");
+      return TP_ERR_NONFINITE;
+    }
+    return TP_OK;
+  }
+  uint32_t verdict = 0;
+  if (hipMemcpyAsync(&verdict, flag, sizeof(verdict), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess) {
     set_error("tp_append_stage: reading the verdict failed");
     return TP_ERR_HIP;
   }

@@ -215,13 +215,21 @@ class TurboPolarKVCacheRuntime:
 
     def _stage(self, k, v, begin: int, n: int, dst: int, check: bool) -> None:
         B, H, T, _ = k.shape
-        self._epoch = self._epoch % 0xFFFFFFFE + 1
-        with torch.cuda.device(k.device):
+        # Even epochs: the staging kernel reports epoch (finite) or epoch + 1.
+        self._epoch = ((self._epoch + 2) & 0xFFFFFFFE) or 2
+        idx = k.device.index
+        prev = torch.cuda.current_device()
+        if prev != idx:
+            torch.cuda.set_device(idx)
+        try:
             st = _lib.lib().tp_append_stage(
                 k.data_ptr(), v.data_ptr(), 1 if k.dtype == torch.float32 else 0, B * H, T, begin, n,
                 self._tail_k.data_ptr(), self._tail_v.data_ptr(), PAGE, dst, 2 if check else 0,
-                self._flag.data_ptr(), self._epoch, _lib.stream_of(k.device),
+                self._flag.data_ptr(), self._epoch, _lib.raw_stream(idx),
             )
+        finally:
+            if prev != idx:
+                torch.cuda.set_device(prev)
         if st == _lib.TP_ERR_NONFINITE:
             raise ValueError("append() inputs must contain finite values")
         _lib.check(st, "tp_append_stage")
