@@ -139,8 +139,35 @@ def stream_of(device: torch.device) -> int:
 
 def raw_stream(device_index: int) -> int:
     """The current stream of a device as a raw handle, without building a
-    torch Stream object (the hot append path calls this once per token)."""
+    torch Stream object (the hot paths call this once per launch)."""
     return torch._C._cuda_getCurrentRawStream(device_index)
+
+
+def stream_handle(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
+
+
+class on_device:
+    """Makes ``device`` current for a launch, switching only when another
+    device is current (a cheaper torch.cuda.device for the per-token paths)."""
+
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, device: torch.device):
+        self.idx = device.index if device.index is not None else torch.cuda.current_device()
+        self.prev = self.idx
+
+    def __enter__(self):
+        self.prev = torch.cuda.current_device()
+        if self.prev != self.idx:
+            torch.cuda.set_device(self.idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev != self.idx:
+            torch.cuda.set_device(self.prev)
+        return False
 
 
 def require_hip(t: torch.Tensor, name: str) -> None:

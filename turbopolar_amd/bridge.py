@@ -25,6 +25,18 @@ from .kernels import PageSet, decode_attention, fp16_scale, fused_qk
 from .payload import PolarKeyBlock, QuantizedVBlock
 
 
+def _pages_of(block: PolarKeyBlock, quant_v: Optional[QuantizedVBlock], head_dim: int) -> PageSet:
+    """PageSet of a key block and its values, kept on the block object: the
+    runtime hands the same block objects to every decode step until a page is
+    added, so the descriptors are built once per page, not once per step."""
+    hit = block.__dict__.get("_tp_pages")
+    if hit is not None and hit[0] is quant_v and hit[1] == head_dim:
+        return hit[2]
+    pages = PageSet(block, quant_v, head_dim)
+    block.__dict__["_tp_pages"] = (quant_v, head_dim, pages)
+    return pages
+
+
 class HipKernelBridge:
     """Process-wide singleton, like the reference bridge (metal.py:72-86)."""
 
@@ -69,7 +81,7 @@ class HipKernelBridge:
     ) -> Tuple[torch.Tensor, Dict[str, Any]]:
         self._no_qjl(use_qjl)
         self._supports_block(block)
-        pages = PageSet(block, quant_v, config.head_dim)
+        pages = _pages_of(block, quant_v, config.head_dim)
         out = decode_attention(q, pages, None, None, actual_seq_len, fp16_scale(config.attention_scale))
         trace = {
             "kernel_name": "tqpolar_online_attention_quant_v",
@@ -100,7 +112,7 @@ class HipKernelBridge:
         pages = None
         if block is not None:
             self._supports_block(block)
-            pages = PageSet(block, quant_v, config.head_dim)
+            pages = _pages_of(block, quant_v, config.head_dim)
         tail_len = int(tail_k.shape[2]) if tail_k is not None else 0
         out = decode_attention(
             q, pages, tail_k if tail_len else None, tail_v if tail_len else None,

@@ -91,7 +91,7 @@ class TurboPolarFastCache:
         if block is None and tail_k is None:
             raise RuntimeError("TurboPolar cache returned no blocks after append")
         q_squeezed = q.squeeze(2)
-        cfg = dataclasses.replace(self.config, attention_scale=scale)
+        cfg = self._config_for_scale(scale)
         if block is not None and quant_v is None:
             raise RuntimeError("Fused attention requires kv_quant storage mode")
         if tail_k is not None and tail_k.shape[2] > 0:
@@ -103,6 +103,15 @@ class TurboPolarFastCache:
                 q_squeezed, block, quant_v, None, None, cfg, actual_seq_len, False
             )
         return out
+
+    def _config_for_scale(self, scale: float) -> TurboPolarConfig:
+        """The config with attention_scale = scale (turbopolar_fast_attention.py:147),
+        built once per scale value."""
+        hit = self.__dict__.get("_scaled_config")
+        if hit is None or hit[0] != scale or hit[1] is not self.config:
+            hit = (scale, self.config, dataclasses.replace(self.config, attention_scale=scale))
+            self.__dict__["_scaled_config"] = hit
+        return hit[2]
 
     def size(self) -> int:
         return self.offset

@@ -13,7 +13,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import TPPages, check, lib, ptr, require_hip, stream_of
+from ._lib import TPPages, check, lib, on_device, ptr, require_hip, stream_handle
 from .payload import PolarKeyBlock, QuantizedVBlock, layout_from_metadata
 
 PAGE = 64
@@ -177,10 +177,10 @@ def encode_pages(
     if D != HEAD_DIM:
         raise ValueError(f"head_dim must be {HEAD_DIM}, got {D}")
     in_dtype = 1 if ref.dtype == torch.float32 else 0
-    with torch.cuda.device(ref.device):
+    with on_device(ref.device):
         st = lib().tp_encode_pages(
             ptr(k), ptr(v), in_dtype, B * H, T, int(token_begin), int(n_tokens),
-            ctypes.byref(layout), ctypes.byref(pages), int(page_begin), stream_of(ref.device),
+            ctypes.byref(layout), ctypes.byref(pages), int(page_begin), stream_handle(ref.device),
         )
     check(st, "tp_encode_pages")
 
@@ -192,9 +192,9 @@ def decode_pages(pageset: PageSet, want_k: bool = True, want_v: bool = True):
     k_out = torch.empty((B, H, S * PAGE, HEAD_DIM), dtype=torch.float16, device=dev) if want_k else None
     v_out = torch.empty((B, H, S * PAGE, HEAD_DIM), dtype=torch.float16, device=dev) if want_v else None
     layout = getattr(pageset, "layout", _lib.make_layout(False, 4, 4, 64))
-    with torch.cuda.device(dev):
+    with on_device(dev):
         st = lib().tp_decode_pages(
-            ctypes.byref(layout), ctypes.byref(pageset.pages), B * H, 0, S, ptr(k_out), ptr(v_out), stream_of(dev)
+            ctypes.byref(layout), ctypes.byref(pageset.pages), B * H, 0, S, ptr(k_out), ptr(v_out), stream_handle(dev)
         )
     check(st, "tp_decode_pages")
     return k_out, v_out
@@ -214,10 +214,10 @@ def fused_qk(q: torch.Tensor, pageset: PageSet, scale: float) -> torch.Tensor:
     if B != pageset.B or Hq % pageset.H:
         raise ValueError(f"q heads {Hq} / batch {B} do not match kv pages {pageset.B}x{pageset.H}")
     scores = torch.empty((B, Hq, pageset.S * PAGE), dtype=torch.float16, device=q16.device)
-    with torch.cuda.device(q16.device):
+    with on_device(q16.device):
         st = lib().tp_fused_qk(
             ptr(q16), B, Hq, pageset.H, ctypes.byref(pageset.layout), ctypes.byref(pageset.pages),
-            pageset.S, float(scale), ptr(scores), stream_of(q16.device),
+            pageset.S, float(scale), ptr(scores), stream_handle(q16.device),
         )
     check(st, "tp_fused_qk")
     return scores
@@ -231,7 +231,7 @@ class _Workspace:
 
     @classmethod
     def get(cls, device: torch.device, nbytes: int) -> torch.Tensor:
-        key = (device.index, stream_of(device))
+        key = (device.index, stream_handle(device))
         buf = cls._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
             buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
@@ -289,11 +289,11 @@ def decode_attention(
     ws = _Workspace.get(dev, need)
     layout = pageset.layout if pageset is not None else _lib.make_layout(False, 4, 4, 64)
     pages = pageset.pages if pageset is not None else TPPages()
-    with torch.cuda.device(dev):
+    with on_device(dev):
         st = L.tp_decode_attention(
             ptr(q16), B, Hq, Hkv, ctypes.byref(layout), ctypes.byref(pages), n_pages,
             ptr(tk), ptr(tv), tail_len, tail_stride, int(actual_seq_len), float(scale), pps,
-            ws.data_ptr(), ws.numel(), ptr(out), stream_of(dev),
+            ws.data_ptr(), ws.numel(), ptr(out), stream_handle(dev),
         )
     check(st, "tp_decode_attention")
     return out

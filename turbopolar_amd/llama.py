@@ -108,18 +108,33 @@ def make_turbo_cache(model, config: Optional[TurboPolarConfig] = None) -> TurboP
     return TurboPolarCache([TurboPolarFastCache(config) for _ in range(n_layers)])
 
 
+_mask_verdict = None  # (mask, its version, seq_len, cache_len, verdict) of the last check
+
+
 def _is_standard_causal_mask(mask: Optional[torch.Tensor], seq_len: int, cache_len: int) -> bool:
     """True for no mask or the full-history causal mask ``[1, 1, seq_len, cache_len]``
     (turbopolar_fast_attention.py:235-244), boolean (True = attend) or additive
     (0 = attend).  Query i (at position cache_len - seq_len + i) sees keys
-    0 .. cache_len - seq_len + i."""
+    0 .. cache_len - seq_len + i.
+
+    A forward pass hands the same mask tensor to every layer; the verdict is
+    kept for that tensor (held, so its memory cannot be reused, and keyed on
+    its version counter, so an in-place change is seen), which makes the
+    comparison, a device-to-host read, once per forward instead of once per
+    layer."""
+    global _mask_verdict
     if mask is None:
         return True
     if tuple(mask.shape) != (1, 1, seq_len, cache_len):
         return False
+    hit = _mask_verdict
+    if hit is not None and hit[0] is mask and hit[1] == mask._version and hit[2] == seq_len and hit[3] == cache_len:
+        return hit[4]
     allowed = mask[0, 0] if mask.dtype == torch.bool else mask[0, 0] == 0
     expected = torch.ones((seq_len, cache_len), dtype=torch.bool, device=mask.device).tril(cache_len - seq_len)
-    return bool(torch.equal(allowed, expected))
+    ok = bool(torch.equal(allowed, expected))
+    _mask_verdict = (mask, mask._version, seq_len, cache_len, ok)
+    return ok
 
 
 _orig_llama_attention_forward = None

@@ -54,6 +54,7 @@ class TurboPolarKVCacheRuntime:
         self._tail_v: Optional[torch.Tensor] = None
         self._tail_len = 0
         self._flag: Optional[torch.Tensor] = None  # tp_append_stage verdict (pinned host memory)
+        self._fused_views = None  # (block_count, storage buffers, (PolarKeyBlock, QuantizedVBlock))
         self._epoch = 0
 
         self._initialized = False
@@ -271,11 +272,22 @@ class TurboPolarKVCacheRuntime:
         compressed_k = None
         quant_v = None
         if self.k_storage.block_count > 0:
-            L = self.config.block_size
-            compressed_k = self.k_storage.to_unified_block(
-                (self._batch_size, self._num_kv_heads, self.k_storage.block_count * L, self._head_dim)
-            )
-            quant_v = self.v_storage.to_quantized_block()
+            # The page views are rebuilt only when a page was added or the
+            # storage reallocated, so a decode step reuses them (and the device
+            # descriptors the bridge attaches to them).  The key holds the
+            # buffers themselves, so a freed buffer can never alias a new one.
+            bufs = (self.k_storage.radii, self.v_storage.codes)
+            key = self.k_storage.block_count
+            hit = self._fused_views
+            if hit is not None and hit[0] == key and hit[1][0] is bufs[0] and hit[1][1] is bufs[1]:
+                compressed_k, quant_v = hit[2]
+            else:
+                L = self.config.block_size
+                compressed_k = self.k_storage.to_unified_block(
+                    (self._batch_size, self._num_kv_heads, self.k_storage.block_count * L, self._head_dim)
+                )
+                quant_v = self.v_storage.to_quantized_block()
+                self._fused_views = (key, bufs, (compressed_k, quant_v))
         return compressed_k, quant_v, self.partial_k, self.partial_v, None, self.actual_seq_len
 
     def _maybe_encode_partial(self) -> Optional[Dict[str, Any]]:
