@@ -467,6 +467,53 @@ def run_append(args, layout, n_appends: int = 4096) -> dict:
     return {"us_per_append": dt / n_appends * 1e6, "appends": n_appends, "pages": rt.total_blocks}
 
 
+def run_snapshot(args, layout, reps: int = 3) -> dict:
+    """Page snapshot (turbopolar_amd.wire) of a full cache: device-to-host
+    state_dict, safetensors write and read back onto the device.  Not a
+    reference workload (the reference has no on-disk format)."""
+    import tempfile
+
+    import torch
+
+    from turbopolar_amd import TurboPolarConfig, TurboPolarKVCacheRuntime, wire
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    int8, l1b, deepb, split = layout
+    cfg = TurboPolarConfig(num_q_heads=args.hq, num_kv_heads=args.hkv, use_int8_radii=int8,
+                           k_angle_bits_level1=l1b, k_angle_bits_deep=deepb, split_dim=split)
+    g = torch.Generator(device=dev).manual_seed(5)
+    rt = TurboPolarKVCacheRuntime(cfg)
+    n = args.context + 37  # full pages plus a dense tail
+    rt.append(torch.randn((1, args.hkv, n, 128), generator=g, device=dev).half(),
+              torch.randn((1, args.hkv, n, 128), generator=g, device=dev).half())
+    torch.cuda.synchronize()
+    t_state, t_save, t_load = [], [], []
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "cache.safetensors")
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            tensors, meta = wire.state_dict(rt)
+            t_state.append(time.perf_counter() - t0)
+            t0 = time.perf_counter()
+            wire.save(rt, path)
+            t_save.append(time.perf_counter() - t0)
+            t0 = time.perf_counter()
+            back = wire.load(path, dev)
+            torch.cuda.synchronize()
+            t_load.append(time.perf_counter() - t0)
+        file_bytes = os.path.getsize(path)
+    S = rt.k_storage.block_count
+    same = all(torch.equal(x[:, :, :S], y[:, :, :S]) for x, y in (
+        (rt.k_storage.radii, back.k_storage.radii), (rt.k_storage.angle_codes_deep, back.k_storage.angle_codes_deep),
+        (rt.v_storage.codes, back.v_storage.codes), (rt.v_storage.scales, back.v_storage.scales)))
+    same = same and torch.equal(rt.partial_k, back.partial_k)
+    payload = sum(t.numel() * t.element_size() for t in tensors.values())
+    return {"state_dict_ms": min(t_state) * 1e3, "save_ms": min(t_save) * 1e3, "load_ms": min(t_load) * 1e3,
+            "payload_bytes": payload, "file_bytes": file_bytes, "pages": S, "tail": rt._tail_len,
+            "identical": bool(same)}
+
+
 def copy_calibration(nbytes: int, reps: int = 10) -> None:
     """Plain device-to-device copy of a known size: the reference for scaling
     rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes."""
@@ -499,7 +546,7 @@ def main():
     ap.add_argument("--rotate", type=int, default=0, help="independent caches to rotate (0 = auto, >256 MB)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=["decode", "encode", "append", "layers", "model", "decompress"],
+    ap.add_argument("--workload", choices=["decode", "encode", "append", "layers", "model", "decompress", "snapshot"],
                     default="decode",
                     help="decode (the BASELINE metric, default); encode / append: configs[3] workloads; "
                          "layers: configs[1] (--layers decode launches per step); "
@@ -604,6 +651,18 @@ def main():
             "config": {"workload": f"{r['appends']} single-token appends of {args.hkv} kv heads "
                                    f"through TurboPolarKVCacheRuntime.append, {r['pages']} page encodes "
                                    f"(BASELINE configs[3])", "layout": args.layout},
+        }))
+        return
+    if args.workload == "snapshot":
+        r = run_snapshot(args, layout)
+        print(json.dumps({
+            "metric": "page snapshot save + load, Llama-3-8B kv shape",
+            "value": round(r["save_ms"] + r["load_ms"], 2), "unit": "ms", "n_gpus": 1,
+            "higher_is_better": False, "dtype": "u8/i8/f16", "data": "synthetic",
+            "breakdown": {k: round(r[k], 2) for k in ("state_dict_ms", "save_ms", "load_ms")},
+            "payload_bytes": r["payload_bytes"], "file_bytes": r["file_bytes"], "identical": r["identical"],
+            "config": {"workload": f"{r['pages']} pages + {r['tail']} tail tokens of {args.hkv} kv heads, "
+                                   f"safetensors file in a temporary directory", "layout": args.layout},
         }))
         return
     n_pages = args.context // 64
