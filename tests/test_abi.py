@@ -149,3 +149,30 @@ def test_append_stage_argument_validation():
         assert st == _lib.TP_ERR_INVALID and "flag" in msg
     L.tp_append_stage(4096, 8192, 0, 8, 1, 0, 1, 12288, 16384, 64, 0, 2, 20480, 3, None)
     assert "even epoch" in L.tp_last_error().decode()  # check 2 takes even epochs
+
+
+def test_integration_stub_matches_the_binding(monkeypatch):
+    """The ctypes stub that INTEGRATION.md offers to the reference declares the
+    same signatures and struct layouts as the package's own binding."""
+    import pathlib
+
+    doc = (pathlib.Path(_lib.__file__).parent.parent / "INTEGRATION.md").read_text()
+    blocks = re.findall(r"```python\n(.*?)```", doc, re.S)
+    stub = next(b for b in blocks if "class TPPages" in b)
+    real_cdll = ctypes.CDLL
+    monkeypatch.setattr(ctypes, "CDLL", lambda name, *a, **k: real_cdll(str(_lib.LIB_PATH), *a, **k))
+    ns = {}
+    exec(compile(stub, "INTEGRATION.md", "exec"), ns)
+    for struct_name in ("TPPageLayout", "TPPages"):
+        mine, theirs = getattr(_lib, struct_name), ns[struct_name]
+        assert [(n, t) for n, t in theirs._fields_] == [(n, t) for n, t in mine._fields_]
+        assert ctypes.sizeof(theirs) == ctypes.sizeof(mine)
+    for name in ("tp_decode_attention", "tp_decode_workspace_bytes"):
+        fn = getattr(ns["_lib"], name)
+        restype, argtypes = _lib._SIGNATURES[name]
+        assert fn.restype == restype
+        norm = [getattr(t, "_type_", t).__name__ if t.__name__.startswith("LP_") else t.__name__ for t in fn.argtypes]
+        want = [getattr(t, "_type_", t).__name__ if t.__name__.startswith("LP_") else t.__name__ for t in argtypes]
+        norm = ["tp_page_layout" if n == "TPPageLayout" else "tp_pages" if n == "TPPages" else n for n in norm]
+        want = ["tp_page_layout" if n == "TPPageLayout" else "tp_pages" if n == "TPPages" else n for n in want]
+        assert norm == want, name
