@@ -426,7 +426,60 @@ def run_encode(args, layout) -> dict:
     ms = t0.elapsed_time(t1) / args.steps
     kv_bytes = 2 * args.hkv * args.context * 128 * 2
     page_bytes = args.hkv * n_pages * (bench_page_bytes(layout))
-    return {"ms": ms, "read": kv_bytes, "write": page_bytes, "n_pages": n_pages}
+    k, v, bufs, codes, scales, _ = sets[0]
+    return {"ms": ms, "read": kv_bytes, "write": page_bytes, "n_pages": n_pages,
+            "set0": (k, v, bufs, codes, scales)}
+
+
+def cpu_encode_baseline(args, layout, set0, budget_s):
+    """Oracle restatement of the reference's page flush (encode_block +
+    quantize_block, encoder.py:24-98, v_quant/encoder.py:16-30) page by page
+    over the first input set, 1 thread, until ``budget_s`` seconds; each
+    sampled page is also compared with what the GPU wrote for it."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import oracle
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    int8, l1b, deepb, split = layout
+    k, v, bufs, codes, scales = set0
+    kn = k.cpu().numpy()
+    vn = v.cpu().numpy()
+    gpu = {name: t.cpu().numpy() for name, t in bufs.items() if t is not None}
+    codes_n, scales_n = codes.cpu().numpy(), scales.cpu().numpy()
+
+    def same(a, b):  # bitwise
+        return bool(np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8)))
+
+    times, exact = [], True
+    ctx = threadpool_limits(1) if threadpool_limits else None
+    try:
+        if ctx:
+            ctx.__enter__()
+        start = time.perf_counter()
+        p = 0
+        while p < args.context // 64:
+            ks, vs = kn[:, :, 64 * p:64 * (p + 1)], vn[:, :, 64 * p:64 * (p + 1)]
+            t0 = time.perf_counter()
+            blk = oracle.encode_block(ks, l1_bits=l1b, deep_bits=deepb, split_dim=split, use_int8_radii=int8)
+            vc, vsc = oracle.quantize_block(vs[:, :, None])
+            times.append(time.perf_counter() - t0)
+            exact &= same(blk["radii"], gpu["radii"][:, :, p])
+            exact &= same(blk["angle_codes_l1"], gpu["angle_codes_l1"][:, :, p])
+            exact &= same(blk["angle_codes_deep"], gpu["angle_codes_deep"][:, :, p])
+            if blk["radii_scales"] is not None:
+                exact &= same(blk["radii_scales"].reshape(-1), gpu["radii_scales"][:, :, p].reshape(-1))
+            exact &= same(vc[:, :, 0], codes_n[:, :, p]) and same(vsc[:, :, 0], scales_n[:, :, p])
+            p += 1
+            if time.perf_counter() - start > budget_s and len(times) >= 2:
+                break
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    per_page = float(np.median(times))
+    return per_page * (args.context // 64) * 1e6, len(times), exact
 
 
 def bench_page_bytes(layout) -> int:
@@ -628,6 +681,13 @@ def main():
         return
     if args.workload == "encode":
         r = run_encode(args, layout)
+        cpu = None
+        if not args.no_cpu:
+            cpu_us, nsamp, exact = cpu_encode_baseline(args, layout, r["set0"], args.cpu_budget)
+            cpu = {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
+                   "sample": f"{nsamp} of {r['n_pages']} page flushes of {args.hkv} kv heads (oracle NumPy "
+                             f"restatement of encode_block + quantize_block, 1 thread; median per page x "
+                             f"{r['n_pages']}; sampled pages bit-exact vs GPU: {exact})"}
         nbytes = r["read"] + r["write"]
         gbps = nbytes / (r["ms"] * 1e-3) / 1e9
         print(json.dumps({
@@ -640,6 +700,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
             "algorithmic_bytes_per_step": {"read": r["read"], "write": r["write"]},
+            "cpu_baseline": cpu,
         }))
         return
     if args.workload == "append":
