@@ -610,6 +610,57 @@ __device__ __forceinline__ void merge_groups(const float4v* red, const float2* r
   Mc = Mx;
 }
 
+// Online fold of records 0 .. mine-1 (record r at pml + 2*SG*r, pac + r*rstride)
+// in batches of B, all B + 1 loads of a batch in flight together: a record
+// past `mine` rereads the last one and is then given weight 0, so the loads
+// are unconditional.  Records and states with m = -inf weigh 0 (NaN they carry
+// survives).
+template <int B>
+__device__ __forceinline__ void fold_records(const float* pml, const float* pac, int SG, int64_t rstride, int mine,
+                                             float& Mc, float& Lc, float4v& Ac) {
+  // The 32 lanes of each half wave share (head, split group) and `mine` (nh * 32
+  // items in whole halves), so one load per batch fetches the B (m, l) pairs,
+  // lane k of the half holding record k, and lane permutes within the half,
+  // whose lanes are all active or all idle, hand them to every lane.
+  const int lane = threadIdx.x & 63;
+  const int half_base = (lane & 32) * 4;  // byte address of lane 0 of this half
+  for (int r0 = 0; r0 < mine; r0 += B) {
+    float2 r[B];
+    float4v x[B];
+    const float2 mlk = *reinterpret_cast<const float2*>(pml + 2 * SG * min(r0 + (lane & (B - 1)), mine - 1));
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int ru = min(r0 + u, mine - 1);
+      x[u] = *reinterpret_cast<const float4v*>(pac + ru * rstride);
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      r[u].x = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(half_base + 4 * u, __builtin_bit_cast(int, mlk.x)));
+      r[u].y = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(half_base + 4 * u, __builtin_bit_cast(int, mlk.y)));
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      if (r0 + u >= mine) {
+        r[u] = make_float2(-INFINITY, 0.0f);
+        x[u] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    }
+    float Mn = Mc;
+#pragma unroll
+    for (int u = 0; u < B; ++u) Mn = fmaxf(Mn, r[u].x);
+    const float w0 = Mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mc - Mn);
+    Lc *= w0;
+    Ac *= w0;
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const float w = r[u].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r[u].x - Mn);
+      Lc += r[u].y * w;
+      Ac += x[u] * w;
+    }
+    Mc = Mn;
+  }
+}
+
 template <int WAVES>
 struct AttnShared {
   Lut lut;
@@ -786,8 +837,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   // Items are (head hh, 4-dim chunk c4), nh * 32 of them, padded to a power
   // of two 2^ish; thread (item, sg), sg < SG = 512 / 2^ish, folds splits
   // sg, sg + SG, ... online (running max, rescaled sums), with all loads of a
-  // batch of 8 records in flight together; the SG partial folds then meet in
-  // LDS and are merged in sg order.
+  // batch of records in flight together (batches of 4 when no thread has more
+  // than 4 records, else 8: every load of a batch costs load bandwidth of the
+  // one CU that combines); the SG partial folds then meet in LDS and are
+  // merged in sg order.
   const int n_items = nh * 32;
   const int ish = n_items <= 32 ? 5 : (n_items <= 64 ? 6 : (n_items <= 128 ? 7 : (n_items <= 256 ? 8 : 9)));
   const int lsg = 9 - ish;
@@ -803,39 +856,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   const int64_t rstride = (int64_t)SG * 16 * kHeadDim;
   float Mc = -INFINITY, Lc = 0.0f;
   float4v Ac = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int r0 = 0; r0 < mine; r0 += 8) {
-    float2 r[8];
-    float4v x[8];
-    // Unconditional loads (a record past `mine` rereads the last one and is
-    // then given weight 0), so all 16 are in flight before the first use.
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int ru = min(r0 + u, mine - 1);
-      r[u] = *reinterpret_cast<const float2*>(pml + 2 * SG * ru);
-      x[u] = *reinterpret_cast<const float4v*>(pac + ru * rstride);
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (r0 + u >= mine) {
-        r[u] = make_float2(-INFINITY, 0.0f);
-        x[u] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-    }
-    float Mn = Mc;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) Mn = fmaxf(Mn, r[u].x);
-    // Records and states with m = -inf weigh 0 (NaN they carry survives).
-    const float w0 = Mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mc - Mn);
-    Lc *= w0;
-    Ac *= w0;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float w = r[u].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r[u].x - Mn);
-      Lc += r[u].y * w;
-      Ac += x[u] * w;
-    }
-    Mc = Mn;
-  }
+  if (((S + SG - 1) >> lsg) <= 4)
+    fold_records<4>(pml, pac, SG, rstride, mine, Mc, Lc, Ac);
+  else
+    fold_records<8>(pml, pac, SG, rstride, mine, Mc, Lc, Ac);
   if (SG > 1) {
     float4v* red = reinterpret_cast<float4v*>(&sh.acc[0][0]);
     float2* redml = reinterpret_cast<float2*>(red + (WAVES * 64));
