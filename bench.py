@@ -567,6 +567,17 @@ def run_snapshot(args, layout, reps: int = 3) -> dict:
             "identical": bool(same)}
 
 
+def profiled_traffic(name: str, args):
+    """HBM bytes per launch that the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary profiles/<name>_8b_32k_traffic.json records, when this run is that
+    workload (32k tokens, 32 q / 8 kv heads); else None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{name}_8b_32k_traffic.json")
+    if not (os.path.exists(path) and args.context == 32768 and args.hq == 32 and args.hkv == 8):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
 def copy_calibration(nbytes: int, reps: int = 10) -> None:
     """Plain device-to-device copy of a known size: the reference for scaling
     rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes."""
@@ -635,7 +646,7 @@ def main():
             "config": {"workload": f"tp_decode_pages: {r['n_pages']} pages x {args.hkv} kv heads -> dense fp16 K "
                                    f"and V ({args.context} tokens)", "layout": args.layout},
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(f"decompress_{args.layout}", args)},
             "algorithmic_bytes_per_step": {"read": r["read"], "write": r["write"]},
         }))
         return
@@ -698,7 +709,7 @@ def main():
             "config": {"workload": f"encode {args.context} fp16 tokens x {args.hkv} kv heads into "
                                    f"{r['n_pages']} pages (BASELINE configs[3])", "layout": args.layout},
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(f"encode_{args.layout}", args)},
             "algorithmic_bytes_per_step": {"read": r["read"], "write": r["write"]},
             "cpu_baseline": cpu,
         }))
