@@ -133,10 +133,6 @@ def ptr(t) -> int | None:
     return t.data_ptr()
 
 
-def stream_of(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
-
-
 def raw_stream(device_index: int) -> int:
     """The current stream of a device as a raw handle, without building a
     torch Stream object (the hot paths call this once per launch)."""
@@ -144,8 +140,8 @@ def raw_stream(device_index: int) -> int:
 
 
 def stream_handle(device: torch.device) -> int:
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    return torch._C._cuda_getCurrentRawStream(idx)
+    """raw_stream of ``device`` (its index, or the current device's)."""
+    return raw_stream(device.index if device.index is not None else torch.cuda.current_device())
 
 
 class on_device:
