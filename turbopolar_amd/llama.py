@@ -23,7 +23,7 @@ path works, and tests use randomly initialised models.
 
 from __future__ import annotations
 
-from typing import List, Optional, Sequence
+from typing import Optional, Sequence
 
 import torch
 
@@ -192,7 +192,3 @@ def unpatch_llama_attention(model=None) -> None:
 
 def is_patched() -> bool:
     return _llama.LlamaAttention.forward is _turbo_llama_attention_forward
-
-
-def caches_of(cache: TurboPolarCache) -> List[TurboPolarFastCache]:
-    return [layer.fast for layer in cache.layers]
