@@ -176,3 +176,17 @@ def test_empty_cache_cannot_be_saved():
         wire.state_dict(rt)
     with pytest.raises(TypeError):
         wire.state_dict(object())
+
+
+def test_snapshot_shares_no_memory_with_the_cache():
+    """A full-capacity cache has contiguous page slices: the snapshot must
+    still copy them, so later changes to the cache leave it alone."""
+    rt = _filled_runtime("default", 4, 3)
+    assert rt.k_storage.capacity == 4  # the [:, :, :4] slices are the whole buffers
+    tensors, _ = wire.state_dict(rt)
+    before = {k: v.clone() for k, v in tensors.items()}
+    rt.k_storage.radii.zero_()
+    rt.v_storage.codes.fill_(7)
+    rt._tail_k.zero_()
+    for k, v in tensors.items():
+        assert torch.equal(v, before[k]), k

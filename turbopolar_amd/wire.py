@@ -59,6 +59,16 @@ def _runtime_of(cache) -> TurboPolarKVCacheRuntime:
     return rt
 
 
+def _host_copy(t: torch.Tensor) -> torch.Tensor:
+    """A host copy that shares no memory with ``t``: device tensors go to
+    pinned memory asynchronously (the caller synchronises once)."""
+    if t.is_cuda:
+        out = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+        out.copy_(t, non_blocking=True)
+        return out
+    return t.clone(memory_format=torch.contiguous_format)
+
+
 def state_dict(cache) -> Tuple[Dict[str, torch.Tensor], Dict[str, str]]:
     """(tensors on the host, string metadata) of a runtime or fast cache."""
     rt = _runtime_of(cache)
@@ -68,18 +78,21 @@ def state_dict(cache) -> Tuple[Dict[str, torch.Tensor], Dict[str, str]]:
     tensors: Dict[str, torch.Tensor] = {}
     if S:
         ks, vs = rt.k_storage, rt.v_storage
-        tensors["k.radii"] = ks.radii[:, :, :S].contiguous().cpu()
+        tensors["k.radii"] = _host_copy(ks.radii[:, :, :S])
         if ks.radii_scales is not None:
-            tensors["k.radii_scales"] = ks.radii_scales[:, :, :S].contiguous().cpu()
+            tensors["k.radii_scales"] = _host_copy(ks.radii_scales[:, :, :S])
         if ks.angle_codes_l1.shape[-1]:
-            tensors["k.angle_l1"] = ks.angle_codes_l1[:, :, :S].contiguous().cpu()
+            tensors["k.angle_l1"] = _host_copy(ks.angle_codes_l1[:, :, :S])
         if ks.angle_codes_deep.shape[-1]:
-            tensors["k.angle_deep"] = ks.angle_codes_deep[:, :, :S].contiguous().cpu()
-        tensors["v.codes"] = vs.codes[:, :, :S].contiguous().cpu()
-        tensors["v.scales"] = vs.scales[:, :, :S].contiguous().cpu()
+            tensors["k.angle_deep"] = _host_copy(ks.angle_codes_deep[:, :, :S])
+        tensors["v.codes"] = _host_copy(vs.codes[:, :, :S])
+        tensors["v.scales"] = _host_copy(vs.scales[:, :, :S])
     if rt._tail_len:
-        tensors["tail.k"] = rt.partial_k.contiguous().cpu()
-        tensors["tail.v"] = rt.partial_v.contiguous().cpu()
+        tensors["tail.k"] = _host_copy(rt.partial_k)
+        tensors["tail.v"] = _host_copy(rt.partial_v)
+    devices = {t.device for t in (rt.k_storage.radii, rt._tail_k) if t is not None and t.is_cuda}
+    for d in devices:
+        torch.cuda.synchronize(d)
     meta = {
         "format": FORMAT,
         "version": str(VERSION),
