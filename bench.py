@@ -372,7 +372,157 @@ def run_decompress(args, layout) -> dict:
     ms = t0.elapsed_time(t1) / args.steps
     read = algorithmic_bytes(args.hq, args.hkv, n_pages, layout) - args.hq * 128 * 4
     write = 2 * k_out.numel() * 2
-    return {"ms": ms, "read": read, "write": write, "n_pages": n_pages}
+    step(0)  # the outputs of cache 0, for the CPU baseline's check
+    torch.cuda.synchronize()
+    return {"ms": ms, "read": read, "write": write, "n_pages": n_pages, "cache0": caches[0], "k_out": k_out,
+            "v_out": v_out}
+
+
+def _f16_ulp_gap(a, b) -> int:
+    """Largest distance in fp16 ulps between finite elements of a and b."""
+    def ordered(x):
+        bits = x.view(np.int16).astype(np.int32)
+        return np.where(bits < 0, -(bits & 0x7FFF), bits)
+    fin = np.isfinite(a) & np.isfinite(b)
+    return int(np.max(np.abs(ordered(a) - ordered(b))[fin], initial=0))
+
+
+def cpu_decompress_baseline(args, r, budget_s):
+    """Oracle restatement of decompress-on-read (decode_block +
+    dequantize_block, decoder.py:7-67, v_quant/encoder.py:32-38) page by page,
+    1 thread, until ``budget_s`` seconds; each sampled page is compared with
+    the GPU's dense K (ulps) and V (bitwise)."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import oracle
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    c = r["cache0"]
+    t = c["pages"].tensors
+    radii, l1, deep = (t[n].cpu().numpy() for n in ("radii", "angle_l1", "angle_deep"))
+    rs = t["radii_scales"].cpu().numpy() if "radii_scales" in t else None
+    codes, scales = t["v_codes"].cpu().numpy(), t["v_scales"].cpu().numpy()
+    meta = c["rt"].k_storage.metadata
+    kg, vg = r["k_out"].cpu().numpy(), r["v_out"].cpu().numpy()
+    times, v_exact, k_ulps = [], True, 0
+    ctx = threadpool_limits(1) if threadpool_limits else None
+    try:
+        if ctx:
+            ctx.__enter__()
+        start = time.perf_counter()
+        for p in range(r["n_pages"]):
+            sl = slice(p, p + 1)
+            t0 = time.perf_counter()
+            k = oracle.decode_block(radii[:, :, sl], rs[:, :, sl] if rs is not None else None, l1[:, :, sl],
+                                    deep[:, :, sl], meta)
+            v = oracle.dequantize_block(codes[:, :, sl], scales[:, :, sl])
+            times.append(time.perf_counter() - t0)
+            tok = slice(64 * p, 64 * (p + 1))
+            v_exact &= bool(np.array_equal(v.reshape(vg[:, :, tok].shape).view(np.uint16), vg[:, :, tok].view(np.uint16)))
+            k_ulps = max(k_ulps, _f16_ulp_gap(k, kg[:, :, tok]))
+            if time.perf_counter() - start > budget_s and len(times) >= 2:
+                break
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    return float(np.median(times)) * r["n_pages"] * 1e6, len(times), v_exact, k_ulps
+
+
+def k_page_bytes(layout) -> int:
+    """Compressed K bytes of one page of one kv head (radii, angle codes, radius scale)."""
+    return bench_page_bytes(layout) - 64 * 136
+
+
+def run_fused_qk(args, layout) -> dict:
+    """tp_fused_qk (execute_fused_qk, metal.py:494-530) over every page of the
+    cache: fp16 scores of all query heads for all S*64 slots, one launch per
+    step, rotating caches as the decode line does."""
+    import torch
+
+    from turbopolar_amd import _lib
+    from turbopolar_amd.kernels import fp16_scale
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    k_bytes = args.hkv * (args.context // 64) * k_page_bytes(layout)
+    args.rotate = max(4, int(np.ceil(320e6 / k_bytes)))  # more than the Infinity Cache holds
+    cfg, caches = build_caches(args, dev, layout)
+    L = _lib.lib()
+    n_pages = caches[0]["pages"].S
+    scores = torch.empty((1, args.hq, n_pages * 64), dtype=torch.float16, device=dev)
+    scale = fp16_scale(cfg.attention_scale)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def step(i):
+        c = caches[i % len(caches)]
+        ps = c["pages"]
+        st = L.tp_fused_qk(c["q"].data_ptr(), 1, args.hq, args.hkv, ctypes.byref(ps.layout), ctypes.byref(ps.pages),
+                           n_pages, scale, scores.data_ptr(), stream)
+        if st:
+            _lib.check(st, "tp_fused_qk")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(args.steps):
+        step(i)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    step(0)
+    torch.cuda.synchronize()
+    read = args.hkv * n_pages * k_page_bytes(layout) + args.hq * 128 * 2
+    write = args.hq * n_pages * 64 * 2
+    return {"ms": ms, "read": read, "write": write, "n_pages": n_pages, "cache0": caches[0], "scores": scores,
+            "scale": scale, "n_caches": len(caches)}
+
+
+def cpu_qk_baseline(args, r, budget_s):
+    """Oracle restatement of _cpu_fused_qk (metal.py:254-260) over the whole
+    cache in float32, 1 thread, repeated until ``budget_s`` seconds; compared
+    with the GPU scores by the reference's own QK test bar (max-abs, cosine)."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import oracle
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    c = r["cache0"]
+    t = c["pages"].tensors
+    blk = {"radii": t["radii"].cpu().numpy(),
+           "radii_scales": t["radii_scales"].cpu().numpy() if "radii_scales" in t else None,
+           "angle_codes_l1": t["angle_l1"].cpu().numpy(), "angle_codes_deep": t["angle_deep"].cpu().numpy(),
+           "metadata": c["rt"].k_storage.metadata}
+    S = r["n_pages"]
+    for n in ("radii", "radii_scales", "angle_codes_l1", "angle_codes_deep"):
+        if blk[n] is not None:
+            blk[n] = blk[n][:, :, :S]
+    q = c["q"].cpu().numpy()
+    times = []
+    ctx = threadpool_limits(1) if threadpool_limits else None
+    try:
+        if ctx:
+            ctx.__enter__()
+        start = time.perf_counter()
+        while True:
+            t0 = time.perf_counter()
+            ref = oracle.cpu_fused_qk(q, blk, r["scale"], dtype=np.float32)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - start > budget_s and len(times) >= 2:
+                break
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    g = r["scores"].float().cpu().numpy().reshape(ref.shape)
+    err = float(np.max(np.abs(g - ref)))
+    cos = float(np.sum(g * ref) / (np.linalg.norm(g) * np.linalg.norm(ref)))
+    return float(np.median(times)) * 1e6, len(times), err, cos
 
 
 def run_encode(args, layout) -> dict:
@@ -610,7 +760,7 @@ def main():
     ap.add_argument("--rotate", type=int, default=0, help="independent caches to rotate (0 = auto, >256 MB)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=["decode", "encode", "append", "layers", "model", "decompress", "snapshot"],
+    ap.add_argument("--workload", choices=["decode", "encode", "append", "layers", "model", "decompress", "snapshot", "qk"],
                     default="decode",
                     help="decode (the BASELINE metric, default); encode / append: configs[3] workloads; "
                          "layers: configs[1] (--layers decode launches per step); "
@@ -636,6 +786,13 @@ def main():
         args.kind = "loguniform" if args.workload == "layers" else "outlier"
     if args.workload == "decompress":
         r = run_decompress(args, layout)
+        cpu = None
+        if not args.no_cpu:
+            cpu_us, nsamp, v_exact, k_ulps = cpu_decompress_baseline(args, r, args.cpu_budget)
+            cpu = {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
+                   "sample": f"{nsamp} of {r['n_pages']} pages of {args.hkv} kv heads (oracle NumPy restatement of "
+                             f"decode_block + dequantize_block, 1 thread; median per page x {r['n_pages']}; sampled "
+                             f"pages: V bit-exact {v_exact}, K within {k_ulps} fp16 ulp of the oracle)"}
         nbytes = r["read"] + r["write"]
         gbps = nbytes / (r["ms"] * 1e-3) / 1e9
         print(json.dumps({
@@ -648,6 +805,30 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(f"decompress_{args.layout}", args)},
             "algorithmic_bytes_per_step": {"read": r["read"], "write": r["write"]},
+            "cpu_baseline": cpu,
+        }))
+        return
+    if args.workload == "qk":
+        r = run_fused_qk(args, layout)
+        cpu = None
+        if not args.no_cpu:
+            cpu_us, nsamp, err, cos = cpu_qk_baseline(args, r, args.cpu_budget)
+            cpu = {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
+                   "sample": f"{nsamp} full steps over the {args.context}-token cache (oracle NumPy float32 "
+                             f"restatement of _cpu_fused_qk, 1 thread; GPU scores max-abs {err:.2e}, cosine {cos:.6f})"}
+        nbytes = r["read"] + r["write"]
+        gbps = nbytes / (r["ms"] * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": "fused QK us/step (scores of every query head over every cached token), Llama-3-8B shape",
+            "value": round(r["ms"] * 1e3, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(r["ms"], 6), "higher_is_better": False,
+            "dtype": "f16", "data": "synthetic",
+            "config": {"workload": f"tp_fused_qk: {args.hq} q / {args.hkv} kv heads, {r['n_pages']} pages "
+                                   f"({args.context} tokens), {r['n_caches']} rotating caches", "layout": args.layout},
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+            "algorithmic_bytes_per_step": {"read": r["read"], "write": r["write"]},
+            "cpu_baseline": cpu,
         }))
         return
     if args.workload == "model":
