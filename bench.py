@@ -728,6 +728,47 @@ def profiled_traffic(name: str, args):
         return json.load(f).get("hbm_bytes_per_launch")
 
 
+def cpu_append_baseline(args, layout, n_appends: int = 4096):
+    """Host restatement of the reference's append (turbo_polar_cache.py:106-126):
+    per single-token append a finiteness check of K and V, the tail
+    concatenation, and at 64 tokens the oracle's page flush (encode_block +
+    quantize_block); 1 thread, the same number of appends as the GPU line."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import oracle
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    int8, l1b, deepb, split = layout
+    rng = np.random.default_rng(3)
+    ks = rng.standard_normal((n_appends, 1, args.hkv, 1, 128)).astype(np.float16)
+    vs = rng.standard_normal((n_appends, 1, args.hkv, 1, 128)).astype(np.float16)
+    pages = 0
+    ctx = threadpool_limits(1) if threadpool_limits else None
+    try:
+        if ctx:
+            ctx.__enter__()
+        t0 = time.perf_counter()
+        tk = tv = None
+        for t in range(n_appends):
+            k, v = ks[t], vs[t]
+            if not (np.isfinite(k).all() and np.isfinite(v).all()):
+                raise ValueError("non-finite synthetic input")
+            tk = k if tk is None else np.concatenate([tk, k], axis=2)
+            tv = v if tv is None else np.concatenate([tv, v], axis=2)
+            if tk.shape[2] == 64:
+                oracle.encode_block(tk, l1_bits=l1b, deep_bits=deepb, split_dim=split, use_int8_radii=int8)
+                oracle.quantize_block(tv[:, :, None])
+                tk = tv = None
+                pages += 1
+        dt = time.perf_counter() - t0
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    return dt / n_appends * 1e6, n_appends, pages
+
+
 def copy_calibration(nbytes: int, reps: int = 10) -> None:
     """Plain device-to-device copy of a known size: the reference for scaling
     rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes."""
@@ -897,6 +938,13 @@ def main():
         return
     if args.workload == "append":
         r = run_append(args, layout)
+        cpu = None
+        if not args.no_cpu:
+            cpu_us, n_cpu, cpu_pages = cpu_append_baseline(args, layout, r["appends"])
+            cpu = {"value": round(cpu_us, 2), "unit": "us/append", "cores": 1, "kind": "port",
+                   "sample": f"{n_cpu} single-token appends with {cpu_pages} page flushes (host restatement of "
+                             f"append: finiteness check, tail concatenation, oracle encode_block + "
+                             f"quantize_block per full page; 1 thread)"}
         print(json.dumps({
             "metric": "single-token append latency, Llama-3-8B kv shape",
             "value": round(r["us_per_append"], 2), "unit": "us/append", "n_gpus": 1,
@@ -904,6 +952,7 @@ def main():
             "config": {"workload": f"{r['appends']} single-token appends of {args.hkv} kv heads "
                                    f"through TurboPolarKVCacheRuntime.append, {r['pages']} page encodes "
                                    f"(BASELINE configs[3])", "layout": args.layout},
+            "cpu_baseline": cpu,
         }))
         return
     if args.workload == "snapshot":
