@@ -867,7 +867,7 @@ def main():
             "config": {"workload": f"tp_fused_qk: {args.hq} q / {args.hkv} kv heads, {r['n_pages']} pages "
                                    f"({args.context} tokens), {r['n_caches']} rotating caches", "layout": args.layout},
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(f"qk_{args.layout}", args)},
             "algorithmic_bytes_per_step": {"read": r["read"], "write": r["write"]},
             "cpu_baseline": cpu,
         }))
