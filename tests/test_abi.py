@@ -176,3 +176,11 @@ def test_integration_stub_matches_the_binding(monkeypatch):
         norm = ["tp_page_layout" if n == "TPPageLayout" else "tp_pages" if n == "TPPages" else n for n in norm]
         want = ["tp_page_layout" if n == "TPPageLayout" else "tp_pages" if n == "TPPages" else n for n in want]
         assert norm == want, name
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """Without the built library every kernel call raises; nothing falls back to the CPU."""
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libturbopolar_hip.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built.*no CPU fallback"):
+        _lib.lib()
