@@ -526,51 +526,26 @@ static inline int32_t counter_stride_of(int64_t units) {
   return w;
 }
 
-// Store of 1, 2 or 4 consecutive floats with sc1 (dpt is wave-uniform).
-__device__ __forceinline__ void st_agent_n(float* p, const float* x, int dpt) {
-  if (dpt == 4) {
-    st_agent4(p, float4v{x[0], x[1], x[2], x[3]});
-  } else if (dpt == 2) {
-    st_agent2(p, x[0], x[1]);
-  } else {
-    asm volatile("global_store_dword %0, %1, off sc1" : : "v"(p), "v"(x[0]) : "memory");
-  }
+// Normalised fp16 output of 4 consecutive dims.
+__device__ __forceinline__ void store_out4(uint16_t* orow, const float* x, float inv) {
+  *reinterpret_cast<uint2*>(orow) = make_uint2((uint32_t)f2h(x[0] * inv) | ((uint32_t)f2h(x[1] * inv) << 16),
+                                               (uint32_t)f2h(x[2] * inv) | ((uint32_t)f2h(x[3] * inv) << 16));
 }
 
-// Normalised fp16 output of 1, 2 or 4 consecutive dims.
-__device__ __forceinline__ void store_out_n(uint16_t* orow, const float* x, float inv, int dpt) {
-  if (dpt == 4) {
-    *reinterpret_cast<uint2*>(orow) = make_uint2((uint32_t)f2h(x[0] * inv) | ((uint32_t)f2h(x[1] * inv) << 16),
-                                                 (uint32_t)f2h(x[2] * inv) | ((uint32_t)f2h(x[3] * inv) << 16));
-  } else if (dpt == 2) {
-    *reinterpret_cast<uint32_t*>(orow) = (uint32_t)f2h(x[0] * inv) | ((uint32_t)f2h(x[1] * inv) << 16);
-  } else {
-    *orow = f2h(x[0] * inv);
-  }
-}
-
-// Folds the 8 wave states of DPT consecutive dims (from d0) of head h, in
-// wave order.  A state with m = -inf weighs 0, so an empty one adds 0 and one
-// that carries NaN (all of its scores NaN) still makes the fold NaN.
-template <int DPT, class Shared>
+// Folds the 8 wave states of dims d0 .. d0+3 of head h, in wave order.  A
+// state with m = -inf weighs 0, so an empty one adds 0 and one that carries
+// NaN (all of its scores NaN) still makes the fold NaN.
+template <class Shared>
 __device__ __forceinline__ void fold_waves(const Shared& sh, int h, int d0, float& M, float& L, float* A) {
   constexpr int W = sizeof(sh.ml) / sizeof(sh.ml[0]);
-  float m[W], l[W], x[W][DPT];
+  float m[W], l[W];
+  float4v x[W];
 #pragma unroll
   for (int u = 0; u < W; ++u) {
     const float2 ml = sh.ml[u][h];
     m[u] = ml.x;
     l[u] = ml.y;
-    const float* src = &sh.acc[u][h * kRedStride + d0];
-    if constexpr (DPT == 4) {
-      const float4v v = *reinterpret_cast<const float4v*>(src);
-      x[u][0] = v[0], x[u][1] = v[1], x[u][2] = v[2], x[u][3] = v[3];
-    } else if constexpr (DPT == 2) {
-      const float2 v = *reinterpret_cast<const float2*>(src);
-      x[u][0] = v.x, x[u][1] = v.y;
-    } else {
-      x[u][0] = src[0];
-    }
+    x[u] = *reinterpret_cast<const float4v*>(&sh.acc[u][h * kRedStride + d0]);
   }
 #pragma unroll
   for (int u = 0; u < W; ++u) M = fmaxf(M, m[u]);
@@ -579,7 +554,7 @@ __device__ __forceinline__ void fold_waves(const Shared& sh, int h, int d0, floa
     const float w = m[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[u] - M);
     L += l[u] * w;
 #pragma unroll
-    for (int i = 0; i < DPT; ++i) A[i] += x[u][i] * w;
+    for (int i = 0; i < 4; ++i) A[i] += x[u][i] * w;
   }
 }
 
@@ -793,28 +768,19 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   }
   lds_barrier();
 
-  // Fold the waves' records.  Every thread takes part: thread t owns dpt
-  // consecutive dims of head t / (128 / dpt), with dpt = 1, 2 or 4 for up to
-  // 4, 8 or 16 heads, and folds the WAVES records in wave order.
-  const int ldpt = nh <= 4 ? 0 : (nh <= 8 ? 1 : 2);  // log2(dpt)
-  const int dpt = 1 << ldpt;
-  const int h = tid >> (7 - ldpt);
-  const int d0 = (tid & ((kHeadDim >> ldpt) - 1)) << ldpt;
+  // Fold the waves' records: thread t owns dims 4 (t % 32) .. +3 of head
+  // t / 32 and folds the WAVES records in wave order (one 16-byte LDS read per
+  // record; spreading 4 heads over all 512 threads at one dim each was slower).
+  const int h = tid >> 5;
+  const int d0 = (tid & 31) << 2;
   const bool live = h < nh;
   float M = -INFINITY, L = 0.0f;
   float A[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (live) {
-    if (ldpt == 0)
-      fold_waves<1>(sh, h, d0, M, L, A);
-    else if (ldpt == 1)
-      fold_waves<2>(sh, h, d0, M, L, A);
-    else
-      fold_waves<4>(sh, h, d0, M, L, A);
-  }
+  if (live) fold_waves(sh, h, d0, M, L, A);
   if (a.n_splits == 1) {
     if (live)
-      store_out_n(a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + h) * kHeadDim + d0, A,
-                  __builtin_amdgcn_rcpf(L), dpt);
+      store_out4(a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + h) * kHeadDim + d0, A,
+                 __builtin_amdgcn_rcpf(L));
     return;
   }
   const int64_t unit = bkv * a.head_blocks + hb;
@@ -822,7 +788,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   const int Sp = (S + 1) & ~1;  // (m, l) row length in pairs
   if (live) {
     if (d0 == 0) st_agent2(a.part_ml + ((unit * 16 + h) * Sp + split) * 2, M, L);
-    st_agent_n(a.part_acc + ((unit * S + split) * 16 + h) * kHeadDim + d0, A, dpt);
+    st_agent4(a.part_acc + ((unit * S + split) * 16 + h) * kHeadDim + d0, float4v{A[0], A[1], A[2], A[3]});
   }
   wait_stores();
   __syncthreads();
