@@ -96,9 +96,9 @@ CASES = [
     ("odd_split", 8, 4, 3, 9, 2),
     ("int8_default_angles", 4, 2, 2, 0, 1),
     ("default", 40, 2, 2, 11, 1),  # GQA 20 > 16: two head blocks
-    ("default", 6, 2, 3, 5, 1),  # GQA 3: 1 dim per folding thread, 96 live items of 128, 4 split groups
-    ("default", 12, 2, 4, 0, 1),  # GQA 6: 2 dims per folding thread
-    ("default", 24, 2, 3, 9, 1),  # GQA 12: 4 dims per folding thread, 1 split group
+    ("default", 6, 2, 3, 5, 1),  # GQA 3: 3 live head rows in the fold; combine: 96 live items of 128, 4 split groups
+    ("default", 12, 2, 4, 0, 1),  # GQA 6: combine items in 192 of 256 slots, 2 split groups
+    ("default", 24, 2, 3, 9, 1),  # GQA 12: 384 combine items, 1 split group
     ("default", 2, 2, 600, 3, 1),  # 600 splits of one head: 16 split groups, chunked reloads
 ]
 
