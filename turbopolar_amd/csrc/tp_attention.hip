@@ -870,14 +870,16 @@ __global__ __launch_bounds__(256) void fused_qk_kernel(AttnArgs a) {
   const int kv = (int)(bkv - (int64_t)b * a.hkv);
   const int h0 = hb * 16;
   const int nh = min(16, a.g - h0);
-  build_lut<KIND>(lut, a, tid);
   half8v qb[4];
   load_q(a, b, kv, h0, nh, l16, l4, qb);
-  __syncthreads();
+  // The page's K loads go out before the table build and the barrier (a wave
+  // past the last page reloads the last page and leaves after the barrier).
   const int page = blockIdx.x * 4 + wave;
-  if (page >= a.n_pages) return;
   KRegs<KIND> kr;
-  load_k<KIND>(a, bkv * a.capacity + page, l16, l4, kr);
+  load_k<KIND>(a, bkv * a.capacity + min(page, a.n_pages - 1), l16, l4, kr);
+  build_lut<KIND>(lut, a, tid);
+  __syncthreads();
+  if (page >= a.n_pages) return;
   float4v s[4];
   qk_regs<KIND>(a, lut, kr, qb, l16, l4, s);
   if (l16 >= nh) return;
