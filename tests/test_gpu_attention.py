@@ -123,10 +123,14 @@ def test_decode_attention_masked_suffix(device, drop):
         check(out, oracle_out(host, tk, tv, q, seq), f"drop={drop} pps={pps}")
 
 
-@pytest.mark.parametrize("layout_name", ["default", "fast", "deep2", "odd_split"])
-def test_fused_qk_parity(device, layout_name):
-    print(f"[qk] layout={layout_name}", flush=True)
-    block, qv, host, tk, tv, q = build_case(device, LAYOUTS[layout_name], 8, 2, 3, 0, seed=9)
+@pytest.mark.parametrize("layout_name,hq,hkv,S", [
+    ("default", 8, 2, 3), ("fast", 8, 2, 3), ("deep2", 8, 2, 3), ("odd_split", 8, 2, 3),
+    ("default", 40, 2, 5),  # two head blocks; the second workgroup has one live wave
+    ("fast", 32, 8, 9),
+])
+def test_fused_qk_parity(device, layout_name, hq, hkv, S):
+    print(f"[qk] layout={layout_name} hq={hq} hkv={hkv} S={S}", flush=True)
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS[layout_name], hq, hkv, S, 0, seed=9)
     scores = kernels.fused_qk(torch.from_numpy(q).to(device), PageSet(block, None), SCALE16)
     torch.cuda.synchronize()
     got = scores.float().cpu().numpy()
