@@ -121,7 +121,9 @@ int32_t tp_fused_qk(const void* q, int64_t batch, int32_t hq, int32_t hkv,
  * q: fp16 [batch][hq][128]; out: fp16 [batch][hq][128].
  * tail_k, tail_v: fp16 [batch][hkv][tail_stride][128] holding tail_len (0..63)
  *   dense tokens that follow the pages (NULL when tail_len == 0).
- * Tokens with global index >= actual_seq_len are masked.
+ * Tokens with global index >= actual_seq_len are masked (actual_seq_len >= 1;
+ *   a value past the stored tokens attends every stored token, as the
+ *   reference's mask does).
  * pages_per_split: pages per workgroup (0 = library default); the grid,
  *   ceil(n_pages / pages_per_split) x batch x hkv x ceil(hq / hkv / 16)
  *   workgroups, must stay below 2^31.
@@ -159,6 +161,16 @@ int32_t tp_default_pages_per_split(int64_t batch, int32_t hq, int32_t hkv, int32
 int32_t tp_decode_pages(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
                         int64_t page_begin, int32_t n_pages, void* k_out, void* v_out,
                         void* stream);
+
+/* tp_decode_pages into rows of a larger output: k_out, v_out are fp16
+ * [bh][out_tokens][128] and page page_begin + p of row r lands at tokens
+ * [out_offset + 64 p, out_offset + 64 p + 64) of row r (out_offset + 64 n_pages
+ * <= out_tokens).  The decompress-on-read path decodes the stored pages and
+ * the zero-padded tail page (turbo_polar_cache.py:200-274) side by side into
+ * one buffer with it.  Same replaced functions as tp_decode_pages. */
+int32_t tp_decode_pages_into(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
+                             int64_t page_begin, int32_t n_pages, void* k_out, void* v_out,
+                             int64_t out_tokens, int64_t out_offset, void* stream);
 
 /* Append staging (replaces the per-input mx.isfinite(...).all() check of
  * TurboPolarKVCacheRuntime._validate_append_inputs, turbo_polar_cache.py:69,

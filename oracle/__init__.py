@@ -12,12 +12,17 @@ Parity status per function (what pins it is listed in ``tests/test_oracle_*.py``
 * ``encode_block`` / ``quantize_block`` -- pinned by the closed-form known
   answers (axis-aligned angles, 3-4-5 radius, fp16 overflow, zero V group,
   group-max codes, half-even ties), by an independent exact-rational
-  restatement (``oracle/exact.py``) on random and edge inputs, and by the
+  restatement (``tests/exact_f16.py``) on random and edge inputs, and by the
   packed-shape rules of the reference's own tests.  The MLX boundary itself
   (exact ulps of MLX's fp16 ``arctan2``/``log``) cannot be imported here; the
   documented policy is "correctly rounded", see ``oracle/turbopolar.py``.
-* ``decode_block`` / ``dequantize_block`` -- pinned by closed forms and the
-  invariants |k_hat pair| == radius and encode(decode(codes)) == codes.
+* ``decode_block`` -- pinned by the invariants |k_hat pair| == radius and
+  encode(decode(codes)) == codes.
+* ``dequantize_block`` -- pinned by exact-rational known answers element by
+  element (dim d takes the scale of group d // 32 of its own token), by the
+  exact round trip of values that are code x power-of-two, and by the
+  quantisation error bound |v - dequantize(quantize(v))| <= 0.53125 s + half
+  an fp16 ulp on groups whose magnitudes differ by up to 2^16.
 * ``cpu_fused_qk`` / ``cpu_online_attention`` /
   ``cpu_online_attention_dense_tail`` -- pinned against textbook softmax
   attention computed independently with torch float64 SDPA on the decoded

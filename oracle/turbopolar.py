@@ -35,8 +35,11 @@ tests/test_oracle_attention.py, tests/test_golden.py):
 * encode_block, angle_codes_f16, atan2_cr, log_cr: known answers of the rules in
   encoder.py:24-98, an independent exact-rational restatement
   (tests/exact_f16.py) compared bit for bit, fp32-input wrap cases.
-* quantize_block / dequantize_block: known answers (zero group, group max,
-  half-even ties) and the exact-rational restatement.
+* quantize_block: known answers (zero group, group max, half-even ties) and
+  the exact-rational restatement.
+* dequantize_block: exact-rational known answers element by element, the
+  exact round trip of code x power-of-two values, and the quantisation error
+  bound 0.53125 s + half an fp16 ulp.
 * decode_block: radius invariant sqrt(kx^2 + ky^2) ~ r, decode->encode
   idempotence.
 * softmax_attention, cpu_fused_qk, cpu_online_attention[_dense_tail]: torch

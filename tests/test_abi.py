@@ -87,10 +87,13 @@ def test_decode_attention_argument_validation():
     assert call(n_pages=9)[0] == _lib.TP_ERR_INVALID
     st, msg = call(tail=64, tk=4096, tv=4096, tstride=64)
     assert st == _lib.TP_ERR_INVALID and "tail_len" in msg
-    st, msg = call(seq=257)
-    assert st == _lib.TP_ERR_INVALID and "actual_seq_len" in msg
+    # A length past the stored tokens is accepted (the reference only masks
+    # tokens at or past it); pps=1 without a workspace then stops the call at
+    # the workspace check, before any launch.
+    st, msg = call(seq=10**9, pps=1)
+    assert st == _lib.TP_ERR_WORKSPACE and "workspace" in msg
     st, msg = call(seq=0)
-    assert st == _lib.TP_ERR_INVALID
+    assert st == _lib.TP_ERR_INVALID and "actual_seq_len" in msg
     st, msg = call(n_pages=0)
     assert st == _lib.TP_ERR_INVALID and "nothing to attend" in msg
     st, msg = call(pps=1)  # 4 splits need a workspace

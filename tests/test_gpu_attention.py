@@ -26,10 +26,10 @@ pytestmark = pytest.mark.gpu
 SCALE16 = fp16_scale(1.0 / np.sqrt(128.0))
 
 
-def build_case(device, layout, hq, hkv, S, tail, seed=0, kind="normal", qscale=1.0):
+def build_case(device, layout, hq, hkv, S, tail, seed=0, kind="normal", qscale=1.0, B=1):
     """Encode S pages on the GPU; returns GPU page views, host pages, tails, q."""
-    k, v = gen_kv(seed, 1, hkv, S * PAGE + tail, kind, np.float16)
-    q = gen_q(seed, 1, hq, qscale)
+    k, v = gen_kv(seed, B, hkv, S * PAGE + tail, kind, np.float16)
+    q = gen_q(seed, B, hq, qscale)
     host = None
     block = qv = None
     if S:
@@ -39,7 +39,7 @@ def build_case(device, layout, hq, hkv, S, tail, seed=0, kind="normal", qscale=1
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
         block = PolarKeyBlock(
             radii=t(host["radii"]), angle_codes_l1=t(host["angle_codes_l1"]),
-            angle_codes_deep=t(host["angle_codes_deep"]), shape=(1, hkv, S * PAGE, 128),
+            angle_codes_deep=t(host["angle_codes_deep"]), shape=(B, hkv, S * PAGE, 128),
             block_size=PAGE, head_dim=128, metadata=meta,
             radii_scales=t(host["radii_scales"]) if layout[0] else None,
         )
@@ -112,6 +112,48 @@ def test_decode_attention_parity(device, layout_name, hq, hkv, S, tail, pps):
     check(out, oracle_out(host, tk, tv, q, seq), layout_name)
 
 
+BATCHED = [
+    # B, layout, hq, hkv, S pages, tail tokens, pages_per_split, tokens masked at the end
+    (2, "default", 40, 2, 3, 11, 1, 0),  # GQA 20: two head blocks per kv head, one-page splits
+    (3, "default", 8, 2, 4, 37, 0, 0),
+    (2, "default", 8, 2, 5, 20, 2, 70),  # masked suffix reaching into the last page
+    (3, "default", 32, 8, 3, 0, 1, 0),
+    (2, "fast", 16, 4, 3, 5, 1, 0),
+    (2, "default", 4, 2, 0, 37, 0, 0),  # dense tail only
+]
+
+
+@pytest.mark.parametrize("B,layout_name,hq,hkv,S,tail,pps,drop", BATCHED)
+def test_decode_attention_batched(device, B, layout_name, hq, hkv, S, tail, pps, drop):
+    """Batch > 1: row b of q and out, page slots b * H_kv + kv of the store and
+    tail rows b * H_kv + kv, checked against the oracle per batch row."""
+    print(f"[attn-batch] B={B} layout={layout_name} hq={hq} hkv={hkv} S={S} tail={tail} pps={pps} drop={drop}",
+          flush=True)
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS[layout_name], hq, hkv, S, tail, seed=60 + B + S, B=B)
+    seq = S * PAGE + tail - drop
+    out = run_gpu(device, block, qv, tk, tv, q, seq, pps)
+    assert out.shape == (B, hq, 128)
+    check(out, oracle_out(host, tk, tv, q, seq), f"batched B={B}")
+    # every batch row differs, so a batch-index mix-up cannot pass by symmetry
+    assert max_abs(out[0], out[1]) > 1e-2
+
+
+@pytest.mark.parametrize("B,layout_name,hq,hkv,S", [(2, "default", 40, 2, 5), (3, "fast", 8, 2, 3)])
+def test_fused_qk_batched(device, B, layout_name, hq, hkv, S):
+    print(f"[qk-batch] B={B} layout={layout_name} hq={hq} hkv={hkv} S={S}", flush=True)
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS[layout_name], hq, hkv, S, 0, seed=70 + B, B=B)
+    scores = kernels.fused_qk(torch.from_numpy(q).to(device), PageSet(block, None), SCALE16)
+    torch.cuda.synchronize()
+    got = scores.float().cpu().numpy()
+    blk = {k: host[k] for k in ("radii", "radii_scales", "angle_codes_l1", "angle_codes_deep", "metadata")}
+    if blk["radii_scales"] is not None:
+        blk["radii_scales"] = blk["radii_scales"].reshape(blk["radii"].shape[:3] + (1, 1))
+    ref = oracle.cpu_fused_qk(q, blk, SCALE16)
+    assert got.shape == ref.shape == (B, hq, S * PAGE)
+    assert max_abs(got, ref) <= 1e-2, max_abs(got, ref)
+    assert cosine(got, ref) >= 0.999
+
+
 @pytest.mark.parametrize("drop", [1, 5, 64, 100])
 def test_decode_attention_masked_suffix(device, drop):
     """actual_seq_len below the stored tokens masks the suffix (metal.py:318-319)."""
@@ -121,6 +163,17 @@ def test_decode_attention_masked_suffix(device, drop):
     for pps in (0, 1):
         out = run_gpu(device, block, qv, tk, tv, q, seq, pps)
         check(out, oracle_out(host, tk, tv, q, seq), f"drop={drop} pps={pps}")
+
+
+def test_seq_len_beyond_stored_tokens(device):
+    """actual_seq_len past the stored tokens attends every stored token, as the
+    reference's mask (global index >= actual_seq_len) does
+    (tqpolar_online_attention.metal:474; metal.py:318)."""
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], 8, 2, 3, 9, seed=8)
+    total = 3 * PAGE + 9
+    ref = oracle_out(host, tk, tv, q, total)
+    for seq in (total + 1, total + 1000, 1 << 40):
+        check(run_gpu(device, block, qv, tk, tv, q, seq), ref, f"seq={seq}")
 
 
 @pytest.mark.parametrize("layout_name,hq,hkv,S", [

@@ -103,3 +103,71 @@ def test_nonstandard_mask_is_rejected(device):
                 model(torch.tensor([[3]], device=device), attention_mask=mask, past_key_values=cache, use_cache=True)
         finally:
             tl.unpatch_llama_attention(model)
+
+
+def test_hook_attention_matches_oracle(device):
+    """Layer 1's fused decode inside the patched model, step by step, against
+    the oracle's _cpu_online_attention_dense_tail (metal.py:293-332) on the
+    identical state: q after RoPE as the hook hands it over (fp16, as the
+    kernel takes it), the cache's stored pages and dense tail after the
+    step's append, the step's sequence length and fp16(scale).  Steps cover a
+    tail-only cache, a page completed by the step and a partial tail."""
+    import oracle
+    from common import ATOL, RTOL_L2, max_abs, rel_l2
+
+    model = _model(device)
+    g = torch.Generator().manual_seed(3)
+    tokens = torch.randint(0, 512, (1, 140), generator=g).to(device)
+    prompt = 60
+    seen = []
+    orig = TurboPolarFastCache.decode_attention
+
+    def capture(self, q, k_new, v_new, scale):
+        out = orig(self, q, k_new, v_new, scale)
+        if self is cache.fast(1):
+            rt = self.runtime
+            block, qv, tk, tv, _, seq = rt.get_fused_attention_inputs()
+            host = lambda t: None if t is None else t.detach().cpu().numpy()  # noqa: E731
+            seen.append({
+                "q": q[:, :, 0].to(torch.float16).cpu().numpy(), "scale": scale, "seq": seq,
+                "blk": None if block is None else {
+                    "radii": host(block.radii),
+                    "radii_scales": None if block.radii_scales is None else
+                    host(block.radii_scales).reshape(block.radii.shape[:3] + (1, 1)),
+                    "angle_codes_l1": host(block.angle_codes_l1), "angle_codes_deep": host(block.angle_codes_deep),
+                    "metadata": block.metadata},
+                "qv": None if qv is None else (host(qv.codes), host(qv.scales)),
+                "tk": host(tk), "tv": host(tv), "out": out.float().cpu().numpy(),
+            })
+        return out
+
+    cache = tl.make_turbo_cache(model)
+    with torch.no_grad():
+        model(tokens[:, :prompt], past_key_values=cache, use_cache=True)
+        TurboPolarFastCache.decode_attention = capture
+        tl.patch_llama_attention(model)
+        try:
+            for t in range(prompt, prompt + 75):  # 61 .. 135 tokens: 0 -> 2 pages
+                model(tokens[:, t:t + 1], past_key_values=cache, use_cache=True)
+        finally:
+            tl.unpatch_llama_attention(model)
+            TurboPolarFastCache.decode_attention = orig
+    assert len(seen) == 75
+    checked = 0
+    for i, st in enumerate(seen):
+        if i % 7 and i not in (2, 3, 67, 68):  # every 7th step, and both sides of the page completions at 64, 128
+            continue
+        hkv = st["tk"].shape[1] if st["tk"] is not None else st["blk"]["radii"].shape[1]
+        empty = np.zeros((1, hkv, 0, 128), np.float16)
+        tk = st["tk"] if st["tk"] is not None else empty
+        tv = st["tv"] if st["tv"] is not None else empty
+        scale = oracle.fp16_scale(st["scale"])
+        if st["blk"] is None:
+            ref = oracle.softmax_attention(st["q"], tk, tv, scale, st["seq"])
+        else:
+            ref = oracle.cpu_online_attention_dense_tail(st["q"], st["blk"], st["qv"], tk, tv, scale, st["seq"])
+        ma, rl = max_abs(st["out"], ref), rel_l2(st["out"], ref)
+        assert ma <= ATOL and rl <= RTOL_L2, f"step {i} (seq {st['seq']}): max_abs={ma:.3g} rel_l2={rl:.3g}"
+        checked += 1
+    assert checked >= 14 and seen[2]["blk"] is None and seen[3]["blk"] is not None and seen[3]["tk"] is None
+    assert seen[67]["seq"] == 128 and seen[67]["tk"] is None and seen[68]["tk"].shape[2] == 1

@@ -285,3 +285,62 @@ def test_append_stage_flag_modes(device, mode, tokens):
     assert stage(bad, 8) == _lib.TP_ERR_NONFINITE
     assert stage(k, 10) == _lib.TP_OK
     assert torch.equal(tail_k[:, 0], k[:, 0])
+
+
+@pytest.mark.parametrize("layout_name", ["default", "fast"])
+def test_fetch_blocks_and_bytes_read(device, layout_name):
+    """fetch_blocks (turbo_polar_cache.py:321-346): the selected pages decoded
+    in the given order, equal within one fp16 ulp to the oracle's decode of
+    the same stored pages, and bytes_read grown by the key bytes of each page
+    fetched (radii + both angle rows, + the page scale for int8 radii)."""
+    cfg = _cfg(layout_name, hq=8, hkv=2)
+    rt = TurboPolarKVCacheRuntime(cfg)
+    rng = np.random.default_rng(31)
+    k = rng.standard_normal((2, 2, 3 * PAGE + 10, 128)).astype(np.float16)
+    v = rng.standard_normal((2, 2, 3 * PAGE + 10, 128)).astype(np.float16)
+    rt.append(torch.from_numpy(k).to(device), torch.from_numpy(v).to(device))
+    blk, _, _, _, _ = _host_state(rt)
+    rs = blk["radii_scales"]
+    kref = oracle.decode_block(blk["radii"], None if rs is None else rs.reshape(rs.shape[:3] + (1, 1)),
+                               blk["angle_codes_l1"], blk["angle_codes_deep"], blk["metadata"])
+    kref = kref.reshape(2, 2, 3, PAGE, 128)
+    int8, l1b, deepb, split = LAYOUTS[layout_name]
+    l1_row, deep_row = oracle.layout_bytes(l1b, deepb, split)
+    per_page = 2 * 2 * PAGE * (64 * (1 if int8 else 2) + l1_row + deep_row) + (2 * 2 * 2 if int8 else 0)
+    assert rt.bytes_read == 0
+    for indices, expect_pages in ((None, [0, 1, 2]), ([2, 0], [2, 0]), ([1], [1])):
+        before = rt.bytes_read
+        got = rt.fetch_blocks(indices)
+        torch.cuda.synchronize()
+        assert tuple(got.shape) == (2, 2, PAGE * len(expect_pages), 128) and got.dtype == torch.float16
+        want = np.concatenate([kref[:, :, p] for p in expect_pages], axis=2)
+        g = got.cpu().numpy().astype(np.float64)
+        ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+        assert np.all(np.abs(g - want) <= ulp + 1e-12), indices
+        assert rt.bytes_read - before == per_page * len(expect_pages)
+    empty = TurboPolarKVCacheRuntime(cfg)
+    assert empty.fetch_blocks().numel() == 0
+
+
+def test_tail_views_follow_the_cache(device):
+    """get_fused_attention_inputs returns the dense tail as views of the
+    runtime's tail buffer (no copy per decode step): they hold the tail at the
+    time of the call and are valid until the next append, which may rewrite
+    them in place.  The partial_k / partial_v properties return copies that an
+    append never changes, as the reference's immutable arrays do."""
+    cfg = _cfg("default")
+    rt = TurboPolarKVCacheRuntime(cfg)
+    rng = np.random.default_rng(32)
+    k = torch.from_numpy(rng.standard_normal((1, 2, 70, 128)).astype(np.float16)).to(device)
+    v = torch.from_numpy(rng.standard_normal((1, 2, 70, 128)).astype(np.float16)).to(device)
+    rt.append(k[:, :, :60], v[:, :, :60])
+    pk = rt.partial_k
+    snap = pk.clone()
+    _, _, tk, _, _, seq = rt.get_fused_attention_inputs()
+    assert seq == 60 and torch.equal(tk, k[:, :, :60])
+    rt.append(k[:, :, 60:], v[:, :, 60:])  # completes page 0, 6 tokens stay in the tail
+    torch.cuda.synchronize()
+    assert torch.equal(pk, snap), "a partial_k copy changed under an append"
+    assert torch.equal(rt.partial_k, k[:, :, 64:70])
+    _, _, tk2, _, _, seq2 = rt.get_fused_attention_inputs()
+    assert seq2 == 70 and torch.equal(tk2, k[:, :, 64:70])

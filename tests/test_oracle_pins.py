@@ -188,6 +188,71 @@ def test_v_quantizer_matches_exact_rational(dtype):
             assert list(codes[0, 0, 0, t, 32 * g: 32 * g + 32]) == c
 
 
+# ------------------------------------------------ V dequantisation (v_quant/encoder.py:32-38)
+
+def test_dequantize_known_answers():
+    """Element by element with exact rationals: dim d of a token takes the scale
+    of group d // 32 of that token (the reshape to [..., D // 32, 32] at
+    v_quant/encoder.py:35), and the product is rounded once to fp16."""
+    rng = np.random.default_rng(21)
+    codes = rng.integers(-128, 128, size=(1, 2, 3, 5, 128)).astype(np.int8)
+    codes[0, 0, 0, 0, :4] = [-128, 127, 0, 1]
+    # four scales of different magnitude per token, so a group read from the
+    # wrong token, group or position changes the product
+    scales = (np.exp2(rng.integers(-9, 3, size=(1, 2, 3, 5, 4))) *
+              rng.uniform(1.0, 2.0, size=(1, 2, 3, 5, 4))).astype(np.float16)
+    scales[0, 0, 0, 0] = np.array([0x068E, 0x3C00, 0x7BFF, 0x0001], np.uint16).view(np.float16)
+    got = oracle.dequantize_block(codes, scales)
+    assert got.dtype == np.float16 and got.shape == codes.shape
+    for b, h, s, t in np.ndindex(1, 2, 3, 5):
+        for d in range(128):
+            want = r16(Fraction(int(codes[b, h, s, t, d])) * Fraction(float(scales[b, h, s, t, d // 32])))
+            g = float(got[b, h, s, t, d])
+            assert g == want or (math.isinf(want) and g == want), (b, h, s, t, d, g, want)
+    # closed forms: -128 * fp16(1e-4) = -0.012817..., 127 * 1.0, 65504 * 0 = 0,
+    # 1 * smallest subnormal = smallest subnormal
+    row = got[0, 0, 0, 0].view(np.uint16)
+    assert float(got[0, 0, 0, 0, 0]) == r16(Fraction(-128) * Fraction(float(np.uint16(0x068E).view(np.float16))))
+    assert row[32] == np.float16(float(codes[0, 0, 0, 0, 32])).view(np.uint16)  # scale 1.0 is the identity
+    assert row[96] == (np.float16(float(codes[0, 0, 0, 0, 96])) * np.uint16(1).view(np.float16)).view(np.uint16)
+
+
+def test_dequantize_inverts_exact_quantization():
+    """Values that are code x power-of-two with the group max at 127 x scale
+    quantise exactly, so dequantize(quantize(v)) returns v bit for bit."""
+    rng = np.random.default_rng(22)
+    v = np.zeros((1, 1, 2, 64, 128), np.float32)
+    for s, t, g in np.ndindex(2, 64, 4):
+        scale = np.exp2(float(rng.integers(-12, 4)))
+        c = rng.integers(-127, 128, size=32).astype(np.float32)
+        c[rng.integers(0, 32)] = rng.choice([-127.0, 127.0])
+        v[0, 0, s, t, 32 * g: 32 * g + 32] = c * scale
+    for dtype in (np.float16, np.float32):
+        x = v.astype(dtype)
+        codes, scales = oracle.quantize_block(x)
+        back = oracle.dequantize_block(codes, scales)
+        assert np.array_equal(back.astype(np.float32), x.astype(np.float16).astype(np.float32))
+
+
+def test_dequantize_bounds_quantization_error():
+    """|v - dequantize(quantize(v))| <= 0.53125 * s + half an fp16 ulp of the
+    result, s the group's scale: the fp16 quotient v / s (|v / s| <= 127.5)
+    errs by at most 2^-5, rint by 0.5, and the product rounds once.  Groups of
+    one token span 2^-8 .. 2^8 in magnitude, so any mix-up of groups breaks it."""
+    rng = np.random.default_rng(23)
+    mag = np.exp2(rng.integers(-8, 9, size=(1, 2, 4, 64, 4, 1))).astype(np.float32)
+    v = (rng.standard_normal((1, 2, 4, 64, 4, 32)).astype(np.float32) * mag).reshape(1, 2, 4, 64, 128)
+    v = v.astype(np.float16)
+    codes, scales = oracle.quantize_block(v)
+    back = oracle.dequantize_block(codes, scales).astype(np.float64)
+    s = np.repeat(scales.astype(np.float64), 32, axis=-1)
+    half_ulp = np.spacing(np.abs(back).astype(np.float16)).astype(np.float64) / 2
+    err = np.abs(back - v.astype(np.float64))
+    assert np.all(err <= 0.53125 * s + half_ulp)
+    # and the bound is tight enough to matter: the error reaches a third of s somewhere
+    assert np.max(err / s) > 0.33
+
+
 def test_f64_to_f16_rounding_is_direct():
     """atan2_cr / log_cr rely on NumPy's float64 -> float16 cast rounding once;
     checked against the exact rounding on values straddling fp16 midpoints."""

@@ -1053,11 +1053,16 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
     set_error("nothing to attend: no pages and no tail");
     return TP_ERR_INVALID;
   }
+  // The reference masks tokens at or past actual_seq_len and accepts a length
+  // beyond the stored tokens (tqpolar_online_attention.metal:474; metal.py:318),
+  // so a longer length attends every stored token.  A length below 1 would
+  // mask everything (the reference's softmax then returns NaN): rejected.
   const int64_t total = (int64_t)n_pages * kPageTokens + tail_len;
-  if (actual_seq_len < 1 || actual_seq_len > total) {
-    set_error("actual_seq_len=%lld outside [1, %lld]", (long long)actual_seq_len, (long long)total);
+  if (actual_seq_len < 1) {
+    set_error("actual_seq_len=%lld must be at least 1", (long long)actual_seq_len);
     return TP_ERR_INVALID;
   }
+  if (actual_seq_len > total) actual_seq_len = total;
   if (pages_per_split <= 0) pages_per_split = tp_default_pages_per_split(batch, hq, hkv, n_pages);
   const int32_t n_splits = n_splits_of(n_pages, pages_per_split);
   const int64_t n_groups = (int64_t)n_splits * batch * hkv * a.head_blocks;

@@ -35,6 +35,8 @@ struct DecodeArgs {
   int32_t deep_row;
   uint16_t* k_out;
   uint16_t* v_out;
+  int64_t out_tokens;  // tokens per (batch, head) row of k_out / v_out
+  int64_t out_offset;  // token of that row where page page_begin lands
 };
 
 __global__ __launch_bounds__(256) void decode_pages_kernel(DecodeArgs a) {
@@ -50,7 +52,7 @@ __global__ __launch_bounds__(256) void decode_pages_kernel(DecodeArgs a) {
   const int qq = tid & 3;
   const int64_t slot = bh * a.capacity + a.page_begin + page;
   const int64_t row = slot * kPageTokens + t;
-  const int64_t out_off = ((bh * a.n_pages + page) * kPageTokens + t) * kHeadDim + 32 * qq;
+  const int64_t out_off = (bh * a.out_tokens + a.out_offset + (int64_t)page * kPageTokens + t) * kHeadDim + 32 * qq;
 
   if (a.k_out) {
     // Tables: (cos, sin) of each l1 / deep code angle (decoder.py:37-55) and
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
   const int page = blockIdx.x;
   const int64_t slot = bh * a.capacity + a.page_begin + page;
   const int64_t row0 = slot * kPageTokens;
-  const int64_t out0 = (bh * a.n_pages + page) * kPageTokens;
+  const int64_t out0 = bh * a.out_tokens + a.out_offset + (int64_t)page * kPageTokens;
   const bool want_k = a.k_out != nullptr;
   const bool want_v = a.v_out != nullptr;
 
@@ -243,15 +245,20 @@ __global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
 
 using namespace tp;
 
-extern "C" int32_t tp_decode_pages(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
-                                   int64_t page_begin, int32_t n_pages, void* k_out, void* v_out,
-                                   void* stream) {
+extern "C" int32_t tp_decode_pages_into(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
+                                        int64_t page_begin, int32_t n_pages, void* k_out, void* v_out,
+                                        int64_t out_tokens, int64_t out_offset, void* stream) {
   clear_error();
   int l1_row = 0, deep_row = 0;
   if (!check_layout(layout, &l1_row, &deep_row)) return TP_ERR_UNSUPPORTED;
   if (!pages || bh < 1 || bh > 65535 || n_pages < 0 || page_begin < 0 ||
       page_begin + n_pages > pages->capacity) {
     set_error("bad page range");
+    return TP_ERR_INVALID;
+  }
+  if (out_offset < 0 || out_offset + (int64_t)n_pages * kPageTokens > out_tokens) {
+    set_error("pages [%lld, %lld) of output rows of %lld tokens", (long long)out_offset,
+              (long long)(out_offset + (int64_t)n_pages * kPageTokens), (long long)out_tokens);
     return TP_ERR_INVALID;
   }
   if (n_pages == 0 || (!k_out && !v_out)) return TP_OK;
@@ -286,6 +293,8 @@ extern "C" int32_t tp_decode_pages(const tp_page_layout* layout, const tp_pages*
   a.deep_row = deep_row;
   a.k_out = static_cast<uint16_t*>(k_out);
   a.v_out = static_cast<uint16_t*>(v_out);
+  a.out_tokens = out_tokens;
+  a.out_offset = out_offset;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool is_default = !layout->int8_radii && layout->l1_bits == 4 && layout->deep_bits == 4 && layout->split_dim == 64;
   const bool is_fast = layout->int8_radii && layout->deep_bits == 8 && layout->split_dim == 0;
@@ -301,4 +310,11 @@ extern "C" int32_t tp_decode_pages(const tp_page_layout* layout, const tp_pages*
   else
     hipLaunchKernelGGL(decode_pages_kernel, grid, dim3(256), 0, s, a);
   return launch_status("tp_decode_pages");
+}
+
+extern "C" int32_t tp_decode_pages(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
+                                   int64_t page_begin, int32_t n_pages, void* k_out, void* v_out,
+                                   void* stream) {
+  return tp_decode_pages_into(layout, pages, bh, page_begin, n_pages, k_out, v_out,
+                              (int64_t)(n_pages > 0 ? n_pages : 0) * kPageTokens, 0, stream);
 }

@@ -185,6 +185,24 @@ def encode_pages(
     check(st, "tp_encode_pages")
 
 
+def decode_pages_into(layout, pages: TPPages, bh: int, page_begin: int, n_pages: int,
+                      k_out: Optional[torch.Tensor], v_out: Optional[torch.Tensor], out_offset: int) -> None:
+    """tp_decode_pages_into: pages [page_begin, page_begin + n_pages) of every
+    (batch, head) row into tokens [out_offset, out_offset + 64 n_pages) of
+    ``k_out`` / ``v_out`` (fp16 ``[B, H, T, 128]``, contiguous)."""
+    ref = k_out if k_out is not None else v_out
+    for t in (k_out, v_out):
+        if t is not None and (t.dtype != torch.float16 or not t.is_contiguous() or t.shape != ref.shape):
+            raise ValueError("k_out / v_out must be contiguous fp16 tensors of one shape")
+    dev = ref.device
+    with on_device(dev):
+        st = lib().tp_decode_pages_into(
+            ctypes.byref(layout), ctypes.byref(pages), int(bh), int(page_begin), int(n_pages), ptr(k_out), ptr(v_out),
+            int(ref.shape[2]), int(out_offset), stream_handle(dev),
+        )
+    check(st, "tp_decode_pages_into")
+
+
 def decode_pages(pageset: PageSet, want_k: bool = True, want_v: bool = True):
     """tp_decode_pages -> dense fp16 ``[B, H, S*64, 128]`` K and/or V."""
     B, H, S = pageset.B, pageset.H, pageset.S
@@ -280,23 +298,55 @@ def decode_attention(
         if tail_stride_v != tail_stride:
             tk, tv = _fresh(tk), _fresh(tv)
             tail_stride = tail_len
+    layout = pageset.layout if pageset is not None else _DEFAULT_LAYOUT
+    pages = pageset.pages if pageset is not None else _NO_PAGES
+    return _launch_decode(q16, Hkv, layout, pages, n_pages, tk, tv, tail_len, tail_stride, actual_seq_len, scale,
+                          pages_per_split, out)
+
+
+_DEFAULT_LAYOUT = _lib.make_layout(False, 4, 4, 64)
+_NO_PAGES = TPPages()
+
+
+def _launch_decode(q16, Hkv, layout, pages, n_pages, tk, tv, tail_len, tail_stride, seq_len, scale, pps, out):
+    B, Hq, _ = q16.shape
     dev = q16.device
     if out is None:
         out = torch.empty((B, Hq, HEAD_DIM), dtype=torch.float16, device=dev)
     L = lib()
-    pps = int(pages_per_split) or int(L.tp_default_pages_per_split(B, Hq, Hkv, n_pages))
+    pps = int(pps) or int(L.tp_default_pages_per_split(B, Hq, Hkv, n_pages))
     need = int(L.tp_decode_workspace_bytes(B, Hq, Hkv, n_pages, tail_len, pps))
     ws = _Workspace.get(dev, need)
-    layout = pageset.layout if pageset is not None else _lib.make_layout(False, 4, 4, 64)
-    pages = pageset.pages if pageset is not None else TPPages()
     with on_device(dev):
         st = L.tp_decode_attention(
             ptr(q16), B, Hq, Hkv, ctypes.byref(layout), ctypes.byref(pages), n_pages,
-            ptr(tk), ptr(tv), tail_len, tail_stride, int(actual_seq_len), float(scale), pps,
+            ptr(tk), ptr(tv), tail_len, tail_stride, int(seq_len), float(scale), pps,
             ws.data_ptr(), ws.numel(), ptr(out), stream_handle(dev),
         )
     check(st, "tp_decode_attention")
     return out
+
+
+def decode_attention_store(q: torch.Tensor, layout, pages: TPPages, n_pages: int, num_kv_heads: int,
+                           tail_k: Optional[torch.Tensor], tail_v: Optional[torch.Tensor], seq_len: int,
+                           scale: float) -> torch.Tensor:
+    """A cache's decode step: ``tp_decode_attention`` over the first ``n_pages``
+    slots of a page store used in place (``pages`` carries its capacity) and a
+    dense tail given as ``[B, H_kv, T, 128]`` views of a token-major buffer
+    (``T`` < 64).  ``q`` is ``[B, H_q, 128]``."""
+    q16 = _q16(q)
+    tail_len = 0 if tail_k is None else int(tail_k.shape[2])
+    tk = tv = None
+    tail_stride = 0
+    if tail_len:
+        tk, tail_stride = _tail_view(tail_k.to(torch.float16))
+        tv, stride_v = _tail_view(tail_v.to(torch.float16))
+        if stride_v != tail_stride:
+            tk, tv, tail_stride = _fresh(tk), _fresh(tv), tail_len
+    if pages is None:
+        pages, n_pages = _NO_PAGES, 0
+    return _launch_decode(q16, num_kv_heads, layout, pages, n_pages, tk, tv, tail_len, tail_stride, seq_len, scale,
+                          0, None)
 
 
 def _tail_view(t: torch.Tensor):

@@ -5,8 +5,11 @@ rfsn_v11/generation/turbo_polar_cache.py:18-395.  Differences of mechanism
 (not of behaviour):
 
 * the dense tail lives in a preallocated ``[B, H, 64, D]`` device buffer
-  instead of being re-concatenated on every append (``partial_k`` /
-  ``partial_v`` are views of it);
+  instead of being re-concatenated on every append.  ``partial_k`` /
+  ``partial_v`` return copies of its valid part (an append never changes
+  them, like the reference's immutable arrays); ``get_fused_attention_inputs``
+  returns views of it, valid until the next append, so a decode step copies
+  nothing;
 * full pages are encoded by one ``tp_encode_pages`` launch per append, written
   straight into the storage slots (no per-page Python loop, no intermediate
   block copies);
@@ -55,6 +58,7 @@ class TurboPolarKVCacheRuntime:
         self._tail_len = 0
         self._flag: Optional[torch.Tensor] = None  # tp_append_stage verdict (pinned host memory)
         self._fused_views = None  # (block_count, storage buffers, (PolarKeyBlock, QuantizedVBlock))
+        self._scratch = None  # one-page store for the padded tail when the storage is full
         self._epoch = 0
 
         self._initialized = False
@@ -66,11 +70,17 @@ class TurboPolarKVCacheRuntime:
     # ------------------------------------------------------------------
     @property
     def partial_k(self) -> Optional[torch.Tensor]:
-        return self._tail_k[:, :, : self._tail_len] if self._tail_len else None
+        return self._tail_k[:, :, : self._tail_len].clone() if self._tail_len else None
 
     @property
     def partial_v(self) -> Optional[torch.Tensor]:
-        return self._tail_v[:, :, : self._tail_len] if self._tail_len else None
+        return self._tail_v[:, :, : self._tail_len].clone() if self._tail_len else None
+
+    def _tail_views(self):
+        """Views of the valid dense tail (rewritten in place by the next append)."""
+        if not self._tail_len:
+            return None, None
+        return self._tail_k[:, :, : self._tail_len], self._tail_v[:, :, : self._tail_len]
 
     def _validate_shapes(self, k_new, v_new) -> None:
         # turbo_polar_cache.py:55-68, same order and messages.
@@ -288,80 +298,78 @@ class TurboPolarKVCacheRuntime:
                 )
                 quant_v = self.v_storage.to_quantized_block()
                 self._fused_views = (key, bufs, (compressed_k, quant_v))
-        return compressed_k, quant_v, self.partial_k, self.partial_v, None, self.actual_seq_len
+        tail_k, tail_v = self._tail_views()
+        return compressed_k, quant_v, tail_k, tail_v, None, self.actual_seq_len
 
-    def _maybe_encode_partial(self) -> Optional[Dict[str, Any]]:
-        """turbo_polar_cache.py:276-319: encode the zero-padded tail as a temporary page."""
-        if not self._tail_len:
-            return None
+    def _partial_page_store(self) -> Tuple[_lib.TPPages, int, bool]:
+        """Encode the zero-padded dense tail as one page (turbo_polar_cache.py:276-319)
+        and return ``(tp_pages, slot, in_storage)`` of where it went: the
+        storage's first free slot when the capacity has one (``in_storage``;
+        the stored pages and the tail page then form one run of slots), else a
+        one-page scratch store kept by the runtime.  Either is rewritten by the
+        next append."""
         B, H = self._batch_size, self._num_kv_heads
         dev = self._tail_k.device
-        bufs = self.polar_encoder.alloc_pages(B, H, 1, dev)
-        codes = torch.zeros((B, H, 1, PAGE, self._head_dim), dtype=torch.int8, device=dev)
-        scales = torch.zeros((B, H, 1, PAGE, self._head_dim // 32), dtype=torch.float16, device=dev)
-        pages = _lib.TPPages(
-            _lib.ptr(bufs["radii"]), _lib.ptr(bufs["radii_scales"]), _lib.ptr(bufs["angle_codes_l1"]),
-            _lib.ptr(bufs["angle_codes_deep"]), _lib.ptr(codes), _lib.ptr(scales), 1,
-        )
+        ks, vs = self.k_storage, self.v_storage
+        in_storage = ks.radii is not None and ks.block_count < ks.capacity
+        if in_storage:
+            pages, slot = pages_of(ks, vs), ks.block_count
+        else:
+            sc = self._scratch
+            if sc is None or sc["radii"].shape[:2] != (B, H) or sc["radii"].device != dev:
+                sc = self.polar_encoder.alloc_pages(B, H, 1, dev)
+                sc["v_codes"] = torch.zeros((B, H, 1, PAGE, self._head_dim), dtype=torch.int8, device=dev)
+                sc["v_scales"] = torch.zeros((B, H, 1, PAGE, self._head_dim // 32), dtype=torch.float16, device=dev)
+                sc["pages"] = _lib.TPPages(
+                    _lib.ptr(sc["radii"]), _lib.ptr(sc["radii_scales"]), _lib.ptr(sc["angle_codes_l1"]),
+                    _lib.ptr(sc["angle_codes_deep"]), _lib.ptr(sc["v_codes"]), _lib.ptr(sc["v_scales"]), 1,
+                )
+                self._scratch = sc
+            pages, slot = sc["pages"], 0
         # The encoder reads tokens past n_tokens as zeros: the reference's
         # mx.pad zero padding of the tail (turbo_polar_cache.py:282-285).
-        encode_pages(self._tail_k, self._tail_v, 0, self._tail_len, self.polar_encoder.layout, pages, 0)
-        return {
-            "radii": bufs["radii"],
-            "radii_scales": bufs["radii_scales"],
-            "angle_l1": bufs["angle_codes_l1"],
-            "angle_deep": bufs["angle_codes_deep"],
-            "quant_v": QuantizedVBlock(codes=codes, scales=scales, group_size=32),
-            "qjl": None,
-            "metadata": self.polar_encoder.metadata,
-        }
+        encode_pages(self._tail_k, self._tail_v, 0, self._tail_len, self.polar_encoder.layout, pages, slot)
+        return pages, slot, in_storage
 
     def get_blocks_for_attention(self):
-        """turbo_polar_cache.py:200-274: pages plus the padded tail page."""
-        partial = self._maybe_encode_partial()
-        L = self.config.block_size
-        if self.k_storage.block_count == 0:
-            if partial is None:
-                return None, None, None, None, self.actual_seq_len
-            r = partial["radii"]
-            unified_k = PolarKeyBlock(
-                radii=r,
-                angle_codes_l1=partial["angle_l1"],
-                angle_codes_deep=partial["angle_deep"],
-                radii_scales=partial["radii_scales"],
-                shape=(r.shape[0], r.shape[1], r.shape[2] * r.shape[3], r.shape[4] * 2),
-                block_size=L,
-                head_dim=self.config.head_dim,
-                metadata=partial["metadata"],
-            )
-            return unified_k, partial["quant_v"], None, None, self.actual_seq_len
+        """turbo_polar_cache.py:200-274: the stored pages plus the zero-padded
+        tail page, as one key block and one value block of S (+1) pages.
 
-        compressed_k = self.k_storage.to_unified_block(
-            (self._batch_size, self._num_kv_heads, self.k_storage.block_count * L, self._head_dim)
-        )
-        quant_v = self.v_storage.to_quantized_block()
-        if partial is not None:
-            radii = torch.cat([compressed_k.radii, partial["radii"]], dim=2)
-            rs = None
-            if compressed_k.radii_scales is not None and partial["radii_scales"] is not None:
-                rs = torch.cat([compressed_k.radii_scales, partial["radii_scales"]], dim=2)
-            compressed_k = PolarKeyBlock(
-                radii=radii,
-                angle_codes_l1=torch.cat([compressed_k.angle_codes_l1, partial["angle_l1"]], dim=2),
-                angle_codes_deep=torch.cat([compressed_k.angle_codes_deep, partial["angle_deep"]], dim=2),
-                radii_scales=rs,
-                shape=(radii.shape[0], radii.shape[1], radii.shape[2] * radii.shape[3], radii.shape[4] * 2),
-                block_size=L,
-                head_dim=self.config.head_dim,
-                metadata=compressed_k.metadata,
-            )
-            pv = partial["quant_v"]
-            quant_v = QuantizedVBlock(
-                codes=torch.cat([quant_v.codes, pv.codes], dim=2),
-                scales=torch.cat([quant_v.scales, pv.scales], dim=2),
-                group_size=quant_v.group_size,
-            )
-        return compressed_k, quant_v, None, None, self.actual_seq_len
+        The tail page is encoded into the storage's first free slot when there
+        is one, and the blocks are then views of the storage (no copy of the
+        cache; valid until the next append).  Only when the storage is full is
+        it encoded into a scratch page and the blocks concatenated."""
+        L = self.config.block_size
+        n = self.k_storage.block_count
+        if n == 0 and not self._tail_len:
+            return None, None, None, None, self.actual_seq_len
+        shape_of = lambda r: (r.shape[0], r.shape[1], r.shape[2] * r.shape[3], self._head_dim)  # noqa: E731
+        if not self._tail_len:
+            k = self.k_storage.to_unified_block((self._batch_size, self._num_kv_heads, n * L, self._head_dim))
+            return k, self.v_storage.to_quantized_block(), None, None, self.actual_seq_len
+        _, _, in_storage = self._partial_page_store()
+        ks, vs = self.k_storage, self.v_storage
+        if in_storage:
+            sl = slice(0, n + 1)
+            radii, l1, deep = ks.radii[:, :, sl], ks.angle_codes_l1[:, :, sl], ks.angle_codes_deep[:, :, sl]
+            rs = ks.radii_scales[:, :, sl] if ks.radii_scales is not None else None
+            codes, scales = vs.codes[:, :, sl], vs.scales[:, :, sl]
+        else:
+            sc = self._scratch
+            radii, l1, deep, rs = sc["radii"], sc["angle_codes_l1"], sc["angle_codes_deep"], sc["radii_scales"]
+            codes, scales = sc["v_codes"], sc["v_scales"]
+            if n:
+                radii = torch.cat([ks.radii[:, :, :n], radii], dim=2)
+                l1 = torch.cat([ks.angle_codes_l1[:, :, :n], l1], dim=2)
+                deep = torch.cat([ks.angle_codes_deep[:, :, :n], deep], dim=2)
+                if rs is not None:
+                    rs = torch.cat([ks.radii_scales[:, :, :n], rs], dim=2)
+                codes = torch.cat([vs.codes[:, :, :n], codes], dim=2)
+                scales = torch.cat([vs.scales[:, :, :n], scales], dim=2)
+        key = PolarKeyBlock(radii=radii, angle_codes_l1=l1, angle_codes_deep=deep, radii_scales=rs,
+                            shape=shape_of(radii), block_size=L, head_dim=self.config.head_dim,
+                            metadata=self.polar_encoder.metadata)
+        return key, QuantizedVBlock(codes=codes, scales=scales, group_size=32), None, None, self.actual_seq_len
 
     def fetch_blocks(self, indices: Optional[list] = None) -> torch.Tensor:
         """turbo_polar_cache.py:321-346: decode selected pages to dense fp16 keys."""
@@ -423,6 +431,8 @@ class TurboPolarKVCacheRuntime:
         self._tail_k = None
         self._tail_v = None
         self._tail_len = 0
+        self._scratch = None
+        self._fused_views = None
         self._initialized = False
         self._batch_size = None
         self._num_kv_heads = None

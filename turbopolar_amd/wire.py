@@ -88,8 +88,9 @@ def state_dict(cache) -> Tuple[Dict[str, torch.Tensor], Dict[str, str]]:
         tensors["v.codes"] = _host_copy(vs.codes[:, :, :S])
         tensors["v.scales"] = _host_copy(vs.scales[:, :, :S])
     if rt._tail_len:
-        tensors["tail.k"] = _host_copy(rt.partial_k)
-        tensors["tail.v"] = _host_copy(rt.partial_v)
+        tail_k, tail_v = rt._tail_views()
+        tensors["tail.k"] = _host_copy(tail_k)
+        tensors["tail.v"] = _host_copy(tail_v)
     devices = {t.device for t in (rt.k_storage.radii, rt._tail_k) if t is not None and t.is_cuda}
     for d in devices:
         torch.cuda.synchronize(d)
