@@ -33,6 +33,8 @@ extern "C" {
 
 #define TP_PAGE_TOKENS 64
 #define TP_HEAD_DIM 128
+/* Static split-K scratch per GPU of tp_decode_attention_noalloc. */
+#define TP_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
 
 /* Status codes.  The Python shim maps TP_ERR_INVALID to ValueError and the
  * others to RuntimeError, mirroring the reference's exception contract. */
@@ -138,6 +140,27 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
                             int32_t tail_len, int64_t tail_stride, int64_t actual_seq_len,
                             float scale, int32_t pages_per_split, void* workspace,
                             size_t workspace_bytes, void* out, void* stream);
+
+/*
+ * tp_decode_attention without a workspace argument: allocates nothing (no
+ * hipMalloc, hipFree or allocating library call).  No counterpart in the
+ * reference; it is for callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid allocation.
+ * The split-K records and ticket counters live in a static device scratch
+ * array of TP_NOALLOC_SCRATCH_BYTES (8 MiB) per GPU, held until the
+ * process ends.  A call whose tp_decode_workspace_bytes(...) exceeds it
+ * returns TP_ERR_WORKSPACE (raise pages_per_split, or use
+ * tp_decode_attention).  All calls on one GPU share that GPU's scratch, so
+ * calls that can run concurrently on one GPU (other streams, other threads)
+ * race; calls on one stream are ordered and safe.  The first call on a GPU
+ * looks up the scratch address and clears its counter area with a kernel on
+ * `stream`.  Other arguments, results and errors as tp_decode_attention.
+ */
+int32_t tp_decode_attention_noalloc(const void* q, int64_t batch, int32_t hq, int32_t hkv,
+                                    const tp_page_layout* layout, const tp_pages* pages,
+                                    int32_t n_pages, const void* tail_k, const void* tail_v,
+                                    int32_t tail_len, int64_t tail_stride, int64_t actual_seq_len,
+                                    float scale, int32_t pages_per_split, void* out, void* stream);
 
 /* Workspace size for tp_decode_attention (same arguments). */
 size_t tp_decode_workspace_bytes(int64_t batch, int32_t hq, int32_t hkv, int32_t n_pages,

@@ -23,6 +23,7 @@ TP_ERR_UNSUPPORTED = 2
 TP_ERR_HIP = 3
 TP_ERR_WORKSPACE = 4
 TP_ERR_NONFINITE = 5
+TP_NOALLOC_SCRATCH_BYTES = 8 << 20  # include/turbopolar.h
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -73,6 +74,13 @@ _SIGNATURES = {
         [
             c_vp, c_i64, c_i32, c_i32, _P_LAYOUT, _P_PAGES, c_i32,
             c_vp, c_vp, c_i32, c_i64, c_i64, c_float, c_i32, c_vp, c_size, c_vp, c_vp,
+        ],
+    ),
+    "tp_decode_attention_noalloc": (
+        c_i32,
+        [
+            c_vp, c_i64, c_i32, c_i32, _P_LAYOUT, _P_PAGES, c_i32,
+            c_vp, c_vp, c_i32, c_i64, c_i64, c_float, c_i32, c_vp, c_vp,
         ],
     ),
     "tp_decode_workspace_bytes": (c_size, [c_i64, c_i32, c_i32, c_i32, c_i32, c_i32]),

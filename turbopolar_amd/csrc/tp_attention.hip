@@ -30,6 +30,8 @@
 // _dense_tail (tqpolar_online_attention.metal:197-390,393-629): tokens with
 // global index >= actual_seq_len are masked, the dense fp16 tail follows the
 // pages, fp32 softmax statistics and accumulation, fp16 output.
+#include <mutex>
+
 #include "tp_common.h"
 
 namespace tp {
@@ -1112,3 +1114,94 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
 }
 
 }  // extern "C"
+
+// ---- entry point that allocates nothing -----------------------------------------
+//
+// tp_decode_attention_noalloc keeps its split-K records and ticket counters in
+// `scratch`, a file-scope device array (kScratchBytes per GPU, held for the
+// life of the process), instead of a caller-provided workspace.  Host code
+// never passes the array's name to a kernel or a copy: the name is a host-side
+// stand-in.  Its device address is taken once per device with
+// hipGetSymbolAddress, with that device current, and kept per device.
+
+namespace tp {
+
+constexpr size_t kScratchBytes = TP_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+
+__global__ __launch_bounds__(256) void clear_words_kernel(uint32_t* p, uint32_t n) {
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) p[i] = 0u;
+}
+
+// Device address of `scratch` on the device of `stream`.  The first call on a
+// device looks it up and clears the ticket-counter area with a fill kernel on
+// `stream` (a kernel, not a memset node, so the call can sit inside a captured
+// graph); every decode launch leaves the counters zero again.
+static int32_t scratch_of(hipStream_t stream, size_t counter_bytes, void** out) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("tp_decode_attention_noalloc: cannot resolve the stream's device (%s)", hipGetErrorString(e));
+    return TP_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) {
+      set_error("tp_decode_attention_noalloc: hipGetDevice failed");
+      return TP_ERR_HIP;
+    }
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) {
+      set_error("tp_decode_attention_noalloc: hipSetDevice(%d) failed", dev);
+      return TP_ERR_HIP;
+    }
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && p) {
+      const uint32_t words = (uint32_t)(counter_bytes / sizeof(uint32_t));
+      hipLaunchKernelGGL(clear_words_kernel, dim3((words + 255) / 256 < 64 ? (words + 255) / 256 : 64), dim3(256), 0,
+                         stream, static_cast<uint32_t*>(p), words);
+      e = hipGetLastError();
+    }
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p) {
+      set_error("tp_decode_attention_noalloc: scratch set-up failed: %s", hipGetErrorString(e));
+      return TP_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TP_OK;
+}
+
+}  // namespace tp
+
+extern "C" int32_t tp_decode_attention_noalloc(const void* q, int64_t batch, int32_t hq, int32_t hkv,
+                                               const tp_page_layout* layout, const tp_pages* pages,
+                                               int32_t n_pages, const void* tail_k, const void* tail_v,
+                                               int32_t tail_len, int64_t tail_stride, int64_t actual_seq_len,
+                                               float scale, int32_t pages_per_split, void* out, void* stream) {
+  clear_error();
+  if (pages_per_split <= 0) pages_per_split = tp_default_pages_per_split(batch, hq, hkv, n_pages);
+  const bool split = n_pages > 0 && n_splits_of(n_pages, pages_per_split) > 1;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  if (split && batch >= 1 && hq >= 1 && hkv >= 1) {
+    const size_t need = tp_decode_workspace_bytes(batch, hq, hkv, n_pages, tail_len, pages_per_split);
+    if (need > kScratchBytes) {
+      set_error("tp_decode_attention_noalloc: this call needs %zu bytes of split-K scratch, the library's static "
+                "scratch holds %zu; raise pages_per_split or call tp_decode_attention with a workspace",
+                need, kScratchBytes);
+      return TP_ERR_WORKSPACE;
+    }
+    const int32_t st = scratch_of(static_cast<hipStream_t>(stream), tp_decode_counter_bytes(batch, hq, hkv), &ws);
+    if (st != TP_OK) return st;
+    ws_bytes = kScratchBytes;
+  }
+  return tp_decode_attention(q, batch, hq, hkv, layout, pages, n_pages, tail_k, tail_v, tail_len, tail_stride,
+                             actual_seq_len, scale, pages_per_split, ws, ws_bytes, out, stream);
+}
