@@ -717,6 +717,73 @@ def run_snapshot(args, layout, reps: int = 3) -> dict:
             "identical": bool(same)}
 
 
+def run_timeline(args, layout) -> dict:
+    """Phase timeline of the decode kernel: the same workload as the headline
+    line, run on libturbopolar_hip_timeline.so (the product's code with the
+    kernel's s_memrealtime phase stamps compiled in, TP_TIMELINE).  Thread 0 of
+    every workgroup stamps its start, the issue of its first loads, each of
+    wave 0's pages (scored once its codes arrived, done), the end of wave 0's
+    pages, the workgroup's record stores, their completion and its ticket; the
+    last workgroup of each unit also stamps the end of its combine.  The stamps of the last of ``steps``
+    back-to-back launches are read back; times are microseconds from the first
+    workgroup's start (100 MHz clock), median and max over workgroups."""
+    import torch
+
+    from turbopolar_amd import _lib, build
+    from turbopolar_amd.kernels import fp16_scale
+
+    if _lib._lib is not None:
+        raise RuntimeError("the timeline workload must load its library first")
+    _lib.LIB_PATH = build.TIMELINE_LIB_PATH
+    if not args.rotate:
+        args.rotate = max(4, int(np.ceil(320e6 / algorithmic_bytes(args.hq, args.hkv, args.context // 64, layout))))
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg, caches = build_caches(args, dev, layout)
+    L = _lib.lib()
+    n_pages = caches[0]["pages"].S
+    pps = args.pps or int(L.tp_default_pages_per_split(1, args.hq, args.hkv, n_pages))
+    need = int(L.tp_decode_workspace_bytes(1, args.hq, args.hkv, n_pages, 0, pps))
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    scale = fp16_scale(cfg.attention_scale)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    for i in range(args.warmup + args.steps):
+        c = caches[i % len(caches)]
+        ps = c["pages"]
+        st = L.tp_decode_attention(c["q"].data_ptr(), 1, args.hq, args.hkv, ctypes.byref(ps.layout),
+                                   ctypes.byref(ps.pages), n_pages, None, None, 0, 0, c["seq"], scale, pps,
+                                   ws.data_ptr(), need, c["out"].data_ptr(), stream)
+        _lib.check(st, "tp_decode_attention")
+    torch.cuda.synchronize()
+    L.tp_timeline_address.restype = ctypes.c_void_p
+    addr = L.tp_timeline_address()
+    stamps = np.zeros((2048, 64), np.uint64)
+    hip = ctypes.CDLL("libamdhip64.so")
+    rc = hip.hipMemcpy(stamps.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(addr), ctypes.c_size_t(stamps.nbytes), 2)
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpy of the stamps failed: {rc}")
+    units = args.hkv * ((args.hq // args.hkv + 15) // 16)
+    groups = units * ((n_pages + pps - 1) // pps)
+    t = stamps[:groups].astype(np.int64)
+    start = t[:, 0]
+    us = (t - start.min()) / 100.0
+    valid = t >= start[:, None]  # stamps written by this launch
+    names = {0: "start", 2: "first loads issued, code tables ready"}
+    for i in range(12):
+        names[4 + 4 * i] = f"wave 0 page {i}: codes arrived, scored"
+        names[5 + 4 * i] = f"wave 0 page {i}: done"
+    names.update({52: "wave 0 pages done", 53: "workgroup record stored", 54: "stores complete",
+                  55: "ticket drawn", 57: "last workgroup: records folded", 58: "last workgroup: groups merged",
+                  56: "last workgroup: output stored"})
+    phases = {}
+    for k, name in names.items():
+        col = us[valid[:, k], k]
+        if col.size:
+            phases[name] = {"median_us": round(float(np.median(col)), 2), "max_us": round(float(col.max()), 2),
+                            "workgroups": int(col.size)}
+    return {"phases": phases, "pps": pps, "groups": groups}
+
+
 def profiled_traffic(name: str, args):
     """HBM bytes per launch that the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     summary profiles/<name>_8b_32k_traffic.json records, when this run is that
@@ -801,7 +868,8 @@ def main():
     ap.add_argument("--rotate", type=int, default=0, help="independent caches to rotate (0 = auto, >256 MB)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=["decode", "encode", "append", "layers", "model", "decompress", "snapshot", "qk"],
+    ap.add_argument("--workload", choices=["decode", "encode", "append", "layers", "model", "decompress", "snapshot", "qk",
+                                           "timeline"],
                     default="decode",
                     help="decode (the BASELINE metric, default); encode / append: configs[3] workloads; "
                          "layers: configs[1] (--layers decode launches per step); "
@@ -871,6 +939,11 @@ def main():
             "algorithmic_bytes_per_step": {"read": r["read"], "write": r["write"]},
             "cpu_baseline": cpu,
         }))
+        return
+    if args.workload == "timeline":
+        r = run_timeline(args, layout)
+        print(json.dumps({"workload": workload_name(args) + " -- kernel phase timeline", "layout": args.layout,
+                          "pages_per_split": r["pps"], "workgroups": r["groups"], "phases": r["phases"]}))
         return
     if args.workload == "model":
         r = run_model(args)

@@ -2,7 +2,10 @@
 
 Run as ``python -m turbopolar_amd.build`` or through ``__graft_entry__.build()``.
 Every call recompiles.  Objects go to ``turbopolar_amd/_build/`` and the shared
-library to ``turbopolar_amd/libturbopolar_hip.so``.
+library to ``turbopolar_amd/libturbopolar_hip.so``.  A second library,
+``libturbopolar_hip_timeline.so``, is the same code with the decode kernel's
+phase stamps compiled in (``-DTP_TIMELINE``); only ``bench.py --workload
+timeline`` loads it.
 """
 
 from __future__ import annotations
@@ -20,6 +23,7 @@ CSRC = PKG_DIR / "csrc"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_NAME = "libturbopolar_hip.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+TIMELINE_LIB_PATH = PKG_DIR / "libturbopolar_hip_timeline.so"
 ARCH = os.environ.get("TP_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["tp_api.hip", "tp_encode.hip", "tp_attention.hip", "tp_decode.hip", "tp_append.hip"]
@@ -47,8 +51,8 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found; the TurboPolar HIP library cannot be built")
 
 
-def _compile(src: Path, obj: Path) -> None:
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj: Path, defines=()) -> None:
+    cmd = [_hipcc(), *HIPCC_FLAGS, *[f"-D{d}" for d in defines], "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
@@ -57,23 +61,30 @@ def _compile(src: Path, obj: Path) -> None:
 def build(verbose: bool = True) -> Path:
     BUILD_DIR.mkdir(exist_ok=True)
     objs = []
-    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as ex:
+    timeline_obj = BUILD_DIR / "tp_attention_timeline.o"
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES) + 1, 8)) as ex:
         futs = []
         for name in SOURCES:
             obj = BUILD_DIR / (Path(name).stem + ".o")
             objs.append(obj)
             futs.append(ex.submit(_compile, CSRC / name, obj))
+        futs.append(ex.submit(_compile, CSRC / "tp_attention.hip", timeline_obj, ("TP_TIMELINE",)))
         for f in futs:
             f.result()
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _link(objs, LIB_PATH)
+    _link([timeline_obj if o.stem == "tp_attention" else o for o in objs], TIMELINE_LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+def _link(objs, out: Path) -> None:
+    tmp = out.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
-    if verbose:
-        print(f"built {LIB_PATH}")
-    return LIB_PATH
+    os.replace(tmp, out)
 
 
 if __name__ == "__main__":

@@ -36,6 +36,31 @@
 
 namespace tp {
 
+#ifdef TP_TIMELINE
+// Phase stamps of the decode kernel (s_memrealtime, 100 MHz), written by
+// thread 0 of workgroups < kTimelineGroups; read by tp_timeline_address().
+// Built only into the timeline library (TP_TIMELINE defined), never into the
+// product.
+constexpr int kTimelineGroups = 2048;
+constexpr int kTimelineStamps = 64;
+__device__ unsigned long long g_timeline[kTimelineGroups][kTimelineStamps];
+#define TP_STAMP(k)                                                                            \
+  do {                                                                                          \
+    if (threadIdx.x == 0 && blockIdx.x < kTimelineGroups)                                       \
+      g_timeline[blockIdx.x][(k)] = __builtin_amdgcn_s_memrealtime();                           \
+  } while (0)
+#else
+#define TP_STAMP(k) \
+  do {              \
+  } while (0)
+#endif
+// Stamp slots (thread 0, i.e. wave 0, of each workgroup): 0 start, 2 first
+// loads issued and code tables ready, 4 + 4i QK of wave 0's page i done (its
+// codes arrived), 5 + 4i its PV done, 52 wave 0's pages done; then for the
+// whole workgroup 53 records stored, 54 stores complete, 55 ticket drawn; the
+// last workgroup of a unit: 57 its record loads folded (thread 0's), 58 split
+// groups merged, 56 output stored.
+
 enum LayoutKind { kKindDefault = 0, kKindFast = 1, kKindGeneric = 2 };
 
 struct AttnArgs {
@@ -75,6 +100,22 @@ struct AttnArgs {
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Page loads carry the non-temporal hint: every page byte is read once per
+// step, and streaming them past the caches measured faster (32k: 20.4 -> 19.7
+// us, 131k: 58.5 -> 54.3 us per step).
+__device__ __forceinline__ uint4 ldnt4(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldnt2(const void* p) {
+  const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ldnt1(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
 
 __device__ __forceinline__ half8v as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   const u32x4 v = {a, b, c, d};
@@ -211,9 +252,9 @@ __device__ __forceinline__ void load_k(const AttnArgs& a, int64_t slot, int l16,
     for (int mt = 0; mt < 4; ++mt) {
       const int t = 16 * mt + l16;
       const uint4* rp = reinterpret_cast<const uint4*>(rbase + t * kPairs);
-      k.r[mt][0] = rp[0];
-      k.r[mt][1] = rp[1];
-      k.c[mt] = *reinterpret_cast<const uint2*>(cbase + t * 16);
+      k.r[mt][0] = ldnt4(rp);
+      k.r[mt][1] = ldnt4(rp + 1);
+      k.c[mt] = ldnt2(cbase + t * 16);
     }
   } else if constexpr (KIND == kKindFast) {
     const int8_t* rbase = static_cast<const int8_t*>(a.radii) + slot * (kPageTokens * kPairs) + 16 * l4;
@@ -221,8 +262,8 @@ __device__ __forceinline__ void load_k(const AttnArgs& a, int64_t slot, int l16,
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int t = 16 * mt + l16;
-      k.r[mt] = *reinterpret_cast<const uint4*>(rbase + t * kPairs);
-      k.c[mt] = *reinterpret_cast<const uint4*>(cbase + t * kPairs);
+      k.r[mt] = ldnt4(rbase + t * kPairs);
+      k.c[mt] = ldnt4(cbase + t * kPairs);
     }
     k.ls_bits = a.radii_scales[slot];
   } else {
@@ -357,12 +398,12 @@ __device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16,
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int t = v_token(ks, l4, e);
-      v.w[8 * ks + e] = *reinterpret_cast<const uint2*>(vbase + t * kHeadDim);
+      v.w[8 * ks + e] = ldnt2(vbase + t * kHeadDim);
     }
   }
   const uint32_t* sbase = reinterpret_cast<const uint32_t*>(a.v_scales + slot * (kPageTokens * kVGroups));
-  v.sd[0] = sbase[lane];
-  v.sd[1] = sbase[lane + 64];
+  v.sd[0] = ldnt1(sbase + lane);
+  v.sd[1] = ldnt1(sbase + lane + 64);
 }
 
 // acc[j] += Vhat^T tile j x P, Vhat = f16(code * scale) exactly: codes become
@@ -495,14 +536,10 @@ __device__ __forceinline__ void softmax_page(const float4v* s, int valid, float 
 
 // ---- cross-workgroup exchange ----------------------------------------------------
 //
-// Partials are written with sc1 (agent-coherent, write-through) vector stores,
-// so no L2 write-back is needed; each wave waits for its stores to be
-// acknowledged before the workgroup barrier that precedes the ticket atomic.
-// The workgroup that draws the last ticket reads every partial with ordinary
-// loads: the sc1 stores have reached memory before the ticket was taken, and no
-// cache can hold an older copy of a partial line, because nothing reads the
-// partials before the last ticket within a launch and the caches are
-// invalidated at every kernel launch.
+// Records are written with sc1 (write-through) vector stores, so the
+// agent-scope release fence before the ticket has little dirty data to write
+// back; each wave waits for its stores before the workgroup barrier that
+// precedes the release and the ticket (finish_unit).
 
 __device__ __forceinline__ void st_agent4(float* p, float4v v) {
   asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
@@ -646,6 +683,139 @@ struct AttnShared {
   int last;
 };
 
+// ---- end of a split: merge the waves, publish the record, combine ------------------
+//
+// Every wave holds an online-softmax state (m_run, l_run, acc) of its tokens:
+// lane (head l16, lane group l4) holds dims 32*l4 + 8*i + j of head l16 in
+// acc[j][i] and a partial l over its own scores.  The waves merge through LDS
+// into one (m, l, acc[128]) per head; with one split that is the output,
+// otherwise it becomes the split's record and the last split of the unit to
+// arrive combines all records.
+//
+// Cross-workgroup ordering follows the HIP memory model at agent scope: every
+// wave's record stores complete (s_waitcnt) before the workgroup barrier, then
+// one thread issues an agent-scope release fence and the relaxed ticket; the
+// workgroup that draws the last ticket issues an agent-scope acquire fence
+// before the barrier after which it reads the records.
+template <int WAVES, class Merge>
+__device__ __forceinline__ void finish_unit(Merge& sh, const AttnArgs& a, int wave, int tid, float m_run, float l_run,
+                                            const float4v* acc, int b, int kv, int h0, int nh, int64_t bkv, int hb,
+                                            int split) {
+  const int lane = tid & 63;
+  const int l16 = lane & 15;
+  const int l4 = lane >> 4;
+  const bool member = wave < WAVES;  // waves past WAVES hold no state and only keep the barriers
+  // Merge the waves through LDS.
+  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  if (member && l4 == 0) sh.ml[wave][l16] = make_float2(m_run, l_tot);
+  // The lane holds dims 32*l4 + 8*i + j (acc[j][i]) of head l16: eight 16-byte
+  // writes of 4 consecutive dims each; with the 132-float row stride the 8
+  // lanes of each write phase cover all banks once.
+  float* arow = &sh.acc[member ? wave : 0][l16 * kRedStride + 32 * l4];
+  if (member && l16 < nh) {  // rows of heads past the block's own hold nothing the fold reads
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int i = q >> 1, j0 = 4 * (q & 1);
+      *reinterpret_cast<float4v*>(arow + 4 * q) = float4v{acc[j0][i], acc[j0 + 1][i], acc[j0 + 2][i], acc[j0 + 3][i]};
+    }
+  }
+  lds_barrier();
+
+  // Fold the waves' records: thread t owns dims 4 (t % 32) .. +3 of head
+  // t / 32 and folds the WAVES records in wave order (one 16-byte LDS read per
+  // record; spreading 4 heads over all 512 threads at one dim each was slower).
+  const int h = tid >> 5;
+  const int d0 = (tid & 31) << 2;
+  const bool live = h < nh;
+  float M = -INFINITY, L = 0.0f;
+  float A[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (live) fold_waves(sh, h, d0, M, L, A);
+  if (a.n_splits == 1) {
+    if (live)
+      store_out4(a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + h) * kHeadDim + d0, A,
+                 __builtin_amdgcn_rcpf(L));
+    return;
+  }
+  const int64_t unit = bkv * a.head_blocks + hb;
+  const int S = a.n_splits;
+  const int Sp = (S + 1) & ~1;  // (m, l) row length in pairs
+  if (live) {
+    if (d0 == 0) st_agent2(a.part_ml + ((unit * 16 + h) * Sp + split) * 2, M, L);
+    st_agent4(a.part_acc + ((unit * S + split) * 16 + h) * kHeadDim + d0, float4v{A[0], A[1], A[2], A[3]});
+  }
+  TP_STAMP(53);
+  wait_stores();
+  __syncthreads();
+  TP_STAMP(54);
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(a.counters + unit * a.counter_stride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev == (uint32_t)(S - 1);
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    sh.last = last;
+  }
+  __syncthreads();
+  TP_STAMP(55);
+  if (!sh.last) return;
+
+  // Last workgroup of this (b, kv, head block): combine the n_splits records.
+  // Items are (head hh, 4-dim chunk c4), nh * 32 of them, padded to a power
+  // of two 2^ish; thread (item, sg), sg < SG = 512 / 2^ish, folds splits
+  // sg, sg + SG, ... online (running max, rescaled sums), with all loads of a
+  // batch of records in flight together (batches of 4 when no thread has more
+  // than 4 records, else 8: every load of a batch costs load bandwidth of the
+  // one CU that combines); the SG partial folds then meet in LDS and are
+  // merged in sg order.
+  const int n_items = nh * 32;
+  const int ish = n_items <= 32 ? 5 : (n_items <= 64 ? 6 : (n_items <= 128 ? 7 : (n_items <= 256 ? 8 : 9)));
+  const int lsg = 9 - ish;
+  const int SG = 1 << lsg;
+  const int it = tid & ((1 << ish) - 1);
+  const int sg = tid >> ish;
+  const bool item = it < n_items && tid < WAVES * 64;
+  const int hh = it >> 5;
+  const int c4 = it & 31;
+  const int mine = item ? (S - sg + SG - 1) >> lsg : 0;
+  const float* pac = a.part_acc + ((unit * S + sg) * 16 + hh) * kHeadDim + 4 * c4;
+  const float* pml = a.part_ml + ((unit * 16 + hh) * Sp + sg) * 2;
+  const int64_t rstride = (int64_t)SG * 16 * kHeadDim;
+  float Mc = -INFINITY, Lc = 0.0f;
+  float4v Ac = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  if (((S + SG - 1) >> lsg) <= 4)
+    fold_records<4>(pml, pac, SG, rstride, mine, Mc, Lc, Ac);
+  else
+    fold_records<8>(pml, pac, SG, rstride, mine, Mc, Lc, Ac);
+  TP_STAMP(57);
+  if (SG > 1) {
+    float4v* red = reinterpret_cast<float4v*>(&sh.acc[0][0]);
+    float2* redml = reinterpret_cast<float2*>(red + (WAVES * 64));
+    if (item) {
+      red[tid] = Ac;
+      redml[tid] = make_float2(Mc, Lc);
+    }
+    lds_barrier();
+    if (sg == 0 && item) {
+      if (lsg == 1)
+        merge_groups<2>(red, redml, it, ish, Mc, Lc, Ac);
+      else if (lsg == 2)
+        merge_groups<4>(red, redml, it, ish, Mc, Lc, Ac);
+      else if (lsg == 3)
+        merge_groups<8>(red, redml, it, ish, Mc, Lc, Ac);
+      else
+        merge_groups<16>(red, redml, it, ish, Mc, Lc, Ac);
+    }
+  }
+  TP_STAMP(58);
+  if (sg == 0 && item) {
+    const float inv = __builtin_amdgcn_rcpf(Lc);
+    uint16_t* orow3 = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + hh) * kHeadDim + 4 * c4;
+    *reinterpret_cast<uint2*>(orow3) = make_uint2((uint32_t)f2h(Ac[0] * inv) | ((uint32_t)f2h(Ac[1] * inv) << 16),
+                                                  (uint32_t)f2h(Ac[2] * inv) | ((uint32_t)f2h(Ac[3] * inv) << 16));
+  }
+  if (tid == 0) __hip_atomic_store(a.counters + unit * a.counter_stride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  TP_STAMP(56);
+}
+
 // ---- decode attention kernel ---------------------------------------------------
 
 template <int KIND, int WAVES>
@@ -654,6 +824,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   // per thread, and the combine sizes its split groups for 512 threads.
   static_assert(WAVES == 8, "decode_attention_kernel assumes 8 waves per workgroup");
   __shared__ AttnShared<WAVES> sh;
+  TP_STAMP(0);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -706,6 +877,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   }
   if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
   lds_barrier();
+  TP_STAMP(2);
 
   const int sbase4 = 4 * (8 * l4 + (l16 >> 3));
   const uint32_t ssel = (l16 & 4) ? 0x07060302u : 0x05040100u;
@@ -721,14 +893,16 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   // unconditional and every wait covers only the loads it needs: QK waits for
   // the page's K codes while its V codes may still be in flight.  A page with
   // a successor is fully valid (only the last live page can be partial).
-  for (; page + WAVES < p_end; page += WAVES) {
+  for (int it = 0; page + WAVES < p_end; page += WAVES, ++it) {
     float4v s[4];
     qk_regs<KIND>(a, sh.lut, kr, qb, l16, l4, s);
+    if (it < 12) TP_STAMP(4 + 4 * it);
     load_k<KIND>(a, bkv * a.capacity + page + WAVES, l16, l4, kr);
     half8v pb[2];
     softmax_page(s, kPageTokens, a.scale_log2, l4, m_run, l_run, acc, pb);
     pv_regs(vr, sbase4, ssel, pb, acc);
     load_v(a, bkv * a.capacity + page + WAVES, l16, l4, lane, vr);
+    if (it < 12) TP_STAMP(5 + 4 * it);
   }
   if (page < p_end) {
     float4v s[4];
@@ -755,105 +929,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     }
   }
 
-  // Merge the waves through LDS.
-  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
-  if (l4 == 0) sh.ml[wave][l16] = make_float2(m_run, l_tot);
-  // The lane holds dims 32*l4 + 8*i + j (acc[j][i]) of head l16: eight 16-byte
-  // writes of 4 consecutive dims each; with the 132-float row stride the 8
-  // lanes of each write phase cover all banks once.
-  float* arow = &sh.acc[wave][l16 * kRedStride + 32 * l4];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int i = q >> 1, j0 = 4 * (q & 1);
-    *reinterpret_cast<float4v*>(arow + 4 * q) = float4v{acc[j0][i], acc[j0 + 1][i], acc[j0 + 2][i], acc[j0 + 3][i]};
-  }
-  lds_barrier();
-
-  // Fold the waves' records: thread t owns dims 4 (t % 32) .. +3 of head
-  // t / 32 and folds the WAVES records in wave order (one 16-byte LDS read per
-  // record; spreading 4 heads over all 512 threads at one dim each was slower).
-  const int h = tid >> 5;
-  const int d0 = (tid & 31) << 2;
-  const bool live = h < nh;
-  float M = -INFINITY, L = 0.0f;
-  float A[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (live) fold_waves(sh, h, d0, M, L, A);
-  if (a.n_splits == 1) {
-    if (live)
-      store_out4(a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + h) * kHeadDim + d0, A,
-                 __builtin_amdgcn_rcpf(L));
-    return;
-  }
-  const int64_t unit = bkv * a.head_blocks + hb;
-  const int S = a.n_splits;
-  const int Sp = (S + 1) & ~1;  // (m, l) row length in pairs
-  if (live) {
-    if (d0 == 0) st_agent2(a.part_ml + ((unit * 16 + h) * Sp + split) * 2, M, L);
-    st_agent4(a.part_acc + ((unit * S + split) * 16 + h) * kHeadDim + d0, float4v{A[0], A[1], A[2], A[3]});
-  }
-  wait_stores();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(a.counters + unit * a.counter_stride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh.last = prev == (uint32_t)(S - 1);
-  }
-  __syncthreads();
-  if (!sh.last) return;
-
-  // Last workgroup of this (b, kv, head block): combine the n_splits records.
-  // Items are (head hh, 4-dim chunk c4), nh * 32 of them, padded to a power
-  // of two 2^ish; thread (item, sg), sg < SG = 512 / 2^ish, folds splits
-  // sg, sg + SG, ... online (running max, rescaled sums), with all loads of a
-  // batch of records in flight together (batches of 4 when no thread has more
-  // than 4 records, else 8: every load of a batch costs load bandwidth of the
-  // one CU that combines); the SG partial folds then meet in LDS and are
-  // merged in sg order.
-  const int n_items = nh * 32;
-  const int ish = n_items <= 32 ? 5 : (n_items <= 64 ? 6 : (n_items <= 128 ? 7 : (n_items <= 256 ? 8 : 9)));
-  const int lsg = 9 - ish;
-  const int SG = 1 << lsg;
-  const int it = tid & ((1 << ish) - 1);
-  const int sg = tid >> ish;
-  const bool item = it < n_items;
-  const int hh = it >> 5;
-  const int c4 = it & 31;
-  const int mine = item ? (S - sg + SG - 1) >> lsg : 0;
-  const float* pac = a.part_acc + ((unit * S + sg) * 16 + hh) * kHeadDim + 4 * c4;
-  const float* pml = a.part_ml + ((unit * 16 + hh) * Sp + sg) * 2;
-  const int64_t rstride = (int64_t)SG * 16 * kHeadDim;
-  float Mc = -INFINITY, Lc = 0.0f;
-  float4v Ac = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-  if (((S + SG - 1) >> lsg) <= 4)
-    fold_records<4>(pml, pac, SG, rstride, mine, Mc, Lc, Ac);
-  else
-    fold_records<8>(pml, pac, SG, rstride, mine, Mc, Lc, Ac);
-  if (SG > 1) {
-    float4v* red = reinterpret_cast<float4v*>(&sh.acc[0][0]);
-    float2* redml = reinterpret_cast<float2*>(red + (WAVES * 64));
-    if (item) {
-      red[tid] = Ac;
-      redml[tid] = make_float2(Mc, Lc);
-    }
-    lds_barrier();
-    if (sg == 0 && item) {
-      if (lsg == 1)
-        merge_groups<2>(red, redml, it, ish, Mc, Lc, Ac);
-      else if (lsg == 2)
-        merge_groups<4>(red, redml, it, ish, Mc, Lc, Ac);
-      else if (lsg == 3)
-        merge_groups<8>(red, redml, it, ish, Mc, Lc, Ac);
-      else
-        merge_groups<16>(red, redml, it, ish, Mc, Lc, Ac);
-    }
-  }
-  if (sg == 0 && item) {
-    const float inv = __builtin_amdgcn_rcpf(Lc);
-    uint16_t* orow3 = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + hh) * kHeadDim + 4 * c4;
-    *reinterpret_cast<uint2*>(orow3) = make_uint2((uint32_t)f2h(Ac[0] * inv) | ((uint32_t)f2h(Ac[1] * inv) << 16),
-                                                  (uint32_t)f2h(Ac[2] * inv) | ((uint32_t)f2h(Ac[3] * inv) << 16));
-  }
-  if (tid == 0) __hip_atomic_store(a.counters + unit * a.counter_stride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  TP_STAMP(52);
+  finish_unit<WAVES>(sh, a, wave, tid, m_run, l_run, acc, b, kv, h0, nh, bkv, hb, split);
 }
 
 // ---- standalone fused QK -----------------------------------------------------------
@@ -1205,3 +1282,10 @@ extern "C" int32_t tp_decode_attention_noalloc(const void* q, int64_t batch, int
   return tp_decode_attention(q, batch, hq, hkv, layout, pages, n_pages, tail_k, tail_v, tail_len, tail_stride,
                              actual_seq_len, scale, pages_per_split, ws, ws_bytes, out, stream);
 }
+
+#ifdef TP_TIMELINE
+extern "C" void* tp_timeline_address() {
+  void* p = nullptr;
+  return hipGetSymbolAddress(&p, HIP_SYMBOL(tp::g_timeline)) == hipSuccess ? p : nullptr;
+}
+#endif
