@@ -158,16 +158,97 @@ def run_gpu(args, layout):
             "ws_bytes": need, "rerun_equal": bool(torch.equal(ref_out, caches[0]["out"]))}
 
 
+def host_cores() -> int:
+    """Host threads the CPU baselines use: every core this process may run on,
+    at most ``TP_BENCH_CPU_THREADS`` (default 16, one GPU's share of a
+    GPU box's host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        n = os.cpu_count() or 1
+    return max(1, min(n, int(os.environ.get("TP_BENCH_CPU_THREADS", "16"))))
+
+
+class _OneBlasThread:
+    """BLAS and OpenMP pools at one thread inside (the baselines' own thread
+    pools carry the parallelism)."""
+
+    def __enter__(self):
+        try:
+            from threadpoolctl import threadpool_limits
+            self._ctx = threadpool_limits(1)
+        except ImportError:  # pragma: no cover
+            self._ctx = None
+        return self
+
+    def __exit__(self, *exc):
+        if self._ctx is not None:
+            self._ctx.__exit__(*exc)
+
+
+def _chunks(n: int, parts: int):
+    """[0, n) cut into at most ``parts`` contiguous ranges."""
+    parts = max(1, min(parts, n))
+    edges = [n * i // parts for i in range(parts + 1)]
+    return [(edges[i], edges[i + 1]) for i in range(parts) if edges[i] < edges[i + 1]]
+
+
+def _sample(fn, budget_s: float, min_runs: int = 2):
+    """Median wall time of repeated ``fn()`` calls for about ``budget_s``
+    seconds (at least ``min_runs`` calls) and the last result."""
+    times, out = [], None
+    start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        out = fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - start > budget_s and len(times) >= min_runs:
+            break
+    return float(np.median(times)), len(times), out
+
+
+def cpu_attention_all_cores(oracle, pool, cores, q, blk, qv, scale, seq):
+    """The oracle's _cpu_online_attention_dense_tail (metal.py:293-332) spread
+    over ``pool``: K decode and V dequantisation per (kv head, page range),
+    then the float32 masked softmax attention per kv head.  Every element
+    takes the oracle's own arithmetic; only the work is divided."""
+    codes, scales = qv
+    B, H, S, L, D = codes.shape
+    k = np.empty((B, H, S * L, D), np.float16)
+    v = np.empty((B, H, S * L, D), np.float16)
+    rs = blk["radii_scales"]
+
+    def dec(h, p0, p1):
+        hs, ps, ts = slice(h, h + 1), slice(p0, p1), slice(p0 * L, p1 * L)
+        k[:, hs, ts] = oracle.decode_block(blk["radii"][:, hs, ps], None if rs is None else rs[:, hs, ps],
+                                           blk["angle_codes_l1"][:, hs, ps], blk["angle_codes_deep"][:, hs, ps],
+                                           blk["metadata"])
+        v[:, hs, ts] = oracle.dequantize_block(codes[:, hs, ps], scales[:, hs, ps]).reshape(B, 1, (p1 - p0) * L, D)
+
+    parts = max(1, -(-4 * cores // H))
+    list(pool.map(lambda t: dec(*t), [(h, p0, p1) for h in range(H) for p0, p1 in _chunks(S, parts)]))
+    g = q.shape[1] // H
+    out = np.empty(q.shape, np.float32)
+
+    def att(h):
+        out[:, h * g:(h + 1) * g] = oracle.softmax_attention(q[:, h * g:(h + 1) * g], k[:, h:h + 1], v[:, h:h + 1],
+                                                             scale, seq, dtype=np.float32)
+
+    list(pool.map(att, range(H)))
+    return out
+
+
 def cpu_baseline(args, layout, caches, budget_s):
-    """Oracle restatement of the reference CPU fallback on one cache (float32, 1 thread)."""
+    """The oracle's restatement of the reference CPU fallback
+    (_cpu_online_attention_dense_tail, metal.py:293-332) on one cache, float32:
+    on every host core the process may use (``host_cores``), and once more on
+    one thread for comparison with single-core figures."""
+    from concurrent.futures import ThreadPoolExecutor
+
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import oracle
     from turbopolar_amd.kernels import fp16_scale
 
-    try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_limits = None
     c = caches[0]
     ps = c["pages"]
     t = ps.tensors
@@ -182,24 +263,16 @@ def cpu_baseline(args, layout, caches, budget_s):
     q = c["q"].cpu().numpy()
     empty = np.zeros((1, args.hkv, 0, 128), np.float16)
     scale = fp16_scale(1.0 / np.sqrt(128.0))
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    times = []
-    try:
-        if ctx:
-            ctx.__enter__()
-        start = time.perf_counter()
-        while True:
-            t0 = time.perf_counter()
-            out = oracle.cpu_online_attention_dense_tail(q, blk, qv, empty, empty, scale, c["seq"], dtype=np.float32)
-            times.append(time.perf_counter() - t0)
-            if time.perf_counter() - start > budget_s and len(times) >= 2:
-                break
-    finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
+    cores = host_cores()
+    with _OneBlasThread(), ThreadPoolExecutor(cores) as pool:
+        t_all, n_all, out = _sample(lambda: cpu_attention_all_cores(oracle, pool, cores, q, blk, qv, scale, c["seq"]),
+                                    budget_s)
+        t_one, n_one, out1 = _sample(lambda: oracle.cpu_online_attention_dense_tail(
+            q, blk, qv, empty, empty, scale, c["seq"], dtype=np.float32), budget_s / 4)
     gpu = c["out"].float().cpu().numpy()
-    err = float(np.max(np.abs(gpu - out)))
-    return float(np.median(times)) * 1e6, len(times), err
+    return {"us": t_all * 1e6, "runs": n_all, "cores": cores, "err": float(np.max(np.abs(gpu - out))),
+            "one_thread_us": t_one * 1e6, "one_thread_runs": n_one,
+            "same_as_one_thread": bool(np.array_equal(out, out1))}
 
 
 def run_layers(args, layout) -> dict:
@@ -378,6 +451,56 @@ def run_decompress(args, layout) -> dict:
             "v_out": v_out}
 
 
+PREFILL_TAIL = 37  # tokens left in the dense tail before and after every prefill step
+
+
+def run_prefill(args, layout) -> dict:
+    """Prefill with a tail: TurboPolarFastCache.update_and_fetch
+    (turbopolar_fast_attention.py:56-86) of a 64-token chunk over a cache of
+    ``context`` + 37 tokens.  Each step appends the chunk (one page encoded,
+    the 37-token tail kept), decodes every stored page and the zero-padded tail
+    page in place into the dense fp16 K and V it returns.  The cache grows by
+    64 tokens a step; the timed region is ``steps`` whole calls, host work
+    included (wall clock, synchronised at both ends)."""
+    import torch
+
+    from turbopolar_amd import TurboPolarConfig
+    from turbopolar_amd.fast_attention import TurboPolarFastCache
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    int8, l1b, deepb, split = layout
+    cfg = TurboPolarConfig(num_q_heads=args.hq, num_kv_heads=args.hkv, use_int8_radii=int8,
+                           k_angle_bits_level1=l1b, k_angle_bits_deep=deepb, split_dim=split)
+    g = torch.Generator(device=dev).manual_seed(11)
+    cache = TurboPolarFastCache(cfg)
+    t0 = args.context + PREFILL_TAIL
+    k0 = synthetic_k(args.kind, args.hkv, t0, g, dev).half()
+    v0 = torch.randn((1, args.hkv, t0, 128), generator=g, device=dev).half()
+    k, v = cache.update_and_fetch(k0, v0)
+    if k.shape[2] != t0 or cache.runtime._tail_len != PREFILL_TAIL:
+        raise RuntimeError("prefill returned the wrong length")
+    del k0, v0, k, v
+    n_chunks = args.warmup + args.steps
+    ck = synthetic_k(args.kind, args.hkv, 64 * n_chunks, g, dev).half()
+    cv = torch.randn((1, args.hkv, 64 * n_chunks, 128), generator=g, device=dev).half()
+    for i in range(args.warmup):
+        cache.update_and_fetch(ck[:, :, 64 * i:64 * (i + 1)], cv[:, :, 64 * i:64 * (i + 1)])
+    torch.cuda.synchronize()
+    first = cache.offset + 64
+    start = time.perf_counter()
+    for i in range(args.warmup, n_chunks):
+        k, v = cache.update_and_fetch(ck[:, :, 64 * i:64 * (i + 1)], cv[:, :, 64 * i:64 * (i + 1)])
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - start) * 1e3 / args.steps
+    last = cache.offset
+    mid_pages = ((first + last) // 2) // 64
+    read = algorithmic_bytes(0, args.hkv, mid_pages, layout) + args.hkv * PREFILL_TAIL * 512 + 2 * args.hkv * 64 * 256
+    write = 2 * args.hkv * (mid_pages + 1) * 64 * 256
+    tail_ok = cache.runtime._tail_len == PREFILL_TAIL and k.shape[2] == last and bool(torch.isfinite(k).all())
+    return {"ms": ms, "first": first, "last": last, "read": read, "write": write, "tail_ok": tail_ok}
+
+
 def _f16_ulp_gap(a, b) -> int:
     """Largest distance in fp16 ulps between finite elements of a and b."""
     def ordered(x):
@@ -389,16 +512,16 @@ def _f16_ulp_gap(a, b) -> int:
 
 def cpu_decompress_baseline(args, r, budget_s):
     """Oracle restatement of decompress-on-read (decode_block +
-    dequantize_block, decoder.py:7-67, v_quant/encoder.py:32-38) page by page,
-    1 thread, until ``budget_s`` seconds; each sampled page is compared with
-    the GPU's dense K (ulps) and V (bitwise)."""
+    dequantize_block, decoder.py:7-67, v_quant/encoder.py:32-38) of the whole
+    cache, page ranges spread over every host core (``host_cores``), repeated
+    for about ``budget_s`` seconds; the result is compared with the GPU's dense
+    K (ulps) and V (bitwise).  Also one page range on one thread, scaled to the
+    cache, for comparison with single-core figures."""
+    from concurrent.futures import ThreadPoolExecutor
+
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import oracle
 
-    try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_limits = None
     c = r["cache0"]
     t = c["pages"].tensors
     radii, l1, deep = (t[n].cpu().numpy() for n in ("radii", "angle_l1", "angle_deep"))
@@ -406,28 +529,25 @@ def cpu_decompress_baseline(args, r, budget_s):
     codes, scales = t["v_codes"].cpu().numpy(), t["v_scales"].cpu().numpy()
     meta = c["rt"].k_storage.metadata
     kg, vg = r["k_out"].cpu().numpy(), r["v_out"].cpu().numpy()
-    times, v_exact, k_ulps = [], True, 0
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    try:
-        if ctx:
-            ctx.__enter__()
-        start = time.perf_counter()
-        for p in range(r["n_pages"]):
-            sl = slice(p, p + 1)
-            t0 = time.perf_counter()
-            k = oracle.decode_block(radii[:, :, sl], rs[:, :, sl] if rs is not None else None, l1[:, :, sl],
-                                    deep[:, :, sl], meta)
-            v = oracle.dequantize_block(codes[:, :, sl], scales[:, :, sl])
-            times.append(time.perf_counter() - t0)
-            tok = slice(64 * p, 64 * (p + 1))
-            v_exact &= bool(np.array_equal(v.reshape(vg[:, :, tok].shape).view(np.uint16), vg[:, :, tok].view(np.uint16)))
-            k_ulps = max(k_ulps, _f16_ulp_gap(k, kg[:, :, tok]))
-            if time.perf_counter() - start > budget_s and len(times) >= 2:
-                break
-    finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
-    return float(np.median(times)) * r["n_pages"] * 1e6, len(times), v_exact, k_ulps
+    S = r["n_pages"]
+    k = np.empty(kg.shape, np.float16)
+    v = np.empty(vg.shape, np.float16)
+
+    def dec(p0, p1):
+        ps, ts = slice(p0, p1), slice(64 * p0, 64 * p1)
+        k[:, :, ts] = oracle.decode_block(radii[:, :, ps], rs[:, :, ps] if rs is not None else None, l1[:, :, ps],
+                                          deep[:, :, ps], meta)
+        v[:, :, ts] = oracle.dequantize_block(codes[:, :, ps], scales[:, :, ps]).reshape(k[:, :, ts].shape)
+
+    cores = host_cores()
+    ranges = _chunks(S, 4 * cores)
+    with _OneBlasThread(), ThreadPoolExecutor(cores) as pool:
+        t_all, n_all, _ = _sample(lambda: list(pool.map(lambda pr: dec(*pr), ranges)), budget_s)
+        p1 = max(1, S // 16)
+        t_one, n_one, _ = _sample(lambda: dec(0, p1), budget_s / 4)
+    v_exact = bool(np.array_equal(v.view(np.uint16), vg.view(np.uint16)))
+    return {"us": t_all * 1e6, "runs": n_all, "cores": cores, "v_exact": v_exact, "k_ulps": _f16_ulp_gap(k, kg),
+            "one_thread_us": t_one * S / p1 * 1e6, "one_thread_sample": f"{n_one} runs over {p1} of {S} pages"}
 
 
 def k_page_bytes(layout) -> int:
@@ -484,15 +604,14 @@ def run_fused_qk(args, layout) -> dict:
 
 def cpu_qk_baseline(args, r, budget_s):
     """Oracle restatement of _cpu_fused_qk (metal.py:254-260) over the whole
-    cache in float32, 1 thread, repeated until ``budget_s`` seconds; compared
-    with the GPU scores by the reference's own QK test bar (max-abs, cosine)."""
+    cache in float32, per (kv head, page range) on every host core, repeated
+    for about ``budget_s`` seconds, and once on one thread; compared with the
+    GPU scores by the reference's own QK test bar (max-abs, cosine)."""
+    from concurrent.futures import ThreadPoolExecutor
+
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import oracle
 
-    try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_limits = None
     c = r["cache0"]
     t = c["pages"].tensors
     blk = {"radii": t["radii"].cpu().numpy(),
@@ -504,25 +623,28 @@ def cpu_qk_baseline(args, r, budget_s):
         if blk[n] is not None:
             blk[n] = blk[n][:, :, :S]
     q = c["q"].cpu().numpy()
-    times = []
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    try:
-        if ctx:
-            ctx.__enter__()
-        start = time.perf_counter()
-        while True:
-            t0 = time.perf_counter()
-            ref = oracle.cpu_fused_qk(q, blk, r["scale"], dtype=np.float32)
-            times.append(time.perf_counter() - t0)
-            if time.perf_counter() - start > budget_s and len(times) >= 2:
-                break
-    finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
-    g = r["scores"].float().cpu().numpy().reshape(ref.shape)
-    err = float(np.max(np.abs(g - ref)))
-    cos = float(np.sum(g * ref) / (np.linalg.norm(g) * np.linalg.norm(ref)))
-    return float(np.median(times)) * 1e6, len(times), err, cos
+    H = blk["radii"].shape[1]
+    g = q.shape[1] // H
+    ref = np.empty((q.shape[0], q.shape[1], S * 64), np.float32)
+
+    def part(h, p0, p1):
+        sub = {n: (None if blk[n] is None else blk[n][:, h:h + 1, p0:p1])
+               for n in ("radii", "radii_scales", "angle_codes_l1", "angle_codes_deep")}
+        sub["metadata"] = blk["metadata"]
+        ref[:, h * g:(h + 1) * g, 64 * p0:64 * p1] = oracle.cpu_fused_qk(q[:, h * g:(h + 1) * g], sub, r["scale"],
+                                                                         dtype=np.float32)
+
+    cores = host_cores()
+    tasks = [(h, p0, p1) for h in range(H) for p0, p1 in _chunks(S, max(1, -(-4 * cores // H)))]
+    with _OneBlasThread(), ThreadPoolExecutor(cores) as pool:
+        t_all, n_all, _ = _sample(lambda: list(pool.map(lambda a: part(*a), tasks)), budget_s)
+        t_one, n_one, one = _sample(lambda: oracle.cpu_fused_qk(q, blk, r["scale"], dtype=np.float32), budget_s / 4)
+    g_ = r["scores"].float().cpu().numpy().reshape(ref.shape)
+    err = float(np.max(np.abs(g_ - ref)))
+    cos = float(np.sum(g_ * ref) / (np.linalg.norm(g_) * np.linalg.norm(ref)))
+    return {"us": t_all * 1e6, "runs": n_all, "cores": cores, "err": err, "cos": cos,
+            "one_thread_us": t_one * 1e6, "one_thread_runs": n_one,
+            "same_as_one_thread": bool(np.array_equal(one.reshape(ref.shape), ref))}
 
 
 def run_encode(args, layout) -> dict:
@@ -583,53 +705,50 @@ def run_encode(args, layout) -> dict:
 
 def cpu_encode_baseline(args, layout, set0, budget_s):
     """Oracle restatement of the reference's page flush (encode_block +
-    quantize_block, encoder.py:24-98, v_quant/encoder.py:16-30) page by page
-    over the first input set, 1 thread, until ``budget_s`` seconds; each
-    sampled page is also compared with what the GPU wrote for it."""
+    quantize_block, encoder.py:24-98, v_quant/encoder.py:16-30) of every page
+    of the first input set, page ranges spread over every host core
+    (``host_cores``), repeated for about ``budget_s`` seconds; every page is
+    compared bitwise with what the GPU wrote for it.  Also a sample of pages
+    on one thread, scaled to the cache."""
+    from concurrent.futures import ThreadPoolExecutor
+
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import oracle
 
-    try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_limits = None
     int8, l1b, deepb, split = layout
     k, v, bufs, codes, scales = set0
     kn = k.cpu().numpy()
     vn = v.cpu().numpy()
     gpu = {name: t.cpu().numpy() for name, t in bufs.items() if t is not None}
     codes_n, scales_n = codes.cpu().numpy(), scales.cpu().numpy()
+    S = args.context // 64
+    res = [None] * S
 
     def same(a, b):  # bitwise
         return bool(np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8)))
 
-    times, exact = [], True
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    try:
-        if ctx:
-            ctx.__enter__()
-        start = time.perf_counter()
-        p = 0
-        while p < args.context // 64:
+    def enc(p0, p1):
+        for p in range(p0, p1):
             ks, vs = kn[:, :, 64 * p:64 * (p + 1)], vn[:, :, 64 * p:64 * (p + 1)]
-            t0 = time.perf_counter()
             blk = oracle.encode_block(ks, l1_bits=l1b, deep_bits=deepb, split_dim=split, use_int8_radii=int8)
-            vc, vsc = oracle.quantize_block(vs[:, :, None])
-            times.append(time.perf_counter() - t0)
-            exact &= same(blk["radii"], gpu["radii"][:, :, p])
-            exact &= same(blk["angle_codes_l1"], gpu["angle_codes_l1"][:, :, p])
-            exact &= same(blk["angle_codes_deep"], gpu["angle_codes_deep"][:, :, p])
-            if blk["radii_scales"] is not None:
-                exact &= same(blk["radii_scales"].reshape(-1), gpu["radii_scales"][:, :, p].reshape(-1))
-            exact &= same(vc[:, :, 0], codes_n[:, :, p]) and same(vsc[:, :, 0], scales_n[:, :, p])
-            p += 1
-            if time.perf_counter() - start > budget_s and len(times) >= 2:
-                break
-    finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
-    per_page = float(np.median(times))
-    return per_page * (args.context // 64) * 1e6, len(times), exact
+            res[p] = (blk, oracle.quantize_block(vs[:, :, None]))
+
+    cores = host_cores()
+    ranges = _chunks(S, 4 * cores)
+    with _OneBlasThread(), ThreadPoolExecutor(cores) as pool:
+        t_all, n_all, _ = _sample(lambda: list(pool.map(lambda pr: enc(*pr), ranges)), budget_s, min_runs=1)
+        p1 = max(1, S // 32)
+        t_one, n_one, _ = _sample(lambda: enc(0, p1), budget_s / 4, min_runs=1)
+    exact = True
+    for p, (blk, (vc, vsc)) in enumerate(res):
+        exact &= same(blk["radii"], gpu["radii"][:, :, p])
+        exact &= same(blk["angle_codes_l1"], gpu["angle_codes_l1"][:, :, p])
+        exact &= same(blk["angle_codes_deep"], gpu["angle_codes_deep"][:, :, p])
+        if blk["radii_scales"] is not None:
+            exact &= same(blk["radii_scales"].reshape(-1), gpu["radii_scales"][:, :, p].reshape(-1))
+        exact &= same(vc[:, :, 0], codes_n[:, :, p]) and same(vsc[:, :, 0], scales_n[:, :, p])
+    return {"us": t_all * 1e6, "runs": n_all, "cores": cores, "exact": exact, "pages": S,
+            "one_thread_us": t_one * S / p1 * 1e6, "one_thread_sample": f"{n_one} runs over {p1} of {S} pages"}
 
 
 def bench_page_bytes(layout) -> int:
@@ -784,6 +903,80 @@ def run_timeline(args, layout) -> dict:
     return {"phases": phases, "pps": pps, "groups": groups}
 
 
+# Bytes per page and kv head of each page field the decode kernel reads, in
+# its order (default: radii, level-1 codes, deep codes, V codes, V scales;
+# fast: int8 log radii, radius scale, deep codes, V codes, V scales).
+PAGE_FIELDS = {"default": (8192, 1024, 1024, 8192, 512), "fast": (4096, 2, 4096, 8192, 512)}
+# Launch shapes of the streaming-read sweep (grid, threads, unroll); the
+# decode kernel's own grid is added in front.
+STREAM_SHAPES = ((2048, 512, 8), (4096, 512, 8), (8192, 512, 8), (8192, 256, 8), (4096, 1024, 4))
+
+
+def run_stream(args, layout) -> dict:
+    """The streaming-read ceiling: tp_measure_stream_read (measurement
+    library) reads buffers of exactly the page fields one decode step reads
+    (same sizes, same 16-byte non-temporal loads), with nothing computed, at
+    the decode kernel's grid and at the launch shapes of STREAM_SHAPES.
+    Buffers rotate over > 320 MB as in the headline line, so reads come
+    from HBM; each shape is timed over ``steps`` back-to-back launches with
+    HIP events on the launch stream."""
+    import torch
+
+    from turbopolar_amd import _lib, build
+
+    if _lib._lib is not None:
+        raise RuntimeError("the stream workload must load its library first")
+    _lib.LIB_PATH = build.TIMELINE_LIB_PATH
+    L = _lib.lib()
+    fn = L.tp_measure_stream_read
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32,
+                   ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    n_pages = args.context // 64
+    fields = [args.hkv * n_pages * f for f in PAGE_FIELDS[args.layout]]
+    fields = [(f + 15) // 16 * 16 for f in fields]
+    total = sum(fields)
+    rotate = args.rotate or max(4, int(np.ceil(320e6 / total)))
+    g = torch.Generator(device=dev).manual_seed(7)
+    sets = []
+    for _ in range(rotate):
+        bufs = [torch.randint(0, 256, (f,), dtype=torch.uint8, device=dev, generator=g) for f in fields]
+        ptrs = (ctypes.c_void_p * len(bufs))(*[b.data_ptr() for b in bufs])
+        sizes = (ctypes.c_int64 * len(bufs))(*fields)
+        sets.append((bufs, ptrs, sizes))
+    pps = int(L.tp_default_pages_per_split(1, args.hq, args.hkv, n_pages))
+    units = args.hkv * ((args.hq // args.hkv + 15) // 16)
+    decode_grid = units * ((n_pages + pps - 1) // pps)
+    shapes = [(decode_grid, 512, 8)] + [s for s in STREAM_SHAPES if s != (decode_grid, 512, 8)]
+    sink = torch.zeros(max(s[0] for s in shapes), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    results = []
+    for grid, threads, unroll in shapes:
+        def launch(i):
+            _, ptrs, sizes = sets[i % rotate]
+            rc = fn(ptrs, sizes, len(fields), grid, threads, unroll, ctypes.c_void_p(sink.data_ptr()),
+                    ctypes.c_void_p(stream))
+            if rc != 0:
+                raise RuntimeError("tp_measure_stream_read rejected its arguments")
+
+        for i in range(args.warmup):
+            launch(i)
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for i in range(args.steps):
+            launch(i)
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) / args.steps * 1e3
+        results.append({"grid": grid, "threads": threads, "unroll": unroll, "us": round(us, 3),
+                        "GBps": round(total / (us * 1e-6) / 1e9, 1)})
+    return {"bytes": total, "fields": fields, "rotate": rotate, "sweep": results, "decode_grid": decode_grid}
+
+
 def profiled_traffic(name: str, args):
     """HBM bytes per launch that the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     summary profiles/<name>_8b_32k_traffic.json records, when this run is that
@@ -869,12 +1062,15 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", choices=["decode", "encode", "append", "layers", "model", "decompress", "snapshot", "qk",
-                                           "timeline"],
+                                           "timeline", "stream", "prefill"],
                     default="decode",
                     help="decode (the BASELINE metric, default); encode / append: configs[3] workloads; "
                          "layers: configs[1] (--layers decode launches per step); "
                          "model: a configs[1]-shape Llama decoding through the transformers hook; "
-                         "decompress: tp_decode_pages of a whole cache (prefill decompress-on-read)")
+                         "decompress: tp_decode_pages of a whole cache (prefill decompress-on-read); "
+                         "prefill: TurboPolarFastCache.update_and_fetch of a chunk over a cache with a tail; "
+                         "timeline: the decode kernel's phase stamps; "
+                         "stream: the streaming-read ceiling of the decode step's page bytes")
     ap.add_argument("--kind", choices=["outlier", "loguniform", "studentt", "normal"], default=None,
                     help="K distribution (default: outlier for decode, loguniform for layers)")
     ap.add_argument("--layers", type=int, default=16)
@@ -897,11 +1093,13 @@ def main():
         r = run_decompress(args, layout)
         cpu = None
         if not args.no_cpu:
-            cpu_us, nsamp, v_exact, k_ulps = cpu_decompress_baseline(args, r, args.cpu_budget)
-            cpu = {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
-                   "sample": f"{nsamp} of {r['n_pages']} pages of {args.hkv} kv heads (oracle NumPy restatement of "
-                             f"decode_block + dequantize_block, 1 thread; median per page x {r['n_pages']}; sampled "
-                             f"pages: V bit-exact {v_exact}, K within {k_ulps} fp16 ulp of the oracle)"}
+            cb = cpu_decompress_baseline(args, r, args.cpu_budget)
+            cpu = {"value": round(cb["us"], 1), "unit": "us/step", "cores": cb["cores"], "kind": "port",
+                   "sample": f"{cb['runs']} decompressions of all {r['n_pages']} pages of {args.hkv} kv heads (oracle "
+                             f"NumPy restatement of decode_block + dequantize_block, page ranges on {cb['cores']} "
+                             f"threads; V bit-exact {cb['v_exact']}, K within {cb['k_ulps']} fp16 ulp of the oracle)",
+                   "one_thread": {"value": round(cb["one_thread_us"], 1), "unit": "us/step", "cores": 1,
+                                  "sample": cb["one_thread_sample"] + ", scaled to the cache"}}
         nbytes = r["read"] + r["write"]
         gbps = nbytes / (r["ms"] * 1e-3) / 1e9
         print(json.dumps({
@@ -921,10 +1119,14 @@ def main():
         r = run_fused_qk(args, layout)
         cpu = None
         if not args.no_cpu:
-            cpu_us, nsamp, err, cos = cpu_qk_baseline(args, r, args.cpu_budget)
-            cpu = {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
-                   "sample": f"{nsamp} full steps over the {args.context}-token cache (oracle NumPy float32 "
-                             f"restatement of _cpu_fused_qk, 1 thread; GPU scores max-abs {err:.2e}, cosine {cos:.6f})"}
+            cb = cpu_qk_baseline(args, r, args.cpu_budget)
+            cpu = {"value": round(cb["us"], 1), "unit": "us/step", "cores": cb["cores"], "kind": "port",
+                   "sample": f"{cb['runs']} full steps over the {args.context}-token cache (oracle NumPy float32 "
+                             f"restatement of _cpu_fused_qk per kv head and page range on {cb['cores']} threads; GPU "
+                             f"scores max-abs {cb['err']:.2e}, cosine {cb['cos']:.6f})",
+                   "one_thread": {"value": round(cb["one_thread_us"], 1), "unit": "us/step", "cores": 1,
+                                  "sample": f"{cb['one_thread_runs']} steps of the unsplit oracle call",
+                                  "outputs_identical": cb["same_as_one_thread"]}}
         nbytes = r["read"] + r["write"]
         gbps = nbytes / (r["ms"] * 1e-3) / 1e9
         print(json.dumps({
@@ -938,6 +1140,43 @@ def main():
                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(f"qk_{args.layout}", args)},
             "algorithmic_bytes_per_step": {"read": r["read"], "write": r["write"]},
             "cpu_baseline": cpu,
+        }))
+        return
+    if args.workload == "prefill":
+        r = run_prefill(args, layout)
+        nbytes = r["read"] + r["write"]
+        gbps = nbytes / (r["ms"] * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": "prefill chunk ms/step (append 64 tokens + decompress-on-read of the whole history with a "
+                      "37-token tail), Llama-3-8B kv shape",
+            "value": round(r["ms"], 4), "unit": "ms/step", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(r["ms"], 4), "higher_is_better": False,
+            "dtype": "f16", "data": "synthetic",
+            "config": {"workload": f"TurboPolarFastCache.update_and_fetch of 64-token chunks, {args.hkv} kv heads, "
+                                   f"history {r['first']} -> {r['last']} tokens (37 in the dense tail)",
+                       "layout": args.layout, "k_distribution": args.kind},
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "note": "wall clock of whole calls (host work included) over the mid-run history's bytes"},
+            "algorithmic_bytes_per_step": {"read": r["read"], "write": r["write"]},
+            "checks": {"tail_kept_and_output_finite": r["tail_ok"]},
+        }))
+        return
+    if args.workload == "stream":
+        r = run_stream(args, layout)
+        best = min(r["sweep"], key=lambda e: e["us"])
+        gbps = r["bytes"] / (best["us"] * 1e-6) / 1e9
+        print(json.dumps({
+            "metric": "streaming-read ceiling: µs to read one decode step's page bytes (no compute)",
+            "value": best["us"], "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "higher_is_better": False, "dtype": "u8", "data": "synthetic",
+            "config": {"workload": f"tp_measure_stream_read over the page fields of {args.hkv} kv heads x "
+                                   f"{args.context // 64} pages ({args.context} tokens), {r['rotate']} rotating sets",
+                       "layout": args.layout, "field_bytes": r["fields"], "best_shape": best},
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+            "decode_grid": next(e for e in r["sweep"] if e["grid"] == r["decode_grid"] and e["threads"] == 512),
+            "sweep": r["sweep"],
         }))
         return
     if args.workload == "timeline":
@@ -989,11 +1228,13 @@ def main():
         r = run_encode(args, layout)
         cpu = None
         if not args.no_cpu:
-            cpu_us, nsamp, exact = cpu_encode_baseline(args, layout, r["set0"], args.cpu_budget)
-            cpu = {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
-                   "sample": f"{nsamp} of {r['n_pages']} page flushes of {args.hkv} kv heads (oracle NumPy "
-                             f"restatement of encode_block + quantize_block, 1 thread; median per page x "
-                             f"{r['n_pages']}; sampled pages bit-exact vs GPU: {exact})"}
+            cb = cpu_encode_baseline(args, layout, r["set0"], args.cpu_budget)
+            cpu = {"value": round(cb["us"], 1), "unit": "us/step", "cores": cb["cores"], "kind": "port",
+                   "sample": f"{cb['runs']} encodes of all {cb['pages']} pages of {args.hkv} kv heads (oracle NumPy "
+                             f"restatement of encode_block + quantize_block, page ranges on {cb['cores']} threads; "
+                             f"every page bit-exact vs GPU: {cb['exact']})",
+                   "one_thread": {"value": round(cb["one_thread_us"], 1), "unit": "us/step", "cores": 1,
+                                  "sample": cb["one_thread_sample"] + ", scaled to the cache"}}
         nbytes = r["read"] + r["write"]
         gbps = nbytes / (r["ms"] * 1e-3) / 1e9
         print(json.dumps({
@@ -1017,7 +1258,7 @@ def main():
             cpu = {"value": round(cpu_us, 2), "unit": "us/append", "cores": 1, "kind": "port",
                    "sample": f"{n_cpu} single-token appends with {cpu_pages} page flushes (host restatement of "
                              f"append: finiteness check, tail concatenation, oracle encode_block + "
-                             f"quantize_block per full page; 1 thread)"}
+                             f"quantize_block per full page; 1 thread: each append depends on the one before)"}
         print(json.dumps({
             "metric": "single-token append latency, Llama-3-8B kv shape",
             "value": round(r["us_per_append"], 2), "unit": "us/append", "n_gpus": 1,
@@ -1051,11 +1292,15 @@ def main():
     gbps = step_bytes / (ms * 1e-3) / 1e9
     cpu = None
     if not args.no_cpu:
-        cpu_us, nsamp, err = cpu_baseline(args, layout, res["caches"], args.cpu_budget)
-        cpu = {"value": round(cpu_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
-               "sample": f"{nsamp} full decode steps of the 32-head/8-kv-head {args.context}-token cache "
-                         f"(oracle NumPy float32 restatement of _cpu_online_attention_dense_tail, 1 thread; "
-                         f"max-abs vs GPU {err:.2e})"}
+        cb = cpu_baseline(args, layout, res["caches"], args.cpu_budget)
+        cpu = {"value": round(cb["us"], 1), "unit": "us/step", "cores": cb["cores"], "kind": "port",
+               "sample": f"{cb['runs']} full decode steps of the {args.hq}-head/{args.hkv}-kv-head {args.context}-token "
+                         f"cache (oracle NumPy float32 restatement of _cpu_online_attention_dense_tail, K decode and "
+                         f"V dequantisation per kv head and page range, attention per kv head, on {cb['cores']} "
+                         f"threads; max-abs vs GPU {cb['err']:.2e})",
+               "one_thread": {"value": round(cb["one_thread_us"], 1), "unit": "us/step", "cores": 1,
+                              "sample": f"{cb['one_thread_runs']} steps of the unsplit oracle call",
+                              "outputs_identical": cb["same_as_one_thread"]}}
     traffic = None
     tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                          f"decode_attention_{args.layout}_8b_32k_traffic.json")

@@ -3,9 +3,10 @@
 Run as ``python -m turbopolar_amd.build`` or through ``__graft_entry__.build()``.
 Every call recompiles.  Objects go to ``turbopolar_amd/_build/`` and the shared
 library to ``turbopolar_amd/libturbopolar_hip.so``.  A second library,
-``libturbopolar_hip_timeline.so``, is the same code with the decode kernel's
-phase stamps compiled in (``-DTP_TIMELINE``); only ``bench.py --workload
-timeline`` loads it.
+``libturbopolar_hip_timeline.so`` (the measurement library), is the same code
+with the decode kernel's phase stamps compiled in (``-DTP_TIMELINE``) plus the
+streaming-read probe of ``tp_measure.hip``; only ``bench.py --workload
+timeline`` and ``--workload stream`` load it.
 """
 
 from __future__ import annotations
@@ -27,6 +28,7 @@ TIMELINE_LIB_PATH = PKG_DIR / "libturbopolar_hip_timeline.so"
 ARCH = os.environ.get("TP_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["tp_api.hip", "tp_encode.hip", "tp_attention.hip", "tp_decode.hip", "tp_append.hip"]
+MEASURE_SOURCES = ["tp_measure.hip"]  # measurement library only
 
 # -ffp-contract=off and correctly rounded fp32 divide/sqrt are required for the
 # encoder's bit-exact fp16 rules; packed fp32 VALU ops are disabled.
@@ -62,17 +64,20 @@ def build(verbose: bool = True) -> Path:
     BUILD_DIR.mkdir(exist_ok=True)
     objs = []
     timeline_obj = BUILD_DIR / "tp_attention_timeline.o"
-    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES) + 1, 8)) as ex:
+    measure_objs = [BUILD_DIR / (Path(n).stem + ".o") for n in MEASURE_SOURCES]
+    with cf.ThreadPoolExecutor(max_workers=8) as ex:
         futs = []
         for name in SOURCES:
             obj = BUILD_DIR / (Path(name).stem + ".o")
             objs.append(obj)
             futs.append(ex.submit(_compile, CSRC / name, obj))
         futs.append(ex.submit(_compile, CSRC / "tp_attention.hip", timeline_obj, ("TP_TIMELINE",)))
+        for name, obj in zip(MEASURE_SOURCES, measure_objs):
+            futs.append(ex.submit(_compile, CSRC / name, obj))
         for f in futs:
             f.result()
     _link(objs, LIB_PATH)
-    _link([timeline_obj if o.stem == "tp_attention" else o for o in objs], TIMELINE_LIB_PATH)
+    _link([timeline_obj if o.stem == "tp_attention" else o for o in objs] + measure_objs, TIMELINE_LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
     return LIB_PATH
