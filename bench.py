@@ -30,6 +30,8 @@ import time
 import numpy as np
 
 HBM_PEAK_GBPS = 8000.0
+# Decode-kernel variants of the measurement library (tp_measure_set_decode_variant).
+VARIANTS = {"mfma": 0, "release": 1, "valu": 2, "valu+release": 3}
 METRIC = "decode-attn µs/step + achieved HBM GB/s (% peak), Llama-3-8B shape, 32k ctx"
 LAYOUTS = {"default": (False, 4, 4, 64), "fast": (True, 4, 8, 0)}
 
@@ -1075,6 +1077,10 @@ def main():
                     help="K distribution (default: outlier for decode, loguniform for layers)")
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--graph", action="store_true", help="layers: replay the step as one HIP graph")
+    ap.add_argument("--variant", choices=sorted(VARIANTS), default=None,
+                    help="decode: run a decode-kernel variant of the measurement library (release: agent-scope "
+                         "release fence before the split ticket; valu: QK and PV on the VALU; mfma: the product "
+                         "kernel as built there)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -1286,6 +1292,16 @@ def main():
     if not args.rotate:
         args.rotate = max(4, int(np.ceil(320e6 / step_bytes)))
 
+    if args.variant is not None:
+        from turbopolar_amd import _lib, build
+
+        if _lib._lib is not None:
+            raise RuntimeError("--variant must load the measurement library first")
+        _lib.LIB_PATH = build.TIMELINE_LIB_PATH
+        fn = _lib.lib().tp_measure_set_decode_variant
+        fn.restype, fn.argtypes = ctypes.c_int32, [ctypes.c_int32]
+        if fn(VARIANTS[args.variant]) != 0:
+            raise RuntimeError(f"variant {args.variant} rejected")
     res = run_gpu(args, layout)
     ms = res["ms"]
     us = ms * 1e3
@@ -1340,6 +1356,8 @@ def main():
         "cpu_baseline": cpu,
         "checks": {"finite": res["finite"], "deterministic_rerun": res["rerun_equal"]},
     }
+    if args.variant is not None:
+        line["kernel_variant"] = f"{args.variant} (measurement library: phase stamps compiled in)"
     print(json.dumps(line))
 
 

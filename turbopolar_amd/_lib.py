@@ -107,21 +107,29 @@ def header_symbols() -> list[str]:
     return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(tp_\w+)\s*\(", text, re.M)))
 
 
+def open_library(path) -> ctypes.CDLL:
+    """Loads a build of the library at ``path`` with its symbols kept local
+    and declares the C signatures (``lib()`` for the product library; the
+    measurement build is opened the same way beside it)."""
+    path = Path(path)
+    if not path.exists():
+        raise RuntimeError(
+            f"{path.name} is not built; run `python -m turbopolar_amd.build` "
+            "(the TurboPolar path has no CPU fallback)"
+        )
+    handle = ctypes.CDLL(str(path), mode=ctypes.RTLD_LOCAL)
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return handle
+
+
 def lib() -> ctypes.CDLL:
     """Loads libturbopolar_hip.so (once) and declares the C signatures."""
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
-            raise RuntimeError(
-                f"{LIB_PATH.name} is not built; run `python -m turbopolar_amd.build` "
-                "(the TurboPolar path has no CPU fallback)"
-            )
-        handle = ctypes.CDLL(str(LIB_PATH))
-        for name, (restype, argtypes) in _SIGNATURES.items():
-            fn = getattr(handle, name)
-            fn.restype = restype
-            fn.argtypes = argtypes
-        _lib = handle
+        _lib = open_library(LIB_PATH)
     return _lib
 
 
