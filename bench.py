@@ -349,6 +349,28 @@ def run_layers(args, layout) -> dict:
     return {"ms": ms, "pps": pps, "n_pages": n_pages, "outputs_match_first_step": ok, "graph_equal": graph_equal}
 
 
+def _gpu_busy_ms(step, n: int):
+    """Sum of the device kernel durations of one ``step()`` (median over ``n``
+    profiled steps, torch.profiler's device activity), in ms; None if the
+    profiler gives no device events here."""
+    import torch
+
+    try:
+        from torch.profiler import ProfilerActivity, profile
+        per = []
+        for _ in range(n):
+            with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+                with torch.no_grad():
+                    step()
+                torch.cuda.synchronize()
+            us = sum(e.time_range.elapsed_us() for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA)
+            per.append(us / 1e3)
+        busy = float(np.median(per))
+        return round(busy, 3) if busy > 0 else None
+    except Exception:  # pragma: no cover - profiler unavailable
+        return None
+
+
 def run_model(args) -> dict:
     """§8 f2: decode through a randomly initialised Llama of the configs[1]
     shape (``args.layers`` layers, ``args.hq`` / ``args.hkv`` heads, head_dim
@@ -383,6 +405,7 @@ def run_model(args) -> dict:
     tokens = torch.randint(0, cfg.vocab_size, (1, args.warmup + args.steps), generator=g, device=dev)
     res = {}
     logits = {}
+    busy = {}
     for name, cache in (("dense", dense), ("turbo", turbo)):
         if name == "turbo":
             tl.patch_llama_attention(model)
@@ -398,12 +421,15 @@ def run_model(args) -> dict:
                 torch.cuda.synchronize()
                 res[name] = (time.perf_counter() - t0) / args.steps
                 logits[name] = torch.stack(outs).double()
+                # three more steps (after the timed ones) under the profiler
+                busy[name] = _gpu_busy_ms(lambda: model(tokens[:, -1:], past_key_values=cache, use_cache=True), 3)
         finally:
             tl.unpatch_llama_attention(model)
     a, b = logits["turbo"], logits["dense"]
     cos = torch.nn.functional.cosine_similarity(a, b, dim=-1)
     top1 = (a.argmax(-1) == b.argmax(-1)).double().mean()
     return {"turbo_s": res["turbo"], "dense_s": res["dense"], "cos_min": float(cos.min()), "top1": float(top1),
+            "turbo_busy_ms": busy.get("turbo"), "dense_busy_ms": busy.get("dense"),
             "turbo_bytes": int(turbo.nbytes), "dense_bytes": int(sum(x.numel() * x.element_size() for x in (
                 *[layer.keys for layer in dense.layers], *[layer.values for layer in dense.layers])))}
 
@@ -1204,6 +1230,9 @@ def main():
                                "kv_bytes": r["dense_bytes"], "note": "the model's own DynamicCache (the same fp16 "
                                                                       "K/V values held as fp32), eager attention"},
             "turbo_kv_bytes": r["turbo_bytes"],
+            "gpu_busy_ms_per_token": {"turbo": r["turbo_busy_ms"], "dense": r["dense_busy_ms"],
+                                      "note": "sum of device kernel durations of one forward (torch.profiler), "
+                                              "against ms_per_step of wall clock"},
             "checks": {"logit_cosine_min_vs_dense": round(r["cos_min"], 6), "top1_agreement_vs_dense": r["top1"]},
         }))
         return

@@ -212,8 +212,11 @@ int32_t tp_decode_pages_into(const tp_page_layout* layout, const tp_pages* pages
  * (up to 16 token rows of 128 fp16 or 8 of fp32) it also reports completion
  * itself (epoch or epoch + 1), so the call polls the flag instead of
  * synchronising the stream (bounded, then synchronising).  Pass a fresh epoch
- * per call so the flag never needs clearing.  With check == 0 the call is
- * asynchronous like the others. */
+ * per call so the flag never needs clearing.  check == 3 (deferred verdict, no
+ * counterpart in the reference): as check == 2, but the call returns after the
+ * launch and the kernel only ever writes epoch + 1 (on a non-finite value);
+ * the caller reads the flag once the stream has passed the launch.  With
+ * check == 0 or 3 the call is asynchronous like the others. */
 int32_t tp_append_stage(const void* k, const void* v, int32_t in_dtype, int64_t bh, int64_t in_tokens,
                         int64_t copy_begin, int64_t n_copy, void* tail_k, void* tail_v, int64_t tail_tokens,
                         int64_t tail_pos, int32_t check, uint32_t* flag, uint32_t epoch, void* stream);

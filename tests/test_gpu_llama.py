@@ -122,8 +122,8 @@ def test_hook_attention_matches_oracle(device):
     seen = []
     orig = TurboPolarFastCache.decode_attention
 
-    def capture(self, q, k_new, v_new, scale):
-        out = orig(self, q, k_new, v_new, scale)
+    def capture(self, q, k_new, v_new, scale, **kw):
+        out = orig(self, q, k_new, v_new, scale, **kw)
         if self is cache.fast(1):
             rt = self.runtime
             block, qv, tk, tv, _, seq = rt.get_fused_attention_inputs()
@@ -171,3 +171,32 @@ def test_hook_attention_matches_oracle(device):
         checked += 1
     assert checked >= 14 and seen[2]["blk"] is None and seen[3]["blk"] is not None and seen[3]["tk"] is None
     assert seen[67]["seq"] == 128 and seen[67]["tk"] is None and seen[68]["tk"].shape[2] == 1
+
+
+def test_nonfinite_kv_in_one_layer_undoes_the_token_everywhere(device):
+    """The hook defers each layer's non-finite verdict and reads them once per
+    forward: a NaN in layer 1's K raises the reference's ValueError from the
+    forward and leaves every layer at its previous length; the next finite
+    step continues as if the bad one never happened."""
+    model = _model(device)
+    cache = tl.make_turbo_cache(model)
+    twin = tl.make_turbo_cache(model)
+    ids = torch.arange(20, device=device)[None] % 512
+    with torch.no_grad():
+        model(ids, past_key_values=cache, use_cache=True)
+        model(ids, past_key_values=twin, use_cache=True)
+        tl.patch_llama_attention(model)
+        try:
+            w = model.model.layers[1].self_attn.k_proj.weight
+            saved = w.data.clone()
+            w.data[3, :] = float("nan")
+            with pytest.raises(ValueError, match="finite"):
+                model(torch.tensor([[7]], device=device), past_key_values=cache, use_cache=True)
+            w.data.copy_(saved)
+            assert [cache.fast(i).offset for i in range(2)] == [20, 20]
+            la = model(torch.tensor([[9]], device=device), past_key_values=cache, use_cache=True).logits
+            lb = model(torch.tensor([[9]], device=device), past_key_values=twin, use_cache=True).logits
+        finally:
+            tl.unpatch_llama_attention(model)
+    assert torch.equal(la, lb)
+    assert [cache.fast(i).offset for i in range(2)] == [21, 21]

@@ -344,3 +344,61 @@ def test_tail_views_follow_the_cache(device):
     assert torch.equal(rt.partial_k, k[:, :, 64:70])
     _, _, tk2, _, _, seq2 = rt.get_fused_attention_inputs()
     assert seq2 == 70 and torch.equal(tk2, k[:, :, 64:70])
+
+
+@pytest.mark.parametrize("start", [10, 63, 127])
+def test_deferred_check_rolls_back(device, start):
+    """append(..., defer_check=True) does not wait for the non-finite verdict;
+    resolve_deferred_check() reads it.  A non-finite token (here also one that
+    completes a page: start 63, 127) is undone with every deferred append
+    after it, the reference's ValueError is raised, and the cache then equals
+    a twin that never saw the token: same counters, same pages, same decode
+    output bit for bit."""
+    cfg = _cfg("default", hq=8, hkv=2)
+    g = torch.Generator(device=device).manual_seed(start)
+    kv = torch.randn((1, 2, start + 8, 128), generator=g, device=device).half()
+    a, b = TurboPolarFastCache(cfg), TurboPolarFastCache(cfg)
+    a.runtime.append(kv[:, :, :start], kv[:, :, :start])
+    b.runtime.append(kv[:, :, :start], kv[:, :, :start])
+    bad = kv[:, :, start:start + 1].clone()
+    bad[0, 1, 0, 5] = float("nan")
+    a.runtime.append(bad, kv[:, :, start:start + 1], defer_check=True)  # returns without a verdict
+    nxt = kv[:, :, start + 1:start + 2]
+    if (start + 1) % PAGE:  # the bad token left a tail: a second deferred append stacks on it
+        a.runtime.append(nxt, nxt, defer_check=True)
+        assert a.runtime.deferred_verdict_pending() and a.offset == start + 2
+        with pytest.raises(ValueError, match="finite"):
+            a.runtime.resolve_deferred_check()
+    else:  # it completed a page: the next deferred append would restart the tail, so it resolves first
+        assert a.runtime.deferred_verdict_pending() and a.offset == start + 1
+        with pytest.raises(ValueError, match="finite"):
+            a.runtime.append(nxt, nxt, defer_check=True)
+    assert not a.runtime.deferred_verdict_pending()
+    for attr in ("actual_seq_len", "_tail_len", "total_blocks", "bytes_written"):
+        assert getattr(a.runtime, attr) == getattr(b.runtime, attr), attr
+    assert a.runtime.k_storage.block_count == b.runtime.k_storage.block_count
+    # Both continue with the same finite tokens (deferred, then resolved) and agree exactly.
+    q = torch.randn((1, 8, 1, 128), generator=g, device=device).half()
+    for t in range(start + 1, start + 8):
+        tok = kv[:, :, t:t + 1]
+        oa = a.decode_attention(q, tok, tok, 0.088, defer_check=True)
+        ob = b.decode_attention(q, tok, tok, 0.088)
+        assert torch.equal(oa, ob), t
+    a.runtime.resolve_deferred_check()
+    assert a.offset == b.offset == start + 7
+
+
+def test_deferred_check_resolved_by_next_plain_append(device):
+    """A pending deferred verdict is resolved before any append that is not
+    itself deferred, so a non-finite token cannot slip past the contract."""
+    rt = TurboPolarKVCacheRuntime(_cfg("default", hq=4, hkv=2))
+    x = torch.randn((1, 2, 5, 128), device=device).half()
+    rt.append(x, x)
+    bad = x[:, :, :1].clone()
+    bad[0, 0, 0, 0] = float("inf")
+    rt.append(bad, x[:, :, :1], defer_check=True)
+    with pytest.raises(ValueError, match="finite"):
+        rt.append(x[:, :, :2], x[:, :, :2])
+    assert rt.actual_seq_len == 5 and rt._tail_len == 5
+    rt.append(x[:, :, :2], x[:, :, :2])
+    assert rt.actual_seq_len == 7

@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256) void append_stage_kernel(AppendArgs a) {
     if (threadIdx.x == 0)
       __hip_atomic_store(a.flag, any_bad ? a.epoch + 1u : a.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
   } else if (bad) {  // every writer stores the same value
-    if (a.check == 2)
+    if (a.check >= 2)
       __hip_atomic_store(a.flag, a.epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);  // pinned host flag
     else
       *a.flag = a.epoch;
@@ -104,8 +104,9 @@ int32_t tp_append_stage(const void* k, const void* v, int32_t in_dtype, int64_t 
               (long long)tail_tokens);
     return TP_ERR_INVALID;
   }
-  if (check < 0 || check > 2 || (check && !flag) || (check == 2 && (epoch & 1u))) {
-    set_error("check must be 0, 1 (device flag) or 2 (pinned host flag, even epoch), with a flag when checking");
+  if (check < 0 || check > 3 || (check && !flag) || (check >= 2 && (epoch & 1u))) {
+    set_error("check must be 0, 1 (device flag), 2 (pinned host flag, even epoch) or 3 (deferred, pinned host "
+              "flag, even epoch), with a flag when checking");
     return TP_ERR_INVALID;
   }
   const uintptr_t al = (uintptr_t)k | (uintptr_t)v | (uintptr_t)tail_k | (uintptr_t)tail_v;
@@ -135,7 +136,7 @@ int32_t tp_append_stage(const void* k, const void* v, int32_t in_dtype, int64_t 
   else
     hipLaunchKernelGGL(append_stage_kernel<false>, dim3(blocks), dim3(256), 0, s, a);
   int32_t st = launch_status("tp_append_stage");
-  if (st != TP_OK || !check) return st;
+  if (st != TP_OK || !check || check == 3) return st;
   if (check == 2) {  // the kernel writes the pinned host flag directly, no copy
     volatile uint32_t* vf = reinterpret_cast<volatile uint32_t*>(flag);
     uint32_t verdict = 0;

@@ -117,14 +117,18 @@ class TurboPolarFastCache:
             raise ValueError(f"decode_attention requires GQA ratio to divide evenly, got {H_q} and {H_kv}")
 
     def decode_attention(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
-                         scale: float) -> torch.Tensor:
+                         scale: float, defer_check: bool = False) -> torch.Tensor:
         """One decode step (turbopolar_fast_attention.py:106-188): append the
         token's K/V ``[1, H_kv, 1, 128]`` and attend ``q`` ``[1, H_q, 1, 128]``
         over every cached token with ``scale`` (taken as fp16, as the
-        reference's kernels receive it).  Returns fp16 ``[1, H_q, 128]``."""
+        reference's kernels receive it).  Returns fp16 ``[1, H_q, 128]``.
+
+        ``defer_check``: the append's non-finite verdict is read later by
+        ``runtime.resolve_deferred_check()`` instead of now (no stream drain
+        per step; the transformers hook resolves every layer once per forward)."""
         self._validate_decode_shape(q, k_new, v_new, self.config)
         rt = self.runtime
-        rt.append(k_new.to(torch.float16), v_new.to(torch.float16))
+        rt.append(k_new.to(torch.float16), v_new.to(torch.float16), defer_check=defer_check)
         if self._scale[0] != scale:
             self._scale = (scale, fp16_scale(scale))
         n_pages = rt.k_storage.block_count

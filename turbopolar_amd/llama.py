@@ -93,6 +93,22 @@ class TurboPolarCache(Cache):
     def nbytes(self) -> int:
         return sum(layer.fast.nbytes for layer in self.layers)
 
+    def resolve_deferred_checks(self) -> None:
+        """The non-finite verdicts of every layer's deferred appends, after one
+        stream synchronisation.  If any layer's input was non-finite, every
+        layer's pending appends are undone (the cache keeps one length across
+        layers) and the reference's ValueError is raised."""
+        runtimes = [layer.fast.runtime for layer in self.layers if layer.fast.runtime.deferred_verdict_pending()]
+        if not runtimes:
+            return
+        torch.cuda.current_stream(runtimes[0]._tail_k.device).synchronize()
+        if any(rt._bad_pending() is not None for rt in runtimes):
+            for rt in runtimes:
+                rt.rollback_deferred()
+            raise ValueError("append() inputs must contain finite values")
+        for rt in runtimes:
+            rt.resolve_deferred_check(synchronize=False)
+
 
 def make_turbo_cache(model, config: Optional[TurboPolarConfig] = None) -> TurboPolarCache:
     """A ``TurboPolarCache`` sized for ``model``: the reference's fast layout
@@ -164,7 +180,9 @@ def _turbo_llama_attention_forward(
             raise NotImplementedError("TurboPolar fused decode only supports standard causal full-history masks.")
         cos, sin = position_embeddings
         q, k = _llama.apply_rotary_pos_emb(q, k, cos, sin)
-        out = fast.decode_attention(q, k, v, self.scaling)  # [B, H_q, D] fp16
+        # The append's non-finite verdict is read once per forward, for every
+        # layer together, by the model-forward wrapper (no stream drain per layer).
+        out = fast.decode_attention(q, k, v, self.scaling, defer_check=_model_wrapped())  # [B, H_q, D] fp16
         out = out.to(hidden_states.dtype).reshape(B, L, -1)
         return self.o_proj(out), None
     return _orig_llama_attention_forward(
@@ -172,22 +190,49 @@ def _turbo_llama_attention_forward(
     )
 
 
+_orig_llama_model_forward = None
+
+
+def _model_wrapped() -> bool:
+    return _llama.LlamaModel.forward is _turbo_llama_model_forward
+
+
+def _turbo_llama_model_forward(self, *args, **kwargs):
+    """LlamaModel.forward, then the deferred non-finite verdicts of the decode
+    steps it ran on a ``TurboPolarCache``: one synchronisation per forward
+    instead of one per layer.  A non-finite K/V in any layer undoes the
+    token's append in every layer and raises the reference's ValueError
+    (turbo_polar_cache.py:69) from the forward."""
+    out = _orig_llama_model_forward(self, *args, **kwargs)
+    pkv = kwargs.get("past_key_values", args[3] if len(args) > 3 else None)
+    if isinstance(pkv, TurboPolarCache):
+        pkv.resolve_deferred_checks()
+    return out
+
+
 def patch_llama_attention(model=None) -> None:
     """Route Llama decode steps on a ``TurboPolarCache`` through the fused kernel
     (turbopolar_fast_attention.py:283-290).  Patches the class, like the
-    reference; ``model`` is accepted for the same signature."""
-    global _orig_llama_attention_forward
+    reference; ``model`` is accepted for the same signature.  LlamaModel.forward
+    is wrapped too, to read the steps' non-finite verdicts once per forward."""
+    global _orig_llama_attention_forward, _orig_llama_model_forward
     if _orig_llama_attention_forward is None:
         _orig_llama_attention_forward = _llama.LlamaAttention.forward
     _llama.LlamaAttention.forward = _turbo_llama_attention_forward
+    if _orig_llama_model_forward is None:
+        _orig_llama_model_forward = _llama.LlamaModel.forward
+    _llama.LlamaModel.forward = _turbo_llama_model_forward
 
 
 def unpatch_llama_attention(model=None) -> None:
     """Restore the original forward (turbopolar_fast_attention.py:293-298)."""
-    global _orig_llama_attention_forward
+    global _orig_llama_attention_forward, _orig_llama_model_forward
     if _orig_llama_attention_forward is not None:
         _llama.LlamaAttention.forward = _orig_llama_attention_forward
         _orig_llama_attention_forward = None
+    if _orig_llama_model_forward is not None:
+        _llama.LlamaModel.forward = _orig_llama_model_forward
+        _orig_llama_model_forward = None
 
 
 def is_patched() -> bool:

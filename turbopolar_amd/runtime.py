@@ -60,6 +60,9 @@ class TurboPolarKVCacheRuntime:
         self._fused_views = None  # (block_count, storage buffers, (PolarKeyBlock, QuantizedVBlock))
         self._scratch = None  # one-page store for the padded tail when the storage is full
         self._epoch = 0
+        # Appends whose non-finite verdict is deferred (append(..., defer_check=True)):
+        # (epoch, state before the append), oldest first.
+        self._pending: list = []
 
         self._initialized = False
         self._batch_size: Optional[int] = None
@@ -176,14 +179,25 @@ class TurboPolarKVCacheRuntime:
         self.total_blocks += n_pages
         self.bytes_written += n_pages * self._page_bytes()
 
-    def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor, defer_check: bool = False) -> None:
         """turbo_polar_cache.py:106-126: extend the tail, flush every full page.
 
         On a HIP device one tp_append_stage launch checks the whole input for
         non-finite values and copies the tokens bound for the dense tail, with
         a single 4-byte read back (the reference synchronises once per input
         in mx.isfinite(...).all()).  Errors come in the reference's order and
-        leave the cache unchanged."""
+        leave the cache unchanged.
+
+        ``defer_check`` (no counterpart in the reference; single-token appends
+        to an initialised cache on a HIP device, otherwise ignored): the
+        non-finite verdict is not waited for, so the call does not drain the
+        stream.  ``resolve_deferred_check()`` reads it later; an append found
+        non-finite then is undone, with every append after it, and raises the
+        reference's ValueError.  Any other call that appends resolves pending
+        verdicts first, and so does a deferred one that would restart the
+        dense tail (its token would overwrite tail rows an undo restores)."""
+        if self._pending and not (defer_check and k_new.ndim == 4 and k_new.shape[2] == 1 and self._tail_len > 0):
+            self.resolve_deferred_check()
         self._validate_shapes(k_new, v_new)
         if not (k_new.is_cuda and v_new.is_cuda) or self._invariant_error(k_new) is not None:
             self._validate_append_inputs(k_new, v_new)
@@ -207,7 +221,14 @@ class TurboPolarKVCacheRuntime:
             n_head, head_dst = T, 0
         else:
             n_head, head_dst = 0, 0
-        self._stage(k_new, v_new, 0, n_head, head_dst, check=True)
+        # A deferred single token lands at tail position tail_len (< 64) and
+        # overwrites nothing valid (a pending append never lets a later one
+        # restart the tail at row 0), so restoring the counters undoes it.
+        defer = defer_check and T == 1 and self._initialized
+        before = self._state() if defer else None
+        self._stage(k_new, v_new, 0, n_head, head_dst, check=3 if defer else 2)
+        if defer:
+            self._pending.append((self._epoch, before))
         self._commit_invariants(k_new)
         self.actual_seq_len += T
         self._tail_len += n_head
@@ -221,10 +242,53 @@ class TurboPolarKVCacheRuntime:
             pos += n_full * PAGE
         rem = T - pos
         if rem:
-            self._stage(k_new, v_new, pos, rem, 0, check=False)
+            self._stage(k_new, v_new, pos, rem, 0, check=0)
             self._tail_len = rem
 
-    def _stage(self, k, v, begin: int, n: int, dst: int, check: bool) -> None:
+    def _state(self) -> tuple:
+        return (self.actual_seq_len, self._tail_len, self.k_storage.block_count, self.v_storage.block_count,
+                self.total_blocks, self.bytes_written)
+
+    def deferred_verdict_pending(self) -> bool:
+        return bool(self._pending)
+
+    def resolve_deferred_check(self, synchronize: bool = True) -> None:
+        """Reads the verdicts of the deferred appends (one stream
+        synchronisation unless the caller already synchronised: pass
+        ``synchronize=False`` then).  If one found a non-finite value, the cache
+        returns to its state before that append (later appends are undone
+        too) and the reference's ValueError is raised."""
+        if not self._pending:
+            return
+        if synchronize:
+            torch.cuda.current_stream(self._tail_k.device).synchronize()
+        bad = self._bad_pending()
+        if bad is None:
+            self._pending.clear()
+            return
+        self.rollback_deferred()
+        raise ValueError("append() inputs must contain finite values")
+
+    def _bad_pending(self):
+        """Index of the first pending append whose verdict is non-finite (the
+        stream must have passed the launches), or None."""
+        word = int(self._flag[0].item()) & 0xFFFFFFFF
+        for i, (epoch, _) in enumerate(self._pending):
+            if word == (epoch + 1) & 0xFFFFFFFF:
+                return i
+        return None
+
+    def rollback_deferred(self) -> None:
+        """Undoes every pending deferred append (the cache returns to its state
+        before the oldest)."""
+        if not self._pending:
+            return
+        (self.actual_seq_len, self._tail_len, self.k_storage.block_count, self.v_storage.block_count,
+         self.total_blocks, self.bytes_written) = self._pending[0][1]
+        self._fused_views = None
+        self._pending.clear()
+
+    def _stage(self, k, v, begin: int, n: int, dst: int, check: int) -> None:
         B, H, T, _ = k.shape
         # Even epochs: the staging kernel reports epoch (finite) or epoch + 1.
         self._epoch = ((self._epoch + 2) & 0xFFFFFFFE) or 2
@@ -235,7 +299,7 @@ class TurboPolarKVCacheRuntime:
         try:
             st = _lib.lib().tp_append_stage(
                 k.data_ptr(), v.data_ptr(), 1 if k.dtype == torch.float32 else 0, B * H, T, begin, n,
-                self._tail_k.data_ptr(), self._tail_v.data_ptr(), PAGE, dst, 2 if check else 0,
+                self._tail_k.data_ptr(), self._tail_v.data_ptr(), PAGE, dst, check,
                 self._flag.data_ptr(), self._epoch, _lib.raw_stream(idx),
             )
         finally:
@@ -433,6 +497,7 @@ class TurboPolarKVCacheRuntime:
         self._tail_len = 0
         self._scratch = None
         self._fused_views = None
+        self._pending = []
         self._initialized = False
         self._batch_size = None
         self._num_kv_heads = None
