@@ -221,6 +221,20 @@ int32_t tp_append_stage(const void* k, const void* v, int32_t in_dtype, int64_t 
                         int64_t copy_begin, int64_t n_copy, void* tail_k, void* tail_v, int64_t tail_tokens,
                         int64_t tail_pos, int32_t check, uint32_t* flag, uint32_t epoch, void* stream);
 
+/* GroupedVQuantizer.quantize_block (rfsn_v11/quant/v_quant/encoder.py:16-30)
+ * for any group size dividing the row: v is [rows][dim] of in_dtype (0 fp16,
+ * 1 fp32); codes int8 [rows][dim], scales fp16 [rows][dim / group_size].  The
+ * page encoder covers groups of 32 over 128 dims; this covers the rest. */
+int32_t tp_quantize_v_groups(const void* v, int32_t in_dtype, int64_t rows, int32_t dim, int32_t group_size,
+                             int8_t* codes, uint16_t* scales, void* stream);
+
+/* The int8 log radii of PolarQuantEncoder.encode_block with use_int8_radii
+ * (rfsn_v11/quant/polar/encoder.py:34-42) over a block of any length, one
+ * scale per row: radii fp16 [rows][n] (n = tokens x 64 pairs) -> codes int8
+ * [rows][n], scales fp16 [rows].  The page encoder covers 64-token blocks. */
+int32_t tp_log_radii_rows(const void* radii, int64_t rows, int64_t n, int8_t* codes, uint16_t* scales,
+                          void* stream);
+
 /* ---- Self-test hooks: no counterpart in the reference.  They evaluate the
  * encoder's scalar fp16 helpers so tests can check them exhaustively. ---- */
 

@@ -67,24 +67,38 @@ class PolarQuantEncoder:
         assert D == self.head_dim
         assert D % 2 == 0
         meta = self.metadata  # raises ValueError for unsupported bit widths
-        if self.use_int8_radii and L != self.block_size:
-            raise NotImplementedError(
-                "int8 log radii share one scale per 64-token page; encode_block needs L == block_size"
-            )
         n_pages = (L + PAGE - 1) // PAGE
+        # The page encoder takes one log scale per 64-token page; a block of
+        # another length (one scale over all of it, encoder.py:34-42) is
+        # encoded with fp16 radii, whose logs tp_log_radii_rows then codes.
+        whole_row_log = self.use_int8_radii and L != PAGE
         bufs = self.alloc_pages(B, H, n_pages, k_block.device)
+        layout = self.layout
+        if whole_row_log:
+            bufs["radii"] = torch.zeros((B, H, n_pages, PAGE, D // 2), dtype=torch.float16, device=k_block.device)
+            layout = _lib.make_layout(False, self.k_angle_bits_level1, self.k_angle_bits_deep, self.split_dim)
         pages = _lib.TPPages(
-            _lib.ptr(bufs["radii"]), _lib.ptr(bufs["radii_scales"]), _lib.ptr(bufs["angle_codes_l1"]),
-            _lib.ptr(bufs["angle_codes_deep"]), None, None, n_pages,
+            _lib.ptr(bufs["radii"]), None if whole_row_log else _lib.ptr(bufs["radii_scales"]),
+            _lib.ptr(bufs["angle_codes_l1"]), _lib.ptr(bufs["angle_codes_deep"]), None, None, n_pages,
         )
-        encode_pages(k_block.contiguous(), None, 0, L, self.layout, pages, 0)
+        encode_pages(k_block.contiguous(), None, 0, L, layout, pages, 0)
 
         def tokens(t):
             return t.reshape(B, H, n_pages * PAGE, t.shape[-1])[:, :, :L]
 
         scales = bufs["radii_scales"]
+        radii = tokens(bufs["radii"])
+        if whole_row_log:
+            r16 = radii.contiguous()
+            radii = torch.empty(r16.shape, dtype=torch.int8, device=r16.device)
+            scales = torch.empty((B, H), dtype=torch.float16, device=r16.device)
+            with _lib.on_device(r16.device):
+                st = _lib.lib().tp_log_radii_rows(r16.data_ptr(), B * H, L * (D // 2), radii.data_ptr(),
+                                                  scales.data_ptr(), _lib.stream_handle(r16.device))
+            _lib.check(st, "tp_log_radii_rows")
+
         return PolarKeyBlock(
-            radii=tokens(bufs["radii"]),
+            radii=radii,
             angle_codes_l1=tokens(bufs["angle_codes_l1"]),
             angle_codes_deep=tokens(bufs["angle_codes_deep"]),
             shape=(B, H, L, D),
@@ -141,7 +155,7 @@ class GroupedVQuantizer:
         B, H, S, L, D = v_block.shape
         assert D % self.group_size == 0
         if self.group_size != 32 or D != HEAD_DIM:
-            raise NotImplementedError("the HIP quantiser implements groups of 32 over head_dim 128")
+            return self._quantize_groups(v_block)
         T = S * L
         n_pages = (T + PAGE - 1) // PAGE
         dev = v_block.device
@@ -154,9 +168,32 @@ class GroupedVQuantizer:
         scales = scales.reshape(B, H, n_pages * PAGE, D // 32)[:, :, :T].reshape(B, H, S, L, D // 32)
         return QuantizedVBlock(codes=codes, scales=scales, group_size=self.group_size)
 
+    def _quantize_groups(self, v_block: torch.Tensor) -> QuantizedVBlock:
+        """Any group size dividing D (tp_quantize_v_groups)."""
+        B, H, S, L, D = v_block.shape
+        _lib.require_hip(v_block, "v_block")
+        if v_block.dtype not in (torch.float16, torch.float32):
+            raise ValueError(f"quantize_block expects float16 or float32, got {v_block.dtype}")
+        v = v_block.contiguous()
+        codes = torch.empty(v.shape, dtype=torch.int8, device=v.device)
+        scales = torch.empty((B, H, S, L, D // self.group_size), dtype=torch.float16, device=v.device)
+        with _lib.on_device(v.device):
+            st = _lib.lib().tp_quantize_v_groups(v.data_ptr(), 1 if v.dtype == torch.float32 else 0, B * H * S * L, D,
+                                                 self.group_size, codes.data_ptr(), scales.data_ptr(),
+                                                 _lib.stream_handle(v.device))
+        _lib.check(st, "tp_quantize_v_groups")
+        return QuantizedVBlock(codes=codes, scales=scales, group_size=self.group_size)
+
     def dequantize_block(self, block: QuantizedVBlock) -> torch.Tensor:
         """Dense fp16 ``[B, H, S, L, D]`` values."""
         B, H, S, L, D = block.codes.shape
+        if block.group_size != 32 or D != HEAD_DIM:
+            # f16(f32(code) * f32(scale)) on the device: the product of an int8
+            # and an fp16 is exact in fp32, so this rounds once, as the page decoder.
+            _lib.require_hip(block.codes, "codes")
+            g = block.group_size
+            prod = block.codes.reshape(B, H, S, L, D // g, g).float() * block.scales.float()[..., None]
+            return prod.reshape(B, H, S, L, D).half()
         if L > PAGE:
             raise ValueError(f"pages hold at most {PAGE} tokens, got {L}")
         view = QuantizedVBlock(

@@ -510,6 +510,67 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
   a.v_scales[row * kVGroups + qq] = s16;
 }
 
+// ---- codec entry points for shapes outside the page encoder ----------------------
+//
+// GroupedVQuantizer.quantize_block for any group size dividing the row and any
+// row length, and the int8 log radii of an L-token block with one scale per
+// (b, h) row (PolarQuantEncoder.encode_block with use_int8_radii and L != 64).
+// Off the decode path: plain, exact per-element arithmetic, no fast paths.
+
+// One thread per group of `group` values of a row of `dim` (v_quant/encoder.py:
+// 16-30): s = f16(max|v| / 127) (fp16(1e-4) if zero), code = int8(clip(rint(v
+// / s))), the quotient rounded to fp16 first for fp16 input.  A NaN in the
+// group is skipped by the maximum, as in the page encoder.
+template <bool F32IN>
+__global__ __launch_bounds__(256) void quantize_groups_kernel(const void* v, int64_t n_groups, int32_t group,
+                                                              int8_t* codes, uint16_t* scales) {
+  const int64_t gi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gi >= n_groups) return;
+  const int64_t base = gi * group;
+  auto val = [&](int i) -> float {
+    if constexpr (F32IN) return static_cast<const float*>(v)[base + i];
+    else return h2f(static_cast<const uint16_t*>(v)[base + i]);
+  };
+  float m = 0.0f;
+  for (int i = 0; i < group; ++i) m = fmaxf(m, fabsf(val(i)));
+  uint16_t s16 = f2h(m / 127.0f);
+  if ((s16 & 0x7fffu) == 0) s16 = kF16VScaleFloor;
+  const float s = h2f(s16);
+  for (int i = 0; i < group; ++i) {
+    const float q = F32IN ? val(i) / s : h2f(f2h(val(i) / s));
+    codes[base + i] = (int8_t)to_int8_rne(q);
+  }
+  scales[gi] = s16;
+}
+
+// One workgroup per (b, h) row of n fp16 radii (encoder.py:34-42): lr =
+// f32(f16 log(max(r, fp16(1e-6)))), scale = f16(max|lr| / 127) (max 0 ->
+// 1e-6), code = int8(clip(rint(lr / scale))).  The maximum skips NaN, as in
+// the page encoder.
+__global__ __launch_bounds__(256) void log_radii_rows_kernel(const uint16_t* radii, int64_t n, int8_t* codes,
+                                                             uint16_t* scales) {
+  __shared__ float s_max[256];
+  const int64_t row = blockIdx.x;
+  const uint16_t* r = radii + row * n;
+  auto log_r = [&](int64_t i) -> float {
+    const uint16_t rb = r[i] > kF16RadiusFloor ? r[i] : kF16RadiusFloor;
+    return h2f(log_f16(h2f(rb)));
+  };
+  float m = 0.0f;
+  for (int64_t i = threadIdx.x; i < n; i += 256) m = fmaxf(m, fabsf(log_r(i)));
+  s_max[threadIdx.x] = m;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) s_max[threadIdx.x] = fmaxf(s_max[threadIdx.x], s_max[threadIdx.x + w]);
+    __syncthreads();
+  }
+  const float mx = s_max[0];
+  const uint16_t ls16 = f2h((mx == 0.0f ? 1e-6f : mx) / 127.0f);
+  const float ls = h2f(ls16);
+  for (int64_t i = threadIdx.x; i < n; i += 256) codes[row * n + i] = (int8_t)to_int8_rne(log_r(i) / ls);
+  if (threadIdx.x == 0) scales[row] = ls16;
+}
+
 // ---- self-test kernels -------------------------------------------------------
 
 __global__ __launch_bounds__(256) void f16_tables_kernel(uint16_t* sqrt_out, uint16_t* log_out,
@@ -705,6 +766,42 @@ int32_t tp_selftest_atan2_exhaustive(unsigned long long* mismatches, int32_t x_b
   hipLaunchKernelGGL(atan2_exhaustive_kernel, dim3(256, (unsigned)x_count), dim3(256), 0,
                      static_cast<hipStream_t>(stream), mismatches, x_begin);
   return launch_status("tp_selftest_atan2_exhaustive");
+}
+
+int32_t tp_quantize_v_groups(const void* v, int32_t in_dtype, int64_t rows, int32_t dim, int32_t group_size,
+                             int8_t* codes, uint16_t* scales, void* stream) {
+  clear_error();
+  if (in_dtype != 0 && in_dtype != 1) {
+    set_error("in_dtype must be 0 (float16) or 1 (float32), got %d", in_dtype);
+    return TP_ERR_INVALID;
+  }
+  if (!v || !codes || !scales || rows < 1 || dim < 1 || group_size < 1 || dim % group_size) {
+    set_error("bad arguments: rows=%lld dim=%d group_size=%d (the group size must divide dim)", (long long)rows,
+              dim, group_size);
+    return TP_ERR_INVALID;
+  }
+  const int64_t n_groups = rows * (dim / group_size);
+  const unsigned blocks = (unsigned)((n_groups + 255) / 256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (in_dtype)
+    hipLaunchKernelGGL(quantize_groups_kernel<true>, dim3(blocks), dim3(256), 0, s, v, n_groups, group_size, codes,
+                       scales);
+  else
+    hipLaunchKernelGGL(quantize_groups_kernel<false>, dim3(blocks), dim3(256), 0, s, v, n_groups, group_size, codes,
+                       scales);
+  return launch_status("tp_quantize_v_groups");
+}
+
+int32_t tp_log_radii_rows(const void* radii, int64_t rows, int64_t n, int8_t* codes, uint16_t* scales,
+                          void* stream) {
+  clear_error();
+  if (!radii || !codes || !scales || rows < 1 || rows > INT32_MAX || n < 1) {
+    set_error("bad arguments: rows=%lld n=%lld", (long long)rows, (long long)n);
+    return TP_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(log_radii_rows_kernel, dim3((unsigned)rows), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(radii), n, codes, scales);
+  return launch_status("tp_log_radii_rows");
 }
 
 int32_t tp_selftest_vcode_exhaustive(unsigned long long* mismatches, int32_t s_begin, int32_t s_count,
