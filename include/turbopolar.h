@@ -71,6 +71,21 @@ typedef struct tp_pages {
   int64_t capacity; /* page slots per bh */
 } tp_pages;
 
+/* QJL residual sketches of the pages (no counterpart struct in the reference:
+ * it passes QJLPayload.packed_signs / norms and q_proj_signs as separate
+ * arrays, metal.py:532-571).  signs: uint8 [bh][capacity][64][proj_dim / 8],
+ * one sketch per token, page p of row bh in slot bh * capacity + p as in the
+ * page store (16-byte aligned); norms: fp16 [bh][capacity][64] residual norms
+ * (8-byte aligned); q_signs: uint8 [batch][hq][proj_dim / 8] sketches of the
+ * queries (8-byte aligned).  The kernels take proj_dim == 64. */
+typedef struct tp_qjl {
+  const void* signs;
+  const void* norms;
+  const void* q_signs;
+  int32_t proj_dim;
+  int64_t capacity; /* sketch page slots per bh (>= n_pages) */
+} tp_qjl;
+
 /* Last error message of the calling thread ("" if none). */
 const char* tp_last_error(void);
 
@@ -220,6 +235,46 @@ int32_t tp_decode_pages_into(const tp_page_layout* layout, const tp_pages* pages
 int32_t tp_append_stage(const void* k, const void* v, int32_t in_dtype, int64_t bh, int64_t in_tokens,
                         int64_t copy_begin, int64_t n_copy, void* tail_k, void* tail_v, int64_t tail_tokens,
                         int64_t tail_pos, int32_t check, uint32_t* flag, uint32_t epoch, void* stream);
+
+/* ---- QJL (rejected by TurboPolarConfig, turbo_polar_config.py:46-47, as in
+ * the reference; these serve the bridge-level QJL calls the reference's own
+ * tests make). ---- */
+
+/* QJLResidualEncoder.compute_residual_sketch (rfsn_v11/quant/qjl/encoder.py:
+ * 30-44) and the query sketch (q @ W >= 0, packed): e [rows][dim] of in_dtype
+ * (0 fp16, 1 fp32), w fp32 [dim][proj_dim] -> packed uint8 [rows][proj_dim / 8]
+ * (bit i of byte j: projection 8j + i >= 0) and, if norms is not NULL, fp16
+ * [rows] = f16(sqrt(sum e^2)).  dim <= 256, proj_dim a multiple of 8 up to 256. */
+int32_t tp_qjl_sketch(const void* e, int32_t in_dtype, int64_t rows, int32_t dim, const float* w, int32_t proj_dim,
+                      uint8_t* packed, uint16_t* norms, void* stream);
+
+/* qjl_dot_estimate (rfsn_v11/quant/qjl/score_estimate.py:6-54): out fp32
+ * [batch][hq][tokens] = norms[kv][t] * |q[h]| * sin(pi/2 (P - 2 hamming) / P),
+ * kv = h / (hq / hkv); q fp16 [batch][hq][dim], k_packed uint8
+ * [batch][hkv][tokens][P / 8], norms fp16 [batch][hkv][tokens], q_packed uint8
+ * [batch][hq][P / 8]. */
+int32_t tp_qjl_dot_estimate(const void* q, int64_t batch, int32_t hq, int32_t hkv, int32_t dim, const void* k_packed,
+                            const void* norms, int64_t tokens, const void* q_packed, int32_t proj_dim, float* out,
+                            void* stream);
+
+/* tp_fused_qk plus the QJL correction * scale (MetalKernelBridge.
+ * execute_fused_qk_qjl, metal.py:532-571, kernel tqpolar_fused_dequant_qk_qjl,
+ * tqpolar_fused_qk.metal:102-233). */
+int32_t tp_fused_qk_qjl(const void* q, int64_t batch, int32_t hq, int32_t hkv, const tp_page_layout* layout,
+                        const tp_pages* pages, int32_t n_pages, const tp_qjl* qjl, float scale, void* scores,
+                        void* stream);
+
+/* tp_decode_attention with the QJL correction added to the page tokens'
+ * scores (execute_online_attention_quant_v[_dense_tail] with use_qjl=True,
+ * metal.py:651-792, kernel branches tqpolar_online_attention.metal:256-345 and
+ * 459-545; the dense tail gets no correction, metal.py:310-316).  Same
+ * arguments as tp_decode_attention plus qjl. */
+int32_t tp_decode_attention_qjl(const void* q, int64_t batch, int32_t hq, int32_t hkv,
+                                const tp_page_layout* layout, const tp_pages* pages, int32_t n_pages,
+                                const tp_qjl* qjl, const void* tail_k, const void* tail_v, int32_t tail_len,
+                                int64_t tail_stride, int64_t actual_seq_len, float scale,
+                                int32_t pages_per_split, void* workspace, size_t workspace_bytes,
+                                void* out, void* stream);
 
 /* GroupedVQuantizer.quantize_block (rfsn_v11/quant/v_quant/encoder.py:16-30)
  * for any group size dividing the row: v is [rows][dim] of in_dtype (0 fp16,

@@ -37,6 +37,12 @@ tests/test_oracle_attention.py, tests/test_golden.py):
   (tests/exact_f16.py) compared bit for bit, fp32-input wrap cases.
 * quantize_block: known answers (zero group, group max, half-even ties) and
   the exact-rational restatement.
+* qjl_projection / qjl_pack_signs / qjl_residual_sketch / qjl_dot_estimate /
+  cpu_fused_qk_qjl (tests/test_oracle_qjl.py): unit columns and the seed's
+  stream, single-bit known answers of the packing, a pure-Python brute force
+  of the estimator, its closed forms (equal sketches: +|E||q|, complementary:
+  -|E||q|, half the bits: 0) and its consistency (with many projections it
+  converges to q . E, which a wrong sign, factor or bit order breaks).
 * dequantize_block: exact-rational known answers element by element, the
   exact round trip of code x power-of-two values, and the quantisation error
   bound 0.53125 s + half an fp16 ulp.
@@ -75,6 +81,11 @@ __all__ = [
     "cpu_online_attention_dense_tail",
     "softmax_attention",
     "fp16_scale",
+    "qjl_projection",
+    "qjl_pack_signs",
+    "qjl_residual_sketch",
+    "qjl_dot_estimate",
+    "cpu_fused_qk_qjl",
 ]
 
 F16 = np.float16
@@ -408,11 +419,12 @@ def dequantize_block(codes: np.ndarray, scales: np.ndarray, group_size: int = 32
 # attention -- kernels/turbo_polar/metal.py:254-332
 # --------------------------------------------------------------------------
 
-def softmax_attention(q, k, v, scale, actual_seq_len=None, dtype=F64):
+def softmax_attention(q, k, v, scale, actual_seq_len=None, dtype=F64, score_bias=None):
     """Masked softmax attention, GQA broadcast by ``repeat`` (metal.py:259,307-308).
 
     q ``[B,Hq,D]``; k, v ``[B,Hkv,T,D]``.  Tokens ``t >= actual_seq_len`` are
-    masked (metal.py:278-279,318-319).
+    masked (metal.py:278-279,318-319).  ``score_bias`` ``[B,Hq,T]`` is added to
+    the scaled scores before the mask (the QJL correction, metal.py:273-275,310-316).
     """
     B, Hq, D = q.shape
     Hkv = k.shape[1]
@@ -425,6 +437,8 @@ def softmax_attention(q, k, v, scale, actual_seq_len=None, dtype=F64):
     vv = v.astype(dtype)
     with np.errstate(invalid="ignore", over="ignore"):
         s = np.matmul(qg, np.swapaxes(kk, -1, -2)) * dtype(scale)  # [B, Hkv, g, T]
+        if score_bias is not None:
+            s = s + score_bias.astype(dtype).reshape(s.shape)
         if actual_seq_len is not None and actual_seq_len < T:
             s[..., actual_seq_len:] = -np.inf
         m = np.max(s, axis=-1, keepdims=True)
@@ -463,12 +477,75 @@ def cpu_online_attention(q, block, quant_v, scale, actual_seq_len, dtype=F64):
     return softmax_attention(q, k, v.reshape(B, H, S * L, D), scale, actual_seq_len, dtype)
 
 
-def cpu_online_attention_dense_tail(q, block, quant_v, tail_k, tail_v, scale, actual_seq_len, dtype=F64):
-    """``_cpu_online_attention_dense_tail`` (metal.py:293-332)."""
+def cpu_online_attention_dense_tail(q, block, quant_v, tail_k, tail_v, scale, actual_seq_len, dtype=F64,
+                                    qjl=None):
+    """``_cpu_online_attention_dense_tail`` (metal.py:293-332).  ``qjl`` =
+    (packed signs, norms, packed query signs, proj_dim): use_qjl=True, the
+    correction times ``scale`` on the page tokens and 0 on the tail
+    (metal.py:310-316)."""
     codes, scales = quant_v
     k = decode_block(*_block_fields(block))
     v = dequantize_block(codes, scales)
     B, H, S, L, D = codes.shape
     full_k = np.concatenate([k.astype(dtype), tail_k.astype(dtype)], axis=2)
     full_v = np.concatenate([v.reshape(B, H, S * L, D).astype(dtype), tail_v.astype(dtype)], axis=2)
-    return softmax_attention(q, full_k, full_v, scale, actual_seq_len, dtype)
+    bias = None
+    if qjl is not None:
+        corr = qjl_dot_estimate(q, *qjl) * F64(scale)
+        tail = np.zeros((B, q.shape[1], tail_k.shape[2]), F64)
+        bias = np.concatenate([corr, tail], axis=2)
+    return softmax_attention(q, full_k, full_v, scale, actual_seq_len, dtype, score_bias=bias)
+
+
+# --------------------------------------------------------------------------
+# QJL -- rfsn_v11/quant/qjl/encoder.py:19-44, score_estimate.py:6-54,
+# kernels/turbo_polar/metal.py:262-265
+# --------------------------------------------------------------------------
+
+def qjl_projection(seed: int = 42, head_dim: int = 128, proj_dim: int = 64) -> np.ndarray:
+    """QJLResidualEncoder's W (encoder.py:20-28): float32 standard normals of
+    ``np.random.default_rng(seed)``, each column over (its norm + 1e-12)."""
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((head_dim, proj_dim), dtype=np.float32)
+    return w / (np.linalg.norm(w, axis=0, keepdims=True) + 1e-12)
+
+
+def qjl_pack_signs(proj: np.ndarray) -> np.ndarray:
+    """``proj >= 0`` packed along the last axis, bit i of byte j the sign of
+    element 8j + i (encoder.py:36-39: powers 1, 2, ..., 128 summed)."""
+    bits = (proj >= 0).astype(np.uint8)
+    shp = bits.shape[:-1] + (bits.shape[-1] // 8, 8)
+    return (bits.reshape(shp) * (1 << np.arange(8, dtype=np.uint16))).sum(axis=-1).astype(np.uint8)
+
+
+def qjl_residual_sketch(e: np.ndarray, w: np.ndarray):
+    """compute_residual_sketch (encoder.py:30-44): packed signs of e @ W
+    (projections in float64) and the fp16 residual norms."""
+    proj = e.astype(F64) @ w.astype(F64)
+    norms = np.sqrt(np.sum(e.astype(F64) ** 2, axis=-1)).astype(F16)
+    return qjl_pack_signs(proj), norms
+
+
+def qjl_dot_estimate(q, packed, norms, q_packed, proj_dim):
+    """qjl_dot_estimate (score_estimate.py:6-54) in float64: for query head h
+    and token t of kv head h // g, |E_t| |q_h| sin(pi/2 * match / P), match
+    the +-1 sign agreement sum.  packed ``[B,Hkv,S,L,P/8]``, norms
+    ``[B,Hkv,S,L]``, q_packed ``[B,Hq,P/8]``; returns ``[B,Hq,S*L]``."""
+    B, Hkv, S, L, _ = packed.shape
+    Hq = q_packed.shape[1]
+    g = Hq // Hkv
+    kb = np.unpackbits(packed.reshape(-1, proj_dim // 8), axis=1, bitorder="little")[:, :proj_dim]
+    ks = kb.reshape(B, Hkv, S * L, proj_dim).astype(np.int64) * 2 - 1
+    qb = np.unpackbits(q_packed.reshape(-1, proj_dim // 8), axis=1, bitorder="little")[:, :proj_dim]
+    qs = qb.reshape(B, Hq, proj_dim).astype(np.int64) * 2 - 1
+    ks = np.repeat(ks, g, axis=1)
+    match = np.einsum("bhp,bhtp->bht", qs, ks)
+    q_norm = np.sqrt(np.sum(q.astype(F64) ** 2, axis=-1))
+    n = np.repeat(norms.reshape(B, Hkv, S * L).astype(F64), g, axis=1)
+    return n * q_norm[:, :, None] * np.sin((np.pi / 2.0) * match / proj_dim)
+
+
+def cpu_fused_qk_qjl(q, block, qjl, scale, dtype=F64):
+    """``_cpu_fused_qk_qjl`` (metal.py:262-265): the fused-QK scores plus the
+    QJL estimate times ``scale``; ``qjl`` as for cpu_online_attention_dense_tail."""
+    return cpu_fused_qk(q, block, scale, dtype) + qjl_dot_estimate(q, *qjl).astype(dtype) * dtype(scale)

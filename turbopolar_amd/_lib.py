@@ -53,12 +53,23 @@ class TPPages(ctypes.Structure):
     ]
 
 
+class TPQjl(ctypes.Structure):
+    _fields_ = [
+        ("signs", c_vp),
+        ("norms", c_vp),
+        ("q_signs", c_vp),
+        ("proj_dim", c_i32),
+        ("capacity", c_i64),
+    ]
+
+
 class TurboPolarHipError(RuntimeError):
     """A HIP runtime or launch failure inside the TurboPolar library."""
 
 
 _P_LAYOUT = ctypes.POINTER(TPPageLayout)
 _P_PAGES = ctypes.POINTER(TPPages)
+_P_QJL = ctypes.POINTER(TPQjl)
 
 _SIGNATURES = {
     "tp_last_error": (ctypes.c_char_p, []),
@@ -92,6 +103,16 @@ _SIGNATURES = {
         c_i32,
         [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i32, c_vp, ctypes.c_uint32, c_vp],
     ),
+    "tp_fused_qk_qjl": (c_i32, [c_vp, c_i64, c_i32, c_i32, _P_LAYOUT, _P_PAGES, c_i32, _P_QJL, c_float, c_vp, c_vp]),
+    "tp_decode_attention_qjl": (
+        c_i32,
+        [
+            c_vp, c_i64, c_i32, c_i32, _P_LAYOUT, _P_PAGES, c_i32, _P_QJL,
+            c_vp, c_vp, c_i32, c_i64, c_i64, c_float, c_i32, c_vp, c_size, c_vp, c_vp,
+        ],
+    ),
+    "tp_qjl_sketch": (c_i32, [c_vp, c_i32, c_i64, c_i32, c_vp, c_i32, c_vp, c_vp, c_vp]),
+    "tp_qjl_dot_estimate": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_i32, c_vp, c_vp]),
     "tp_quantize_v_groups": (c_i32, [c_vp, c_i32, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
     "tp_log_radii_rows": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "tp_selftest_f16_tables": (c_i32, [c_vp, c_vp, c_vp, c_vp]),

@@ -7,11 +7,14 @@ rfsn_v11/kernels/turbo_polar/metal.py:57-792 for the supported path:
 * ``execute_online_attention_quant_v(...) -> (out, trace)``    (metal.py:651-715)
 * ``execute_online_attention_quant_v_dense_tail(...)``         (metal.py:717-792)
 
-Differences: there is no silent CPU fallback (unsupported inputs raise), the
-trace reports ``hip_used`` where the reference reports ``metal_used``, and
-QJL (``use_qjl=True``) raises NotImplementedError -- the config rejects it
-(turbo_polar_config.py:46-47).  ``attention_scale`` reaches the kernels as
-fp16, as the reference passes it (metal.py:518,692,774).
+* ``execute_fused_qk_qjl(q, block, qjl_payload, q_proj_signs, config)`` (metal.py:532-571)
+
+Differences: there is no silent CPU fallback (unsupported inputs raise), and
+the trace reports ``hip_used`` where the reference reports ``metal_used``.
+``use_qjl=True`` adds the QJL correction to the page tokens' scores
+(tp_decode_attention_qjl; the config still rejects QJL for the runtime,
+turbo_polar_config.py:46-47, as in the reference).  ``attention_scale``
+reaches the kernels as fp16, as the reference passes it (metal.py:518,692,774).
 """
 
 from __future__ import annotations
@@ -23,6 +26,7 @@ import torch
 from . import _lib
 from .kernels import PageSet, decode_attention, fp16_scale, fused_qk
 from .payload import PolarKeyBlock, QuantizedVBlock
+from .qjl import QJLPages
 
 
 def _pages_of(block: PolarKeyBlock, quant_v: Optional[QuantizedVBlock], head_dim: int) -> PageSet:
@@ -60,13 +64,24 @@ class HipKernelBridge:
             raise ValueError(f"unsupported radii dtype: {block.radii.dtype}")
 
     @staticmethod
-    def _no_qjl(use_qjl: bool) -> None:
-        if use_qjl:
-            raise NotImplementedError("QJL is not supported in this release; set use_qjl=False")
+    def _qjl(use_qjl: bool, qjl_payload, q_proj_signs) -> Optional[QJLPages]:
+        """The QJL descriptor when use_qjl (metal.py:573-580's check), else None."""
+        if not use_qjl:
+            return None
+        if qjl_payload is None or q_proj_signs is None:
+            raise ValueError("qjl_payload and q_proj_signs are required when use_qjl=True")
+        return QJLPages(qjl_payload, q_proj_signs)
 
     def execute_fused_qk(self, q: torch.Tensor, block: PolarKeyBlock, config) -> torch.Tensor:
         self._supports_block(block)
         return fused_qk(q, PageSet(block, None, config.head_dim), fp16_scale(config.attention_scale))
+
+    def execute_fused_qk_qjl(self, q: torch.Tensor, block: PolarKeyBlock, qjl_payload, q_proj_signs: torch.Tensor,
+                             config) -> torch.Tensor:
+        """Scores plus the QJL correction times attention_scale (metal.py:532-571)."""
+        self._supports_block(block)
+        qjl = self._qjl(True, qjl_payload, q_proj_signs)
+        return fused_qk(q, PageSet(block, None, config.head_dim), fp16_scale(config.attention_scale), qjl=qjl)
 
     def execute_online_attention_quant_v(
         self,
@@ -79,16 +94,16 @@ class HipKernelBridge:
         actual_seq_len: int,
         use_qjl: bool = False,
     ) -> Tuple[torch.Tensor, Dict[str, Any]]:
-        self._no_qjl(use_qjl)
+        qjl = self._qjl(use_qjl, qjl_payload, q_proj_signs)
         self._supports_block(block)
         pages = _pages_of(block, quant_v, config.head_dim)
-        out = decode_attention(q, pages, None, None, actual_seq_len, fp16_scale(config.attention_scale))
+        out = decode_attention(q, pages, None, None, actual_seq_len, fp16_scale(config.attention_scale), qjl=qjl)
         trace = {
             "kernel_name": "tqpolar_online_attention_quant_v",
-            "hip_kernel": "tp_decode_attention",
+            "hip_kernel": "tp_decode_attention_qjl" if use_qjl else "tp_decode_attention",
             "hip_used": True,
             "fallback_used": False,
-            "qjl_used": False,
+            "qjl_used": bool(use_qjl),
             "quant_v_used": True,
             "actual_seq_len": actual_seq_len,
             "num_queries_per_kv": q.shape[1] // pages.H,
@@ -108,7 +123,7 @@ class HipKernelBridge:
         actual_seq_len: int,
         use_qjl: bool = False,
     ) -> Tuple[torch.Tensor, Dict[str, Any]]:
-        self._no_qjl(use_qjl)
+        qjl = self._qjl(use_qjl, qjl_payload, q_proj_signs)
         pages = None
         if block is not None:
             self._supports_block(block)
@@ -116,15 +131,15 @@ class HipKernelBridge:
         tail_len = int(tail_k.shape[2]) if tail_k is not None else 0
         out = decode_attention(
             q, pages, tail_k if tail_len else None, tail_v if tail_len else None,
-            actual_seq_len, fp16_scale(config.attention_scale),
+            actual_seq_len, fp16_scale(config.attention_scale), qjl=qjl if pages is not None else None,
         )
         hkv = pages.H if pages is not None else int(tail_k.shape[1])
         trace = {
             "kernel_name": "tqpolar_online_attention_quant_v_dense_tail",
-            "hip_kernel": "tp_decode_attention",
+            "hip_kernel": "tp_decode_attention_qjl" if (use_qjl and pages is not None) else "tp_decode_attention",
             "hip_used": True,
             "fallback_used": False,
-            "qjl_used": False,
+            "qjl_used": bool(use_qjl),
             "quant_v_used": True,
             "tail_length": tail_len,
             "actual_seq_len": actual_seq_len,

@@ -27,7 +27,7 @@ LIB_PATH = PKG_DIR / LIB_NAME
 TIMELINE_LIB_PATH = PKG_DIR / "libturbopolar_hip_timeline.so"
 ARCH = os.environ.get("TP_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["tp_api.hip", "tp_encode.hip", "tp_attention.hip", "tp_decode.hip", "tp_append.hip"]
+SOURCES = ["tp_api.hip", "tp_encode.hip", "tp_attention.hip", "tp_decode.hip", "tp_append.hip", "tp_qjl.hip"]
 MEASURE_SOURCES = ["tp_measure.hip"]  # measurement library only
 
 # -ffp-contract=off and correctly rounded fp32 divide/sqrt are required for the

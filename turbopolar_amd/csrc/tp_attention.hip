@@ -97,6 +97,12 @@ struct AttnArgs {
   uint32_t* counters;
   float* part_ml;
   float* part_acc;
+  // QJL (tp_fused_qk_qjl, tp_decode_attention_qjl): per-token sketch and
+  // residual norm in the page slots, the queries' sketches.
+  const uint64_t* qjl_signs;
+  const uint16_t* qjl_norms;
+  const uint64_t* q_signs;
+  int64_t qjl_capacity;  // sketch slots per bh
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -213,6 +219,58 @@ __device__ __forceinline__ void load_q(const AttnArgs& a, int b, int kv, int h0,
     uint4 w = make_uint4(0u, 0u, 0u, 0u);
     if (l16 < nh) w = *reinterpret_cast<const uint4*>(qrow + 8 * kk);
     qb[kk] = as_half8(w.x, w.y, w.z, w.w);
+  }
+}
+
+// ---- QJL correction ---------------------------------------------------------------
+//
+// tqpolar_fused_qk.metal:200-231, metal.py:262-275 and score_estimate.py:6-54:
+// the score of token t for query head h gains |E_t| |q_h| sin(pi/2 (P - 2
+// hamming(sketch_t, sketch_h)) / P) (before the attention scale), P = 64
+// sketch bits.  The sine of the 65 possible Hamming distances is a table in LDS.
+
+constexpr int kQjlBits = 64;
+
+__device__ __forceinline__ void build_qjl_sin(float* tab, int tid) {
+  if (tid <= kQjlBits) tab[tid] = sinf(1.57079632679489662f * (float)(kQjlBits - 2 * tid) / (float)kQjlBits);
+}
+
+// |q| of the lane's head from its MFMA B operands (32 dims per lane, rows
+// l4 = 0..3 hold the four quarters) and the head's sketch.
+__device__ __forceinline__ void qjl_query(const AttnArgs& a, int b, int kv, int h0, int nh, int l16, const half8v* qb,
+                                          uint64_t& qsig, float& qnorm) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = (float)qb[kk][e];
+      ss = __builtin_fmaf(x, x, ss);
+    }
+  }
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  qnorm = sqrtf(ss);
+  qsig = l16 < nh ? a.q_signs[(int64_t)b * a.hq + (int64_t)kv * a.g + h0 + l16] : 0ull;
+}
+
+// Adds the correction to one page's scores s[mt][i] (token 16*mt + 4*l4 + i,
+// head l16) of page slot `slot`.
+__device__ __forceinline__ void qjl_correct(const AttnArgs& a, int64_t slot, int l4, uint64_t qsig, float qnorm,
+                                            const float* sin_tab, float4v* s) {
+  const uint64_t* sg = a.qjl_signs + slot * kPageTokens + 4 * l4;
+  const uint16_t* nm = a.qjl_norms + slot * kPageTokens + 4 * l4;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const u32x4 w01 = *reinterpret_cast<const u32x4*>(sg + 16 * mt);
+    const u32x4 w23 = *reinterpret_cast<const u32x4*>(sg + 16 * mt + 2);
+    const uint2 nn = *reinterpret_cast<const uint2*>(nm + 16 * mt);
+    const uint64_t k[4] = {((uint64_t)w01.y << 32) | w01.x, ((uint64_t)w01.w << 32) | w01.z,
+                           ((uint64_t)w23.y << 32) | w23.x, ((uint64_t)w23.w << 32) | w23.z};
+    const float n[4] = {h2f((uint16_t)(nn.x & 0xffffu)), h2f((uint16_t)(nn.x >> 16)), h2f((uint16_t)(nn.y & 0xffffu)),
+                        h2f((uint16_t)(nn.y >> 16))};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[mt][i] += n[i] * qnorm * sin_tab[__builtin_popcountll(k[i] ^ qsig)];
   }
 }
 
@@ -836,7 +894,7 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
 
 // ---- decode attention kernel ---------------------------------------------------
 
-template <int KIND, int WAVES, bool REL = false>
+template <int KIND, int WAVES, bool REL = false, bool QJL = false>
 __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a) {
   // The fold maps 512 threads onto up to 16 heads x 128 dims at 1, 2 or 4 dims
   // per thread, and the combine sizes its split groups for 512 threads.
@@ -894,6 +952,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     load_v(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
   }
   if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
+  __shared__ float qjl_sin[QJL ? kQjlBits + 1 : 1];
+  uint64_t qsig = 0;
+  float qnorm = 0.0f;
+  if constexpr (QJL) {
+    build_qjl_sin(qjl_sin, tid);
+    qjl_query(a, b, kv, h0, nh, l16, qb, qsig, qnorm);
+  }
   lds_barrier();
   TP_STAMP(2);
 
@@ -914,6 +979,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   for (int it = 0; page + WAVES < p_end; page += WAVES, ++it) {
     float4v s[4];
     qk_regs<KIND>(a, sh.lut, kr, qb, l16, l4, s);
+    if constexpr (QJL) qjl_correct(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
     if (it < 12) TP_STAMP(4 + 4 * it);
     load_k<KIND>(a, bkv * a.capacity + page + WAVES, l16, l4, kr);
     half8v pb[2];
@@ -925,13 +991,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   if (page < p_end) {
     float4v s[4];
     qk_regs<KIND>(a, sh.lut, kr, qb, l16, l4, s);
+    if constexpr (QJL) qjl_correct(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
     const int valid = (int)min((int64_t)kPageTokens, a.seq_len - (int64_t)page * kPageTokens);
     half8v pb[2];
     softmax_page(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
     pv_regs(vr, sbase4, ssel, pb, acc);
   }
 
-  // The dense tail follows the last page; the last split's least loaded wave takes it.
+  // The dense tail follows the last page; the last split's least loaded wave
+  // takes it (no QJL correction on the tail: metal.py:310-316 pads it with 0).
   if (split == a.n_splits - 1 && a.tail_len > 0) {
     const int n_local = max(p_end - p_begin, 0);
     if (wave == n_local % WAVES) {
@@ -1240,9 +1308,10 @@ __global__ __launch_bounds__(512) void decode_attention_valu_kernel(AttnArgs a) 
 
 // ---- standalone fused QK -----------------------------------------------------------
 
-template <int KIND>
+template <int KIND, bool QJL = false>
 __global__ __launch_bounds__(256) void fused_qk_kernel(AttnArgs a) {
   __shared__ Lut lut;
+  __shared__ float qjl_sin[QJL ? kQjlBits + 1 : 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
@@ -1262,10 +1331,17 @@ __global__ __launch_bounds__(256) void fused_qk_kernel(AttnArgs a) {
   KRegs<KIND> kr;
   load_k<KIND>(a, bkv * a.capacity + min(page, a.n_pages - 1), l16, l4, kr);
   build_lut<KIND>(lut, a, tid);
+  uint64_t qsig = 0;
+  float qnorm = 0.0f;
+  if constexpr (QJL) {
+    build_qjl_sin(qjl_sin, tid);
+    qjl_query(a, b, kv, h0, nh, l16, qb, qsig, qnorm);
+  }
   __syncthreads();
   if (page >= a.n_pages) return;
   float4v s[4];
   qk_regs<KIND>(a, lut, kr, qb, l16, l4, s);
+  if constexpr (QJL) qjl_correct(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
   if (l16 >= nh) return;
   const int64_t hq_idx = (int64_t)b * a.hq + (int64_t)kv * a.g + h0 + l16;
   uint16_t* srow = a.scores + hq_idx * ((int64_t)a.n_pages * kPageTokens) + (int64_t)page * kPageTokens + 4 * l4;
@@ -1411,6 +1487,56 @@ int32_t tp_fused_qk(const void* q, int64_t batch, int32_t hq, int32_t hkv,
   return launch_status("tp_fused_qk");
 }
 
+// Validates a tp_qjl against the pages and fills the kernel arguments.
+static bool fill_qjl(AttnArgs& a, const tp_qjl* qjl, int32_t n_pages) {
+  if (!qjl) {
+    set_error("qjl_payload and q_proj_signs are required when use_qjl=True");
+    return false;
+  }
+  if (qjl->proj_dim != kQjlBits) {
+    set_error("the QJL kernels take proj_dim == %d sketch bits, got %d", kQjlBits, qjl->proj_dim);
+    return false;
+  }
+  if (!qjl->q_signs || ((uintptr_t)qjl->q_signs & 7u) ||
+      (n_pages > 0 && (!qjl->signs || !qjl->norms || ((uintptr_t)qjl->signs & 15u) || ((uintptr_t)qjl->norms & 7u)))) {
+    set_error("QJL buffers missing or misaligned (sketches 16-byte, norms and query sketches 8-byte aligned)");
+    return false;
+  }
+  if (n_pages > 0 && qjl->capacity < n_pages) {
+    set_error("QJL sketch capacity %lld is below n_pages=%d", (long long)qjl->capacity, n_pages);
+    return false;
+  }
+  a.qjl_capacity = qjl->capacity;
+  a.qjl_signs = static_cast<const uint64_t*>(qjl->signs);
+  a.qjl_norms = static_cast<const uint16_t*>(qjl->norms);
+  a.q_signs = static_cast<const uint64_t*>(qjl->q_signs);
+  return true;
+}
+
+int32_t tp_fused_qk_qjl(const void* q, int64_t batch, int32_t hq, int32_t hkv, const tp_page_layout* layout,
+                        const tp_pages* pages, int32_t n_pages, const tp_qjl* qjl, float scale, void* scores,
+                        void* stream) {
+  clear_error();
+  AttnArgs a{};
+  if (!fill_common(a, q, batch, hq, hkv, layout, pages, n_pages, false)) return TP_ERR_INVALID;
+  if (!fill_qjl(a, qjl, n_pages)) return TP_ERR_INVALID;
+  if (n_pages == 0) return TP_OK;
+  if (!scores || ((uintptr_t)scores & 7u)) {
+    set_error("scores must be a non-NULL 8-byte aligned buffer");
+    return TP_ERR_INVALID;
+  }
+  a.scores = static_cast<uint16_t*>(scores);
+  a.scale = scale;
+  const dim3 grid((unsigned)((n_pages + 3) / 4), (unsigned)(batch * hkv), (unsigned)a.head_blocks);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (layout_kind(layout)) {
+    case kKindDefault: hipLaunchKernelGGL((fused_qk_kernel<kKindDefault, true>), grid, dim3(256), 0, s, a); break;
+    case kKindFast: hipLaunchKernelGGL((fused_qk_kernel<kKindFast, true>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((fused_qk_kernel<kKindGeneric, true>), grid, dim3(256), 0, s, a); break;
+  }
+  return launch_status("tp_fused_qk_qjl");
+}
+
 #ifdef TP_TIMELINE
 // Measurement library only: the decode-kernel variant tp_decode_attention
 // launches (0: the product kernel; 1: + agent-scope release fence before the
@@ -1449,15 +1575,19 @@ static int32_t launch_measure_variant(const AttnArgs& a, dim3 grid, int kind, hi
 }
 #endif
 
-int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hkv,
-                            const tp_page_layout* layout, const tp_pages* pages, int32_t n_pages,
-                            const void* tail_k, const void* tail_v, int32_t tail_len,
-                            int64_t tail_stride, int64_t actual_seq_len, float scale,
-                            int32_t pages_per_split, void* workspace, size_t workspace_bytes,
-                            void* out, void* stream) {
+}  // extern "C"
+
+// tp_decode_attention and, with qjl, tp_decode_attention_qjl.
+static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, int32_t hkv,
+                                     const tp_page_layout* layout, const tp_pages* pages, int32_t n_pages,
+                                     const tp_qjl* qjl, const void* tail_k, const void* tail_v, int32_t tail_len,
+                                     int64_t tail_stride, int64_t actual_seq_len, float scale,
+                                     int32_t pages_per_split, void* workspace, size_t workspace_bytes, void* out,
+                                     void* stream, bool use_qjl) {
   clear_error();
   AttnArgs a{};
   if (!fill_common(a, q, batch, hq, hkv, layout, pages, n_pages, true)) return TP_ERR_INVALID;
+  if (use_qjl && !fill_qjl(a, qjl, n_pages)) return TP_ERR_INVALID;
   if (!out || ((uintptr_t)out & 15u)) {
     set_error("out must be a non-NULL 16-byte aligned buffer");
     return TP_ERR_INVALID;
@@ -1519,6 +1649,21 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
   }
   const dim3 grid((unsigned)n_groups);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (use_qjl) {
+    const dim3 block(kDecodeWaves * 64);
+    switch (n_pages > 0 ? layout_kind(layout) : (int)kKindGeneric) {
+      case kKindDefault:
+        hipLaunchKernelGGL((decode_attention_kernel<kKindDefault, kDecodeWaves, false, true>), grid, block, 0, s, a);
+        break;
+      case kKindFast:
+        hipLaunchKernelGGL((decode_attention_kernel<kKindFast, kDecodeWaves, false, true>), grid, block, 0, s, a);
+        break;
+      default:
+        hipLaunchKernelGGL((decode_attention_kernel<kKindGeneric, kDecodeWaves, false, true>), grid, block, 0, s, a);
+        break;
+    }
+    return launch_status("tp_decode_attention_qjl");
+  }
 #ifdef TP_TIMELINE
   if (g_measure_variant != 0) return launch_measure_variant(a, grid, n_pages > 0 ? layout_kind(layout) : -1, s);
 #endif
@@ -1534,6 +1679,30 @@ int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hk
       break;
   }
   return launch_status("tp_decode_attention");
+}
+
+extern "C" {
+
+int32_t tp_decode_attention(const void* q, int64_t batch, int32_t hq, int32_t hkv,
+                            const tp_page_layout* layout, const tp_pages* pages, int32_t n_pages,
+                            const void* tail_k, const void* tail_v, int32_t tail_len,
+                            int64_t tail_stride, int64_t actual_seq_len, float scale,
+                            int32_t pages_per_split, void* workspace, size_t workspace_bytes,
+                            void* out, void* stream) {
+  return decode_attention_impl(q, batch, hq, hkv, layout, pages, n_pages, nullptr, tail_k, tail_v, tail_len,
+                               tail_stride, actual_seq_len, scale, pages_per_split, workspace, workspace_bytes, out,
+                               stream, false);
+}
+
+int32_t tp_decode_attention_qjl(const void* q, int64_t batch, int32_t hq, int32_t hkv,
+                                const tp_page_layout* layout, const tp_pages* pages, int32_t n_pages,
+                                const tp_qjl* qjl, const void* tail_k, const void* tail_v, int32_t tail_len,
+                                int64_t tail_stride, int64_t actual_seq_len, float scale,
+                                int32_t pages_per_split, void* workspace, size_t workspace_bytes,
+                                void* out, void* stream) {
+  return decode_attention_impl(q, batch, hq, hkv, layout, pages, n_pages, qjl, tail_k, tail_v, tail_len,
+                               tail_stride, actual_seq_len, scale, pages_per_split, workspace, workspace_bytes, out,
+                               stream, true);
 }
 
 }  // extern "C"

@@ -225,19 +225,27 @@ def _q16(q: torch.Tensor) -> torch.Tensor:
     return q.to(torch.float16).contiguous()
 
 
-def fused_qk(q: torch.Tensor, pageset: PageSet, scale: float) -> torch.Tensor:
-    """tp_fused_qk -> fp16 scores ``[B, H_q, S*64]``."""
+def fused_qk(q: torch.Tensor, pageset: PageSet, scale: float, qjl=None) -> torch.Tensor:
+    """tp_fused_qk -> fp16 scores ``[B, H_q, S*64]``; with ``qjl`` (a
+    ``qjl.QJLPages``) tp_fused_qk_qjl, which adds the QJL correction."""
     q16 = _q16(q)
     B, Hq, _ = q16.shape
     if B != pageset.B or Hq % pageset.H:
         raise ValueError(f"q heads {Hq} / batch {B} do not match kv pages {pageset.B}x{pageset.H}")
     scores = torch.empty((B, Hq, pageset.S * PAGE), dtype=torch.float16, device=q16.device)
     with on_device(q16.device):
-        st = lib().tp_fused_qk(
-            ptr(q16), B, Hq, pageset.H, ctypes.byref(pageset.layout), ctypes.byref(pageset.pages),
-            pageset.S, float(scale), ptr(scores), stream_handle(q16.device),
-        )
-    check(st, "tp_fused_qk")
+        if qjl is None:
+            st = lib().tp_fused_qk(
+                ptr(q16), B, Hq, pageset.H, ctypes.byref(pageset.layout), ctypes.byref(pageset.pages),
+                pageset.S, float(scale), ptr(scores), stream_handle(q16.device),
+            )
+        else:
+            qjl.check_against(pageset.B, pageset.H, pageset.S, Hq)
+            st = lib().tp_fused_qk_qjl(
+                ptr(q16), B, Hq, pageset.H, ctypes.byref(pageset.layout), ctypes.byref(pageset.pages),
+                pageset.S, ctypes.byref(qjl.desc), float(scale), ptr(scores), stream_handle(q16.device),
+            )
+    check(st, "tp_fused_qk_qjl" if qjl is not None else "tp_fused_qk")
     return scores
 
 
@@ -267,11 +275,13 @@ def decode_attention(
     num_kv_heads: Optional[int] = None,
     pages_per_split: int = 0,
     out: Optional[torch.Tensor] = None,
+    qjl=None,
 ) -> torch.Tensor:
     """tp_decode_attention -> fp16 ``[B, H_q, 128]``.
 
     ``tail_k``/``tail_v``: ``[B, H_kv, T_tail, 128]`` (T_tail < 64, any float
-    dtype; converted to fp16 as metal.py:744 does)."""
+    dtype; converted to fp16 as metal.py:744 does).  ``qjl`` (a
+    ``qjl.QJLPages`` of the pages): tp_decode_attention_qjl."""
     q16 = _q16(q)
     B, Hq, _ = q16.shape
     tail_len = 0 if tail_k is None else int(tail_k.shape[2])
@@ -300,15 +310,18 @@ def decode_attention(
             tail_stride = tail_len
     layout = pageset.layout if pageset is not None else _DEFAULT_LAYOUT
     pages = pageset.pages if pageset is not None else _NO_PAGES
+    if qjl is not None:
+        qjl.check_against(B, Hkv, n_pages, Hq)
     return _launch_decode(q16, Hkv, layout, pages, n_pages, tk, tv, tail_len, tail_stride, actual_seq_len, scale,
-                          pages_per_split, out)
+                          pages_per_split, out, qjl)
 
 
 _DEFAULT_LAYOUT = _lib.make_layout(False, 4, 4, 64)
 _NO_PAGES = TPPages()
 
 
-def _launch_decode(q16, Hkv, layout, pages, n_pages, tk, tv, tail_len, tail_stride, seq_len, scale, pps, out):
+def _launch_decode(q16, Hkv, layout, pages, n_pages, tk, tv, tail_len, tail_stride, seq_len, scale, pps, out,
+                   qjl=None):
     B, Hq, _ = q16.shape
     dev = q16.device
     if out is None:
@@ -318,12 +331,19 @@ def _launch_decode(q16, Hkv, layout, pages, n_pages, tk, tv, tail_len, tail_stri
     need = int(L.tp_decode_workspace_bytes(B, Hq, Hkv, n_pages, tail_len, pps))
     ws = _Workspace.get(dev, need)
     with on_device(dev):
-        st = L.tp_decode_attention(
-            ptr(q16), B, Hq, Hkv, ctypes.byref(layout), ctypes.byref(pages), n_pages,
-            ptr(tk), ptr(tv), tail_len, tail_stride, int(seq_len), float(scale), pps,
-            ws.data_ptr(), ws.numel(), ptr(out), stream_handle(dev),
-        )
-    check(st, "tp_decode_attention")
+        if qjl is None:
+            st = L.tp_decode_attention(
+                ptr(q16), B, Hq, Hkv, ctypes.byref(layout), ctypes.byref(pages), n_pages,
+                ptr(tk), ptr(tv), tail_len, tail_stride, int(seq_len), float(scale), pps,
+                ws.data_ptr(), ws.numel(), ptr(out), stream_handle(dev),
+            )
+        else:
+            st = L.tp_decode_attention_qjl(
+                ptr(q16), B, Hq, Hkv, ctypes.byref(layout), ctypes.byref(pages), n_pages, ctypes.byref(qjl.desc),
+                ptr(tk), ptr(tv), tail_len, tail_stride, int(seq_len), float(scale), pps,
+                ws.data_ptr(), ws.numel(), ptr(out), stream_handle(dev),
+            )
+    check(st, "tp_decode_attention_qjl" if qjl is not None else "tp_decode_attention")
     return out
 
 
