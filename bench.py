@@ -127,8 +127,23 @@ def run_gpu(args, layout):
     stream = torch.cuda.current_stream(dev).cuda_stream
     fn = L.tp_decode_attention
     calls = []
-    for c in caches:
+    for i, c in enumerate(caches):
         ps = c["pages"]
+        if getattr(args, "qjl", False):
+            # Synthetic sketches of the pages' residuals (random bits and norms:
+            # the kernel's work does not depend on their values) and of q.
+            from turbopolar_amd.qjl import QJLPages, QJLPayload
+
+            g = torch.Generator(device=dev).manual_seed(77 + i)
+            signs = torch.randint(0, 256, (1, args.hkv, n_pages, 64, 8), generator=g, device=dev, dtype=torch.uint8)
+            norms = (torch.rand((1, args.hkv, n_pages, 64), generator=g, device=dev) * 0.1).half()
+            qsig = torch.randint(0, 256, (1, args.hq, 8), generator=g, device=dev, dtype=torch.uint8)
+            c["qjl"] = QJLPages(QJLPayload(signs, norms, 64, 42, (1, args.hkv, n_pages, 64, 128)), qsig)
+            fn = L.tp_decode_attention_qjl
+            calls.append((c["q"].data_ptr(), 1, args.hq, args.hkv, ctypes.byref(ps.layout), ctypes.byref(ps.pages),
+                          n_pages, ctypes.byref(c["qjl"].desc), None, None, 0, 0, c["seq"], scale, pps,
+                          ws.data_ptr(), need, c["out"].data_ptr(), stream))
+            continue
         calls.append((c["q"].data_ptr(), 1, args.hq, args.hkv, ctypes.byref(ps.layout), ctypes.byref(ps.pages),
                       n_pages, None, None, 0, 0, c["seq"], scale, pps, ws.data_ptr(), need,
                       c["out"].data_ptr(), stream))
@@ -1103,6 +1118,8 @@ def main():
                     help="K distribution (default: outlier for decode, loguniform for layers)")
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--graph", action="store_true", help="layers: replay the step as one HIP graph")
+    ap.add_argument("--qjl", action="store_true",
+                    help="decode: tp_decode_attention_qjl (QJL correction on every page token; synthetic sketches)")
     ap.add_argument("--variant", choices=sorted(VARIANTS), default=None,
                     help="decode: run a decode-kernel variant of the measurement library (release: agent-scope "
                          "release fence before the split ticket; valu: QK and PV on the VALU; mfma: the product "
@@ -1318,6 +1335,8 @@ def main():
         return
     n_pages = args.context // 64
     step_bytes = algorithmic_bytes(args.hq, args.hkv, n_pages, layout)
+    if args.qjl:
+        step_bytes += args.hkv * n_pages * 64 * (8 + 2) + args.hq * 8  # sketches, residual norms, query sketches
     if not args.rotate:
         args.rotate = max(4, int(np.ceil(320e6 / step_bytes)))
 
@@ -1336,7 +1355,7 @@ def main():
     us = ms * 1e3
     gbps = step_bytes / (ms * 1e-3) / 1e9
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not args.qjl:
         cb = cpu_baseline(args, layout, res["caches"], args.cpu_budget)
         cpu = {"value": round(cb["us"], 1), "unit": "us/step", "cores": cb["cores"], "kind": "port",
                "sample": f"{cb['runs']} full decode steps of the {args.hq}-head/{args.hkv}-kv-head {args.context}-token "
@@ -1352,8 +1371,12 @@ def main():
     if os.path.exists(tpath) and args.context == 32768 and args.hq == 32 and args.hkv == 8:
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
+    metric = METRIC
+    if (args.context, args.hq, args.hkv) != (32768, 32, 8):
+        metric = (f"decode-attn µs/step + achieved HBM GB/s (% peak), {args.hq} q / {args.hkv} kv heads, "
+                  f"{args.context} ctx")
     line = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(us, 3),
         "unit": "us/step",
         "n_gpus": 1,
@@ -1387,6 +1410,11 @@ def main():
     }
     if args.variant is not None:
         line["kernel_variant"] = f"{args.variant} (measurement library: phase stamps compiled in)"
+    if args.qjl:
+        line["metric"] = "decode-attn with QJL correction µs/step + achieved HBM GB/s, Llama-3-8B shape"
+        line["config"]["workload"] += " + QJL (tp_decode_attention_qjl, 64-bit sketches, synthetic)"
+        line["cpu_baseline"] = None
+        line["roofline"]["traffic"] = None
     print(json.dumps(line))
 
 
