@@ -31,7 +31,7 @@ import numpy as np
 
 HBM_PEAK_GBPS = 8000.0
 # Decode-kernel variants of the measurement library (tp_measure_set_decode_variant).
-VARIANTS = {"mfma": 0, "release": 1, "valu": 2, "valu+release": 3}
+VARIANTS = {"mfma": 0, "release": 1, "valu": 2, "valu+release": 3, "no-acquire": 4}
 METRIC = "decode-attn µs/step + achieved HBM GB/s (% peak), Llama-3-8B shape, 32k ctx"
 LAYOUTS = {"default": (False, 4, 4, 64), "fast": (True, 4, 8, 0)}
 
@@ -897,6 +897,11 @@ def run_timeline(args, layout) -> dict:
     if _lib._lib is not None:
         raise RuntimeError("the timeline workload must load its library first")
     _lib.LIB_PATH = build.TIMELINE_LIB_PATH
+    if args.variant is not None:
+        fn = _lib.lib().tp_measure_set_decode_variant
+        fn.restype, fn.argtypes = ctypes.c_int32, [ctypes.c_int32]
+        if fn(VARIANTS[args.variant]) != 0:
+            raise RuntimeError(f"variant {args.variant} rejected")
     if not args.rotate:
         args.rotate = max(4, int(np.ceil(320e6 / algorithmic_bytes(args.hq, args.hkv, args.context // 64, layout))))
     dev = torch.device("cuda:0")
@@ -952,7 +957,8 @@ def run_timeline(args, layout) -> dict:
 PAGE_FIELDS = {"default": (8192, 1024, 1024, 8192, 512), "fast": (4096, 2, 4096, 8192, 512)}
 # Launch shapes of the streaming-read sweep (grid, threads, unroll); the
 # decode kernel's own grid is added in front.
-STREAM_SHAPES = ((2048, 512, 8), (4096, 512, 8), (8192, 512, 8), (8192, 256, 8), (4096, 1024, 4))
+STREAM_SHAPES = ((256, 512, 16), (512, 256, 16), (256, 1024, 8), (2048, 512, 8), (4096, 512, 8), (8192, 512, 8),
+                 (8192, 256, 8), (4096, 1024, 4))
 
 
 def run_stream(args, layout) -> dict:
@@ -1122,8 +1128,8 @@ def main():
                     help="decode: tp_decode_attention_qjl (QJL correction on every page token; synthetic sketches)")
     ap.add_argument("--variant", choices=sorted(VARIANTS), default=None,
                     help="decode: run a decode-kernel variant of the measurement library (release: agent-scope "
-                         "release fence before the split ticket; valu: QK and PV on the VALU; mfma: the product "
-                         "kernel as built there)")
+                         "release fence before the split ticket; valu: QK and PV on the VALU; no-acquire: without "
+                         "the combining workgroup's acquire fence; mfma: the product kernel as built there)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)

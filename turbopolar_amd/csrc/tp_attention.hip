@@ -759,11 +759,15 @@ struct AttnShared {
 // with a relaxed agent-scope atomic; the workgroup that draws the last ticket
 // issues an agent-scope acquire fence (invalidating its XCD's non-coherent
 // cache lines) before the barrier after which it reads the records.
-template <int WAVES, bool REL, class Merge>
+// End-phase variants of the measurement library (0 in the product).
+constexpr int kFlRelease = 1;    // agent-scope release fence before the ticket
+constexpr int kFlNoAcquire = 2;  // no acquire fence in the combining workgroup
+
+template <int WAVES, int FL, class Merge>
 __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int tid, int b, int kv, int h0, int nh,
                                               int64_t bkv, int hb, int split);
 
-template <int WAVES, bool REL = false, class Merge>
+template <int WAVES, int FL = 0, class Merge>
 __device__ __forceinline__ void finish_unit(Merge& sh, const AttnArgs& a, int wave, int tid, float m_run, float l_run,
                                             const float4v* acc, int b, int kv, int h0, int nh, int64_t bkv, int hb,
                                             int split) {
@@ -786,13 +790,12 @@ __device__ __forceinline__ void finish_unit(Merge& sh, const AttnArgs& a, int wa
       *reinterpret_cast<float4v*>(arow + 4 * q) = float4v{acc[j0][i], acc[j0 + 1][i], acc[j0 + 2][i], acc[j0 + 3][i]};
     }
   }
-  finish_merged<WAVES, REL>(sh, a, tid, b, kv, h0, nh, bkv, hb, split);
+  finish_merged<WAVES, FL>(sh, a, tid, b, kv, h0, nh, bkv, hb, split);
 }
 
 // The rest of the end phase once every wave's state (sh.ml[w][h], sh.acc[w]
-// rows of the live heads) is in LDS.  REL (measurement builds only): an
-// agent-scope release fence before the ticket.
-template <int WAVES, bool REL, class Merge>
+// rows of the live heads) is in LDS.  FL: end-phase variant flags (above).
+template <int WAVES, int FL, class Merge>
 __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int tid, int b, int kv, int h0, int nh,
                                               int64_t bkv, int hb, int split) {
   lds_barrier();
@@ -824,10 +827,12 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
   __syncthreads();
   TP_STAMP(54);
   if (tid == 0) {
-    if constexpr (REL) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if constexpr ((FL & kFlRelease) != 0) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     const uint32_t prev = __hip_atomic_fetch_add(a.counters + unit * a.counter_stride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = prev == (uint32_t)(S - 1);
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if constexpr ((FL & kFlNoAcquire) == 0) {
+      if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
     sh.last = last;
   }
   __syncthreads();
@@ -894,7 +899,7 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
 
 // ---- decode attention kernel ---------------------------------------------------
 
-template <int KIND, int WAVES, bool REL = false, bool QJL = false>
+template <int KIND, int WAVES, int FL = 0, bool QJL = false>
 __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a) {
   // The fold maps 512 threads onto up to 16 heads x 128 dims at 1, 2 or 4 dims
   // per thread, and the combine sizes its split groups for 512 threads.
@@ -1016,15 +1021,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   }
 
   TP_STAMP(52);
-  finish_unit<WAVES, REL>(sh, a, wave, tid, m_run, l_run, acc, b, kv, h0, nh, bkv, hb, split);
+  finish_unit<WAVES, FL>(sh, a, wave, tid, m_run, l_run, acc, b, kv, h0, nh, bkv, hb, split);
 }
 
 #ifdef TP_TIMELINE
 // ---- measurement variants ------------------------------------------------------------
 //
 // Built into the measurement library only (never into the product library):
-// the decode kernel above with an agent-scope release fence before the split
-// ticket (REL), and decode_attention_valu_kernel, the default-layout kernel
+// the decode kernel above with its end-phase variant flags (kFlRelease,
+// kFlNoAcquire), and decode_attention_valu_kernel, the default-layout kernel
 // with QK and PV on the VALU (packed fp16 dot products v_dot2_f32_f16, fp32
 // accumulation) instead of MFMA, for blocks of exactly NHV = 4 or 8 query
 // heads and no dense tail.  Page loads, K decode, V dequantisation, the
@@ -1302,7 +1307,7 @@ __global__ __launch_bounds__(512) void decode_attention_valu_kernel(AttnArgs a) 
       *reinterpret_cast<float4v*>(row + 4) = float4v{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
     }
   }
-  finish_merged<WAVES, REL>(sh, a, tid, b, kv, h0, NHV, bkv, hb, split);
+  finish_merged<WAVES, REL ? kFlRelease : 0>(sh, a, tid, b, kv, h0, NHV, bkv, hb, split);
 }
 #endif  // TP_TIMELINE
 
@@ -1540,11 +1545,12 @@ int32_t tp_fused_qk_qjl(const void* q, int64_t batch, int32_t hq, int32_t hkv, c
 #ifdef TP_TIMELINE
 // Measurement library only: the decode-kernel variant tp_decode_attention
 // launches (0: the product kernel; 1: + agent-scope release fence before the
-// split ticket; 2: QK and PV on the VALU; 3: 2 + the release fence).
+// split ticket; 2: QK and PV on the VALU; 3: 2 + the release fence; 4: the
+// product kernel without the combining workgroup's acquire fence).
 static int32_t g_measure_variant = 0;
 
 int32_t tp_measure_set_decode_variant(int32_t variant) {
-  if (variant < 0 || variant > 3) return TP_ERR_INVALID;
+  if (variant < 0 || variant > 4) return TP_ERR_INVALID;
   g_measure_variant = variant;
   return TP_OK;
 }
@@ -1553,11 +1559,19 @@ static int32_t launch_measure_variant(const AttnArgs& a, dim3 grid, int kind, hi
   const dim3 block(kDecodeWaves * 64);
   if (g_measure_variant == 1) {
     switch (kind) {
-      case kKindDefault: hipLaunchKernelGGL((decode_attention_kernel<kKindDefault, kDecodeWaves, true>), grid, block, 0, s, a); break;
-      case kKindFast: hipLaunchKernelGGL((decode_attention_kernel<kKindFast, kDecodeWaves, true>), grid, block, 0, s, a); break;
-      default: hipLaunchKernelGGL((decode_attention_kernel<kKindGeneric, kDecodeWaves, true>), grid, block, 0, s, a); break;
+      case kKindDefault: hipLaunchKernelGGL((decode_attention_kernel<kKindDefault, kDecodeWaves, kFlRelease>), grid, block, 0, s, a); break;
+      case kKindFast: hipLaunchKernelGGL((decode_attention_kernel<kKindFast, kDecodeWaves, kFlRelease>), grid, block, 0, s, a); break;
+      default: hipLaunchKernelGGL((decode_attention_kernel<kKindGeneric, kDecodeWaves, kFlRelease>), grid, block, 0, s, a); break;
     }
     return launch_status("tp_decode_attention (release variant)");
+  }
+  if (g_measure_variant == 4) {
+    switch (kind) {
+      case kKindDefault: hipLaunchKernelGGL((decode_attention_kernel<kKindDefault, kDecodeWaves, kFlNoAcquire>), grid, block, 0, s, a); break;
+      case kKindFast: hipLaunchKernelGGL((decode_attention_kernel<kKindFast, kDecodeWaves, kFlNoAcquire>), grid, block, 0, s, a); break;
+      default: hipLaunchKernelGGL((decode_attention_kernel<kKindGeneric, kDecodeWaves, kFlNoAcquire>), grid, block, 0, s, a); break;
+    }
+    return launch_status("tp_decode_attention (no-acquire variant)");
   }
   if (kind != kKindDefault || a.tail_len != 0 || a.head_blocks != 1 || (a.g != 4 && a.g != 8)) {
     set_error("the VALU variant takes the default layout, no tail and 4 or 8 query heads per kv head");
@@ -1653,13 +1667,13 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
     const dim3 block(kDecodeWaves * 64);
     switch (n_pages > 0 ? layout_kind(layout) : (int)kKindGeneric) {
       case kKindDefault:
-        hipLaunchKernelGGL((decode_attention_kernel<kKindDefault, kDecodeWaves, false, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((decode_attention_kernel<kKindDefault, kDecodeWaves, 0, true>), grid, block, 0, s, a);
         break;
       case kKindFast:
-        hipLaunchKernelGGL((decode_attention_kernel<kKindFast, kDecodeWaves, false, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((decode_attention_kernel<kKindFast, kDecodeWaves, 0, true>), grid, block, 0, s, a);
         break;
       default:
-        hipLaunchKernelGGL((decode_attention_kernel<kKindGeneric, kDecodeWaves, false, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((decode_attention_kernel<kKindGeneric, kDecodeWaves, 0, true>), grid, block, 0, s, a);
         break;
     }
     return launch_status("tp_decode_attention_qjl");

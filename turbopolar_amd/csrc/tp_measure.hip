@@ -54,8 +54,8 @@ __global__ __launch_bounds__(1024) void stream_read_kernel(Segments s, uint32_t*
 }  // namespace
 
 // Reads buffers[0..count) (byte sizes sizes[], each a multiple of 16 and
-// 16-byte aligned) with grid x threads workgroups, unroll 4 or 8.  sink: at
-// least grid words of device memory.  Returns 0, or -1 for arguments outside
+// 16-byte aligned) with grid x threads workgroups, unroll 4, 8 or 16.  sink:
+// at least grid words of device memory.  Returns 0, or -1 for arguments outside
 // these limits (nothing is launched then).
 extern "C" int32_t tp_measure_stream_read(const void* const* buffers, const int64_t* sizes, int32_t count,
                                           int32_t grid, int32_t threads, int32_t unroll, uint32_t* sink,
@@ -74,6 +74,8 @@ extern "C" int32_t tp_measure_stream_read(const void* const* buffers, const int6
     hipLaunchKernelGGL(stream_read_kernel<4>, dim3(grid), dim3(threads), 0, stream, s, sink);
   else if (unroll == 8)
     hipLaunchKernelGGL(stream_read_kernel<8>, dim3(grid), dim3(threads), 0, stream, s, sink);
+  else if (unroll == 16)
+    hipLaunchKernelGGL(stream_read_kernel<16>, dim3(grid), dim3(threads), 0, stream, s, sink);
   else
     return -1;
   return hipGetLastError() == hipSuccess ? 0 : -1;
