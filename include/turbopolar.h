@@ -120,7 +120,8 @@ int32_t tp_encode_pages(const void* k, const void* v, int32_t in_dtype, int64_t 
  * Fused dequant . QK scores over all n_pages*64 page slots (no masking).
  * Replaces MetalKernelBridge.execute_fused_qk (metal.py:494-530) and its kernel
  * tqpolar_fused_dequant_qk (tqpolar_fused_qk.metal:4-100).
- * q: fp16 [batch][hq][128]; scores: fp16 [batch][hq][n_pages*64].
+ * q: fp16 [batch][hq][128]; scores: fp16 [batch][hq][n_pages*64], 16-byte
+ * aligned.
  * scale is applied in fp32 (the shim passes fp16(attention_scale), as
  * metal.py:518 does).
  */

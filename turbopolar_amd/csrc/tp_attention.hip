@@ -1313,10 +1313,21 @@ __global__ __launch_bounds__(512) void decode_attention_valu_kernel(AttnArgs a) 
 
 // ---- standalone fused QK -----------------------------------------------------------
 
+// Scores of one page leave through LDS: each wave writes its [16 heads][64
+// tokens] fp16 block (row stride 72 halves) and reads it back as 16-byte
+// chunks, eight lanes per head row, so every global store instruction writes
+// whole 128-byte rows instead of 8-byte pieces of 16 rows.  One page per
+// wave, eight waves per workgroup (measured against four and two: 8 is the
+// fastest, by 0.05 us on the default layout and 0.25 us on the fast one at
+// 512 pages x 8 kv heads).
+constexpr int kQkRow = 72;  // halves per staged head row
+constexpr int kQkWaves = 8;
+
 template <int KIND, bool QJL = false>
-__global__ __launch_bounds__(256) void fused_qk_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kQkWaves * 64) void fused_qk_kernel(AttnArgs a) {
   __shared__ Lut lut;
   __shared__ float qjl_sin[QJL ? kQjlBits + 1 : 1];
+  __shared__ uint4 stage[kQkWaves][16 * kQkRow / 8];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
@@ -1332,10 +1343,10 @@ __global__ __launch_bounds__(256) void fused_qk_kernel(AttnArgs a) {
   load_q(a, b, kv, h0, nh, l16, l4, qb);
   // The page's K loads go out before the table build and the barrier (a wave
   // past the last page reloads the last page and leaves after the barrier).
-  const int page = blockIdx.x * 4 + wave;
+  const int page = blockIdx.x * kQkWaves + wave;
   KRegs<KIND> kr;
   load_k<KIND>(a, bkv * a.capacity + min(page, a.n_pages - 1), l16, l4, kr);
-  build_lut<KIND>(lut, a, tid);
+  if (tid < 256) build_lut<KIND>(lut, a, tid);
   uint64_t qsig = 0;
   float qnorm = 0.0f;
   if constexpr (QJL) {
@@ -1347,14 +1358,25 @@ __global__ __launch_bounds__(256) void fused_qk_kernel(AttnArgs a) {
   float4v s[4];
   qk_regs<KIND>(a, lut, kr, qb, l16, l4, s);
   if constexpr (QJL) qjl_correct(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
-  if (l16 >= nh) return;
-  const int64_t hq_idx = (int64_t)b * a.hq + (int64_t)kv * a.g + h0 + l16;
-  uint16_t* srow = a.scores + hq_idx * ((int64_t)a.n_pages * kPageTokens) + (int64_t)page * kPageTokens + 4 * l4;
+  uint16_t* st = reinterpret_cast<uint16_t*>(&stage[wave][0]);
+  if (l16 < nh) {
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const uint32_t w0 = (uint32_t)f2h(s[mt][0] * a.scale) | ((uint32_t)f2h(s[mt][1] * a.scale) << 16);
-    const uint32_t w1 = (uint32_t)f2h(s[mt][2] * a.scale) | ((uint32_t)f2h(s[mt][3] * a.scale) << 16);
-    *reinterpret_cast<uint2*>(srow + 16 * mt) = make_uint2(w0, w1);
+    for (int mt = 0; mt < 4; ++mt) {
+      const uint32_t w0 = (uint32_t)f2h(s[mt][0] * a.scale) | ((uint32_t)f2h(s[mt][1] * a.scale) << 16);
+      const uint32_t w1 = (uint32_t)f2h(s[mt][2] * a.scale) | ((uint32_t)f2h(s[mt][3] * a.scale) << 16);
+      *reinterpret_cast<uint2*>(st + l16 * kQkRow + 16 * mt + 4 * l4) = make_uint2(w0, w1);
+    }
+  }
+  wave_lds_sync();
+  const int64_t row0 = ((int64_t)b * a.hq + (int64_t)kv * a.g + h0) * ((int64_t)a.n_pages * kPageTokens) +
+                       (int64_t)page * kPageTokens;
+#pragma unroll
+  for (int r0 = 0; r0 < 16; r0 += 8) {
+    const int h = r0 + (lane >> 3);
+    const int c = lane & 7;
+    if (h < nh)
+      *reinterpret_cast<uint4*>(a.scores + row0 + (int64_t)h * a.n_pages * kPageTokens + 8 * c) =
+          *reinterpret_cast<const uint4*>(st + h * kQkRow + 8 * c);
   }
 }
 
@@ -1476,18 +1498,18 @@ int32_t tp_fused_qk(const void* q, int64_t batch, int32_t hq, int32_t hkv,
   AttnArgs a{};
   if (!fill_common(a, q, batch, hq, hkv, layout, pages, n_pages, false)) return TP_ERR_INVALID;
   if (n_pages == 0) return TP_OK;
-  if (!scores || ((uintptr_t)scores & 7u)) {
-    set_error("scores must be a non-NULL 8-byte aligned buffer");
+  if (!scores || ((uintptr_t)scores & 15u)) {
+    set_error("scores must be a non-NULL 16-byte aligned buffer");
     return TP_ERR_INVALID;
   }
   a.scores = static_cast<uint16_t*>(scores);
   a.scale = scale;
-  const dim3 grid((unsigned)((n_pages + 3) / 4), (unsigned)(batch * hkv), (unsigned)a.head_blocks);
+  const dim3 grid((unsigned)((n_pages + kQkWaves - 1) / kQkWaves), (unsigned)(batch * hkv), (unsigned)a.head_blocks);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (layout_kind(layout)) {
-    case kKindDefault: hipLaunchKernelGGL(fused_qk_kernel<kKindDefault>, grid, dim3(256), 0, s, a); break;
-    case kKindFast: hipLaunchKernelGGL(fused_qk_kernel<kKindFast>, grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL(fused_qk_kernel<kKindGeneric>, grid, dim3(256), 0, s, a); break;
+    case kKindDefault: hipLaunchKernelGGL(fused_qk_kernel<kKindDefault>, grid, dim3(kQkWaves * 64), 0, s, a); break;
+    case kKindFast: hipLaunchKernelGGL(fused_qk_kernel<kKindFast>, grid, dim3(kQkWaves * 64), 0, s, a); break;
+    default: hipLaunchKernelGGL(fused_qk_kernel<kKindGeneric>, grid, dim3(kQkWaves * 64), 0, s, a); break;
   }
   return launch_status("tp_fused_qk");
 }
@@ -1526,18 +1548,18 @@ int32_t tp_fused_qk_qjl(const void* q, int64_t batch, int32_t hq, int32_t hkv, c
   if (!fill_common(a, q, batch, hq, hkv, layout, pages, n_pages, false)) return TP_ERR_INVALID;
   if (!fill_qjl(a, qjl, n_pages)) return TP_ERR_INVALID;
   if (n_pages == 0) return TP_OK;
-  if (!scores || ((uintptr_t)scores & 7u)) {
-    set_error("scores must be a non-NULL 8-byte aligned buffer");
+  if (!scores || ((uintptr_t)scores & 15u)) {
+    set_error("scores must be a non-NULL 16-byte aligned buffer");
     return TP_ERR_INVALID;
   }
   a.scores = static_cast<uint16_t*>(scores);
   a.scale = scale;
-  const dim3 grid((unsigned)((n_pages + 3) / 4), (unsigned)(batch * hkv), (unsigned)a.head_blocks);
+  const dim3 grid((unsigned)((n_pages + kQkWaves - 1) / kQkWaves), (unsigned)(batch * hkv), (unsigned)a.head_blocks);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (layout_kind(layout)) {
-    case kKindDefault: hipLaunchKernelGGL((fused_qk_kernel<kKindDefault, true>), grid, dim3(256), 0, s, a); break;
-    case kKindFast: hipLaunchKernelGGL((fused_qk_kernel<kKindFast, true>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((fused_qk_kernel<kKindGeneric, true>), grid, dim3(256), 0, s, a); break;
+    case kKindDefault: hipLaunchKernelGGL((fused_qk_kernel<kKindDefault, true>), grid, dim3(kQkWaves * 64), 0, s, a); break;
+    case kKindFast: hipLaunchKernelGGL((fused_qk_kernel<kKindFast, true>), grid, dim3(kQkWaves * 64), 0, s, a); break;
+    default: hipLaunchKernelGGL((fused_qk_kernel<kKindGeneric, true>), grid, dim3(kQkWaves * 64), 0, s, a); break;
   }
   return launch_status("tp_fused_qk_qjl");
 }

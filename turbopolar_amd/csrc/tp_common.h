@@ -240,6 +240,15 @@ __host__ __device__ inline int packed_row_bytes(int n, int bits) {
 
 // Workgroup barrier that orders LDS only: global loads already in flight stay
 // in flight (a full __syncthreads() would wait for them).
+// Orders one wave's LDS accesses against its other lanes' (the wave's own
+// LDS operations complete at the workgroup-scope fences); no other wave takes
+// part, so waves may run different iteration counts around it.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();

@@ -19,15 +19,6 @@ namespace tp {
 constexpr int kQjlMaxDim = 256;
 constexpr int kQjlMaxProj = 256;
 
-// Orders one wave's LDS accesses: the workgroup-scope fences wait for the
-// wave's own LDS operations; no other wave takes part (the waves of a
-// workgroup run different numbers of rows, so no workgroup barrier).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 template <bool F32IN>
 __global__ __launch_bounds__(256) void qjl_sketch_kernel(const void* e, int64_t rows, int32_t dim, const float* w,
                                                          int32_t proj, uint8_t* packed, uint16_t* norms) {
