@@ -959,16 +959,22 @@ PAGE_FIELDS = {"default": (8192, 1024, 1024, 8192, 512), "fast": (4096, 2, 4096,
 # decode kernel's own grid is added in front.
 STREAM_SHAPES = ((256, 512, 16), (512, 256, 16), (256, 1024, 8), (2048, 512, 8), (4096, 512, 8), (8192, 512, 8),
                  (8192, 256, 8), (4096, 1024, 4))
+# Launch shapes of the dynamic sweep (tp_measure_stream_read_dynamic: every
+# wave claims U-KiB chunks from a counter); the decode grid is added in front.
+STREAM_DYNAMIC_SHAPES = ((256, 512, 4), (256, 512, 16), (512, 512, 8), (512, 256, 8), (1024, 256, 8), (1024, 512, 8),
+                         (2048, 256, 8))
 
 
 def run_stream(args, layout) -> dict:
     """The streaming-read ceiling: tp_measure_stream_read (measurement
     library) reads buffers of exactly the page fields one decode step reads
     (same sizes, same 16-byte non-temporal loads), with nothing computed, at
-    the decode kernel's grid and at the launch shapes of STREAM_SHAPES.
-    Buffers rotate over > 320 MB as in the headline line, so reads come
-    from HBM; each shape is timed over ``steps`` back-to-back launches with
-    HIP events on the launch stream."""
+    the decode kernel's grid and at the launch shapes of STREAM_SHAPES, then
+    with the chunks claimed dynamically by every wave
+    (tp_measure_stream_read_dynamic) at the decode grid and at
+    STREAM_DYNAMIC_SHAPES.  Buffers rotate over > 320 MB as in the headline
+    line, so reads come from HBM; each shape is timed over ``steps``
+    back-to-back launches with HIP events on the launch stream."""
     import torch
 
     from turbopolar_amd import _lib, build
@@ -981,6 +987,11 @@ def run_stream(args, layout) -> dict:
     fn.restype = ctypes.c_int32
     fn.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32,
                    ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    fn_dyn = L.tp_measure_stream_read_dynamic
+    fn_dyn.restype = ctypes.c_int32
+    fn_dyn.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int64), ctypes.c_int32,
+                       ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_uint64,
+                       ctypes.POINTER(ctypes.c_uint64), ctypes.c_void_p, ctypes.c_void_p]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     n_pages = args.context // 64
@@ -999,14 +1010,23 @@ def run_stream(args, layout) -> dict:
     units = args.hkv * ((args.hq // args.hkv + 15) // 16)
     decode_grid = units * ((n_pages + pps - 1) // pps)
     shapes = [(decode_grid, 512, 8)] + [s for s in STREAM_SHAPES if s != (decode_grid, 512, 8)]
-    sink = torch.zeros(max(s[0] for s in shapes), dtype=torch.int32, device=dev)
+    dyn_shapes = [(decode_grid, 512, 8)] + [s for s in STREAM_DYNAMIC_SHAPES if s != (decode_grid, 512, 8)]
+    sink = torch.zeros(max(s[0] for s in shapes + dyn_shapes), dtype=torch.int32, device=dev)
+    counter = torch.zeros(1, dtype=torch.int64, device=dev)
+    base = ctypes.c_uint64(0)
     stream = torch.cuda.current_stream(dev).cuda_stream
     results = []
-    for grid, threads, unroll in shapes:
+    for dynamic, grid, threads, unroll in [(False, *x) for x in shapes] + [(True, *x) for x in dyn_shapes]:
         def launch(i):
             _, ptrs, sizes = sets[i % rotate]
-            rc = fn(ptrs, sizes, len(fields), grid, threads, unroll, ctypes.c_void_p(sink.data_ptr()),
-                    ctypes.c_void_p(stream))
+            if dynamic:
+                nxt = ctypes.c_uint64(0)
+                rc = fn_dyn(ptrs, sizes, len(fields), grid, threads, unroll, ctypes.c_void_p(counter.data_ptr()),
+                            base, ctypes.byref(nxt), ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream))
+                base.value = nxt.value
+            else:
+                rc = fn(ptrs, sizes, len(fields), grid, threads, unroll, ctypes.c_void_p(sink.data_ptr()),
+                        ctypes.c_void_p(stream))
             if rc != 0:
                 raise RuntimeError("tp_measure_stream_read rejected its arguments")
 
@@ -1021,7 +1041,8 @@ def run_stream(args, layout) -> dict:
         t1.record()
         torch.cuda.synchronize()
         us = t0.elapsed_time(t1) / args.steps * 1e3
-        results.append({"grid": grid, "threads": threads, "unroll": unroll, "us": round(us, 3),
+        results.append({"grid": grid, "threads": threads, "unroll": unroll,
+                        "claim": "dynamic" if dynamic else "static", "us": round(us, 3),
                         "GBps": round(total / (us * 1e-6) / 1e9, 1)})
     return {"bytes": total, "fields": fields, "rotate": rotate, "sweep": results, "decode_grid": decode_grid}
 
@@ -1230,7 +1251,10 @@ def main():
                        "layout": args.layout, "field_bytes": r["fields"], "best_shape": best},
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
-            "decode_grid": next(e for e in r["sweep"] if e["grid"] == r["decode_grid"] and e["threads"] == 512),
+            "decode_grid": next(e for e in r["sweep"] if e["grid"] == r["decode_grid"] and e["threads"] == 512
+                                and e["unroll"] == 8 and e["claim"] == "static"),
+            "decode_grid_dynamic": next(e for e in r["sweep"] if e["grid"] == r["decode_grid"] and e["threads"] == 512
+                                        and e["unroll"] == 8 and e["claim"] == "dynamic"),
             "sweep": r["sweep"],
         }))
         return
