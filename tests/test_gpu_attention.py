@@ -99,7 +99,7 @@ CASES = [
     ("default", 6, 2, 3, 5, 1),  # GQA 3: 3 live head rows in the fold; combine: 96 live items of 128, 4 split groups
     ("default", 12, 2, 4, 0, 1),  # GQA 6: combine items in 192 of 256 slots, 2 split groups
     ("default", 24, 2, 3, 9, 1),  # GQA 12: 384 combine items, 1 split group
-    ("default", 2, 2, 600, 3, 1),  # 600 splits of one head: 16 split groups, chunked reloads
+    ("default", 2, 2, 600, 3, 1),  # 600 splits of one head: two-tier combine, 38 groups
 ]
 
 
@@ -295,8 +295,8 @@ def test_split_invariance(device):
 
 
 def test_max_splits_combine(device):
-    """1536 one-page splits of 4 heads: the combine folds 384 records per
-    thread in chunks of 8 reloads."""
+    """1536 one-page splits of 4 heads: two-tier combine of 96 groups of 16
+    (the last combine folds 96 group records)."""
     print("[attn-maxsplits] S=1536 pps=1", flush=True)
     block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], 8, 2, 1536, 9, seed=21)
     seq = 1536 * PAGE + 9
@@ -304,12 +304,61 @@ def test_max_splits_combine(device):
     check(out, oracle_out(host, tk, tv, q, seq), "max splits")
 
 
+TIERED = [
+    # layout, hq, hkv, S pages, tail, pages_per_split, B, tokens masked at the end
+    ("default", 4, 1, 65, 0, 1, 1, 0),  # 5 groups of 16, 16, 16, 16, 1 splits
+    ("default", 4, 1, 256, 0, 1, 1, 0),  # 16 full groups
+    ("default", 8, 1, 300, 37, 1, 1, 0),  # 19 groups, the last of 12, with a tail
+    ("default", 16, 2, 97, 5, 1, 2, 0),  # batch 2, GQA 8: 4 units of 7 groups
+    ("default", 8, 1, 130, 11, 1, 1, 200),  # masked suffix: the last group (splits 128, 129) holds no live token
+    ("fast", 32, 8, 80, 0, 1, 1, 0),  # 8 units of 5 groups
+    ("default", 24, 2, 70, 9, 1, 1, 0),  # GQA 12: 384 combine items per group record
+]
+
+
+@pytest.mark.parametrize("layout_name,hq,hkv,S,tail,pps,B,drop", TIERED)
+def test_two_tier_combine(device, layout_name, hq, hkv, S, tail, pps, B, drop):
+    """More than 64 splits per (b, kv head, head block): groups of 16 splits
+    combine into group records, and the last group combines the groups."""
+    print(f"[attn-tiers] layout={layout_name} hq={hq} hkv={hkv} S={S} tail={tail} pps={pps} B={B} drop={drop}",
+          flush=True)
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS[layout_name], hq, hkv, S, tail, seed=90 + S, B=B)
+    seq = S * PAGE + tail - drop
+    out = run_gpu(device, block, qv, tk, tv, q, seq, pps)
+    check(out, oracle_out(host, tk, tv, q, seq), f"tiers S={S}")
+
+
+def test_two_tier_launches_repeat_exactly(device):
+    """200 launches alternating a two-tier and a one-tier shape on one
+    workspace: every output is bit-identical to that shape's first output, so
+    the group tickets, the group records and both counter resets are
+    race-free."""
+    cases = []
+    for hq, hkv, S, seed in ((8, 1, 100, 3), (32, 8, 24, 4)):
+        block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], hq, hkv, S, 7, seed=seed)
+        cases.append((PageSet(block, qv), torch.from_numpy(q).to(device), torch.from_numpy(tk).to(device),
+                      torch.from_numpy(tv).to(device), S * PAGE + 7, host, tk, tv, q))
+    refs = [kernels.decode_attention(c[1], c[0], c[2], c[3], c[4], SCALE16, pages_per_split=1).clone()
+            for c in cases]
+    torch.cuda.synchronize()
+    for i, c in enumerate(cases):
+        check(refs[i].float().cpu().numpy(), oracle_out(c[5], c[6], c[7], c[8], c[4]), f"case {i}")
+    bad = torch.zeros((), dtype=torch.int64, device=device)
+    for it in range(200):
+        c = cases[it % 2]
+        out = kernels.decode_attention(c[1], c[0], c[2], c[3], c[4], SCALE16, pages_per_split=1)
+        bad += (out != refs[it % 2]).sum()
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 0
+
+
 def test_workspace_shared_across_shapes(device):
     """One workspace serves calls whose unit counts (batch x kv heads x head
     blocks) rise and fall: every call's records land after the fixed counter
     area, so no call finds an earlier call's records where its counters are."""
     for i, (hq, hkv, S, tail, pps) in enumerate([(4, 2, 5, 3, 1), (32, 8, 5, 1, 2), (8, 1, 6, 0, 1),
-                                                 (64, 8, 4, 9, 1), (4, 2, 7, 0, 2), (32, 8, 3, 0, 1)]):
+                                                 (64, 8, 4, 9, 1), (4, 1, 70, 5, 1), (4, 2, 7, 0, 2),
+                                                 (32, 8, 3, 0, 1)]):
         print(f"[attn-shared-ws] hq={hq} hkv={hkv} S={S} tail={tail} pps={pps}", flush=True)
         block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], hq, hkv, S, tail, seed=40 + i)
         seq = S * PAGE + tail

@@ -104,6 +104,7 @@ def test_fused_qk_qjl_matches_oracle(device, layout_name, hq, hkv, S):
     ("fast", 64, 8, 4, 9, 1, 0, 1),
     ("default", 8, 2, 7, 0, 3, 21, 2),
     ("fast", 4, 4, 3, 63, 0, 0, 1),
+    ("default", 8, 1, 70, 5, 1, 0, 1),  # 70 splits: two-tier combine
 ])
 def test_decode_attention_qjl_matches_oracle(device, layout_name, hq, hkv, S, tail, pps, masked, B):
     print(f"[qjl attn] {layout_name} hq={hq} hkv={hkv} S={S} tail={tail} pps={pps} masked={masked} B={B}", flush=True)
