@@ -772,6 +772,7 @@ struct AttnShared {
 // End-phase variants of the measurement library (0 in the product).
 constexpr int kFlRelease = 1;    // agent-scope release fence before the ticket
 constexpr int kFlNoAcquire = 2;  // no acquire fence in the combining workgroup
+constexpr int kFlTiers = 4;      // two-tier combine (launched only when tier_splits > 0)
 
 // One thread draws a ticket of a counter that `count` workgroups increment:
 // relaxed agent-scope add; the workgroup that draws the last ticket issues an
@@ -921,7 +922,8 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
   // One tier: the unit's ticket counts its S splits.  Two tiers: the ticket
   // of the split's group counts the group's splits, and the group's combiner
   // then draws the unit's ticket, which counts the groups.
-  const int T = a.tier_splits;
+  constexpr bool kTiers = (FL & kFlTiers) != 0;
+  const int T = kTiers ? a.tier_splits : 0;
   const int grp = T > 0 ? split / T : 0;
   const int first = grp * T;
   const int count = T > 0 ? min(T, S - first) : S;
@@ -938,7 +940,7 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
   float Mc, Lc;
   float4v Ac;
   combine_records(sh, ci, a.part_ml, a.part_acc, unit, S, Sp, first, count, Mc, Lc, Ac);
-  if (T > 0) {
+  if constexpr (kTiers) {
     // Publish the group's record, then the unit's ticket over the groups.
     const int G = a.tier_groups;
     const int Gp = (G + 1) & ~1;
@@ -1714,6 +1716,17 @@ static int32_t launch_measure_variant(const AttnArgs& a, dim3 grid, int kind, hi
 }  // extern "C"
 
 // tp_decode_attention and, with qjl, tp_decode_attention_qjl.
+// The decode kernel of a layout kind, with the two-tier combine compiled in
+// only for launches that use it.
+template <int KIND, bool QJL>
+static void launch_decode(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  const dim3 block(kDecodeWaves * 64);
+  if (a.tier_splits > 0)
+    hipLaunchKernelGGL((decode_attention_kernel<KIND, kDecodeWaves, kFlTiers, QJL>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_attention_kernel<KIND, kDecodeWaves, 0, QJL>), grid, block, 0, s, a);
+}
+
 static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, int32_t hkv,
                                      const tp_page_layout* layout, const tp_pages* pages, int32_t n_pages,
                                      const tp_qjl* qjl, const void* tail_k, const void* tail_v, int32_t tail_len,
@@ -1794,33 +1807,25 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
   const dim3 grid((unsigned)n_groups);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (use_qjl) {
-    const dim3 block(kDecodeWaves * 64);
     switch (n_pages > 0 ? layout_kind(layout) : (int)kKindGeneric) {
-      case kKindDefault:
-        hipLaunchKernelGGL((decode_attention_kernel<kKindDefault, kDecodeWaves, 0, true>), grid, block, 0, s, a);
-        break;
-      case kKindFast:
-        hipLaunchKernelGGL((decode_attention_kernel<kKindFast, kDecodeWaves, 0, true>), grid, block, 0, s, a);
-        break;
-      default:
-        hipLaunchKernelGGL((decode_attention_kernel<kKindGeneric, kDecodeWaves, 0, true>), grid, block, 0, s, a);
-        break;
+      case kKindDefault: launch_decode<kKindDefault, true>(a, grid, s); break;
+      case kKindFast: launch_decode<kKindFast, true>(a, grid, s); break;
+      default: launch_decode<kKindGeneric, true>(a, grid, s); break;
     }
     return launch_status("tp_decode_attention_qjl");
   }
 #ifdef TP_TIMELINE
-  if (g_measure_variant != 0) return launch_measure_variant(a, grid, n_pages > 0 ? layout_kind(layout) : -1, s);
+  if (g_measure_variant != 0) {
+    // The measurement variants combine in one tier (any split count).
+    a.tier_splits = 0;
+    a.tier_groups = 0;
+    return launch_measure_variant(a, grid, n_pages > 0 ? layout_kind(layout) : -1, s);
+  }
 #endif
   switch (n_pages > 0 ? layout_kind(layout) : (int)kKindGeneric) {
-    case kKindDefault:
-      hipLaunchKernelGGL((decode_attention_kernel<kKindDefault, kDecodeWaves>), grid, dim3(kDecodeWaves * 64), 0, s, a);
-      break;
-    case kKindFast:
-      hipLaunchKernelGGL((decode_attention_kernel<kKindFast, kDecodeWaves>), grid, dim3(kDecodeWaves * 64), 0, s, a);
-      break;
-    default:
-      hipLaunchKernelGGL((decode_attention_kernel<kKindGeneric, kDecodeWaves>), grid, dim3(kDecodeWaves * 64), 0, s, a);
-      break;
+    case kKindDefault: launch_decode<kKindDefault, false>(a, grid, s); break;
+    case kKindFast: launch_decode<kKindFast, false>(a, grid, s); break;
+    default: launch_decode<kKindGeneric, false>(a, grid, s); break;
   }
   return launch_status("tp_decode_attention");
 }
