@@ -1475,8 +1475,8 @@ static int32_t n_splits_of(int32_t n_pages, int32_t pps) {
 // groups of kTierSplits whose last workgroup combines the group, and the last
 // group combines the groups, so no workgroup folds more than max(kTierSplits,
 // groups) records.  Measured (default splits): one kv head of 4 / 8 query
-// heads at 131k, 256 splits, 21.6 -> 15.7 / 28.0 -> 16.8 us; 128 splits at
-// 32k (1 or 2 kv heads) -11 %; at 64 splits (4 kv heads, 131k) one tier is
+// heads at 131k, 256 splits, 21.75 -> 15.9 / 28.2 -> 16.9 us; 128 splits at
+// 32k (1 or 2 kv heads) -10 %; at 64 splits (4 kv heads, 131k) one tier is
 // 0.7 us faster; groups of 16 beat 8 and 32.  Every counter of both tiers
 // must fit the fixed counter area; a shape whose counters would not keeps one
 // tier.
