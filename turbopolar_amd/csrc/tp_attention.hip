@@ -219,15 +219,26 @@ __device__ __forceinline__ void build_lut(Lut& lut, const AttnArgs& a, int tid) 
   }
 }
 
+// Word 3 of a raw buffer resource on gfx9-family GPUs: DATA_FORMAT 32-bit
+// (bits 18:15 = 4), every other field 0 (untyped loads, no swizzle).
+constexpr int kRawBufferWord3 = 0x00020000;
+
 // Q rows of the head block as MFMA B operands: lane (h = l16, l4) holds
-// q[h][32*l4 + 8*kk .. +8] for kk = 0..3.
+// q[h][32*l4 + 8*kk .. +8] for kk = 0..3, and zeros for heads past the
+// block's own (l16 >= nh).  The rows are read as raw buffer loads bounded to
+// the block's nh rows, so those lanes read zeros by the buffer's range check:
+// no branch around the loads.  Under a branch, the compiler waited for q
+// (s_waitcnt vmcnt) at the branch's join, before any page load was issued, so
+// every launch paid a memory round trip for q before its first page request.
 __device__ __forceinline__ void load_q(const AttnArgs& a, int b, int kv, int h0, int nh, int l16,
                                        int l4, half8v* qb) {
-  const uint16_t* qrow = a.q + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + l16) * kHeadDim + 32 * l4;
+  const uint16_t* qblk = a.q + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0) * kHeadDim;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(qblk), (short)0, nh * kHeadDim * (int)sizeof(uint16_t), kRawBufferWord3);
+  const int off = (l16 * kHeadDim + 32 * l4) * (int)sizeof(uint16_t);
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
-    uint4 w = make_uint4(0u, 0u, 0u, 0u);
-    if (l16 < nh) w = *reinterpret_cast<const uint4*>(qrow + 8 * kk);
+    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * kk, 0, 0);
     qb[kk] = as_half8(w.x, w.y, w.z, w.w);
   }
 }
@@ -261,7 +272,7 @@ __device__ __forceinline__ void qjl_query(const AttnArgs& a, int b, int kv, int 
   ss += __shfl_xor(ss, 16, 64);
   ss += __shfl_xor(ss, 32, 64);
   qnorm = sqrtf(ss);
-  qsig = l16 < nh ? a.q_signs[(int64_t)b * a.hq + (int64_t)kv * a.g + h0 + l16] : 0ull;
+  qsig = a.q_signs[(int64_t)b * a.hq + (int64_t)kv * a.g + h0 + min(l16, nh - 1)];  // unconditional, as load_q
 }
 
 // Adds the correction to one page's scores s[mt][i] (token 16*mt + 4*l4 + i,
