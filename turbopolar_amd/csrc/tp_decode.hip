@@ -147,7 +147,11 @@ __device__ __forceinline__ uint32_t i8pair_to_h2(uint32_t w, int first) {
   return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
 }
 
-template <int KIND>
+// WANT_K / WANT_V: which of k_out / v_out the launch writes.  They are
+// template parameters, not branches on the pointers: a register set under a
+// branch made the compiler wait for the K loads at its join, so the V loads
+// went out one memory round trip late.
+template <int KIND, bool WANT_K, bool WANT_V>
 __global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
   constexpr bool kFast = KIND == kDecFast;
   constexpr int kCodes = kFast ? 256 : 16;
@@ -162,14 +166,14 @@ __global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
   const int64_t slot = bh * a.capacity + a.page_begin + page;
   const int64_t row0 = slot * kPageTokens;
   const int64_t out0 = bh * a.out_tokens + a.out_offset + (int64_t)page * kPageTokens;
-  const bool want_k = a.k_out != nullptr;
-  const bool want_v = a.v_out != nullptr;
+  constexpr bool want_k = WANT_K;
+  constexpr bool want_v = WANT_V;
 
   // All loads first.
   uint32_t rw[kTok][kFast ? 1 : 2];  // radii of pairs 4c..4c+3
   uint32_t cw[kTok];                 // their angle codes (low 16 bits for 4-bit codes)
   uint16_t ls16 = 0;
-  if (want_k) {
+  if constexpr (want_k) {
 #pragma unroll
     for (int k = 0; k < kTok; ++k) {
       const int64_t row = row0 + t0 + 16 * k;
@@ -186,7 +190,7 @@ __global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
   }
   uint2 vc[kTok];
   uint16_t vs16[kTok];
-  if (want_v) {
+  if constexpr (want_v) {
 #pragma unroll
     for (int k = 0; k < kTok; ++k) {
       const int64_t row = row0 + t0 + 16 * k;
@@ -202,7 +206,7 @@ __global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
   }
 
   // V (v_quant/encoder.py:32-38).
-  if (want_v) {
+  if constexpr (want_v) {
 #pragma unroll
     for (int k = 0; k < kTok; ++k) {
       const half2v sp = __builtin_bit_cast(half2v, (uint32_t)vs16[k] | ((uint32_t)vs16[k] << 16));
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
       *reinterpret_cast<uint4*>(a.v_out + (out0 + t0 + 16 * k) * kHeadDim + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
-  if (!want_k) return;
+  if constexpr (!want_k) return;
   if constexpr (kFast) s_exp[tid] = expf((float)(tid - 128) * h2f(ls16));
   __syncthreads();
 
@@ -244,6 +248,16 @@ __global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
 }  // namespace tp
 
 using namespace tp;
+
+template <int KIND>
+static void launch_spec(const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  if (a.k_out && a.v_out)
+    hipLaunchKernelGGL((decode_pages_spec_kernel<KIND, true, true>), grid, dim3(256), 0, s, a);
+  else if (a.k_out)
+    hipLaunchKernelGGL((decode_pages_spec_kernel<KIND, true, false>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_pages_spec_kernel<KIND, false, true>), grid, dim3(256), 0, s, a);
+}
 
 extern "C" int32_t tp_decode_pages_into(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
                                         int64_t page_begin, int32_t n_pages, void* k_out, void* v_out,
@@ -303,11 +317,12 @@ extern "C" int32_t tp_decode_pages_into(const tp_page_layout* layout, const tp_p
                                                     ((uintptr_t)pages->radii & 3u) == 0)) &&
                        (!v_out || ((uintptr_t)pages->v_codes & 7u) == 0);
   const dim3 grid((unsigned)n_pages, (unsigned)bh);
-  if (is_default && aligned)
-    hipLaunchKernelGGL(decode_pages_spec_kernel<kDecDefault>, grid, dim3(256), 0, s, a);
-  else if (is_fast && aligned)
-    hipLaunchKernelGGL(decode_pages_spec_kernel<kDecFast>, grid, dim3(256), 0, s, a);
-  else
+  if ((is_default || is_fast) && aligned) {
+    if (is_default)
+      launch_spec<kDecDefault>(a, grid, s);
+    else
+      launch_spec<kDecFast>(a, grid, s);
+  } else
     hipLaunchKernelGGL(decode_pages_kernel, grid, dim3(256), 0, s, a);
   return launch_status("tp_decode_pages");
 }
