@@ -1116,13 +1116,24 @@ def copy_calibration(nbytes: int, reps: int = 10) -> None:
     print(json.dumps({"copy_calibration_bytes": nbytes, "reps": reps}))
 
 
+# Untimed warm-up steps per workload when --warmup is not given.  A kernel
+# launched from a fresh process runs before the GPU's clocks have settled: the
+# 32k decode step timed after 20 warm-up launches read 19.8 us and after 2000
+# (about 40 ms of GPU work) 18.5-18.6 us on the same box, so the kernel
+# workloads warm up for tens of milliseconds.  prefill and model consume their
+# warm-up steps as real tokens (longer context), so they keep short warm-ups.
+WARMUP_DEFAULTS = {"decode": 2000, "qk": 2000, "decompress": 1000, "encode": 1000, "stream": 1000,
+                   "layers": 200, "timeline": 200, "prefill": 3, "model": 4}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain copy of BYTES bytes (counter calibration)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps before the timed ones (default: per workload, WARMUP_DEFAULTS)")
     ap.add_argument("--layout", choices=sorted(LAYOUTS), default="default")
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--hq", type=int, default=32)
@@ -1162,6 +1173,8 @@ def main():
         sys.exit(2)
     if args.context % 64:
         sys.exit("--context must be a multiple of 64")
+    if args.warmup is None:
+        args.warmup = WARMUP_DEFAULTS.get(args.workload, 20)
     layout = LAYOUTS[args.layout]
     if args.kind is None:
         args.kind = "loguniform" if args.workload == "layers" else "outlier"
