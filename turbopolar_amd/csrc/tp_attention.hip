@@ -56,8 +56,9 @@ __device__ unsigned long long g_timeline[kTimelineGroups][kTimelineStamps];
   do {              \
   } while (0)
 #endif
-// Stamp slots (thread 0, i.e. wave 0, of each workgroup): 0 start, 2 first
-// loads issued and code tables ready, 4 + 4i QK of wave 0's page i done (its
+// Stamp slots (thread 0, i.e. wave 0, of each workgroup): 0 start, 1 its
+// first page loads issued, 3 its share of the code tables built, 2 the barrier
+// after them passed, 4 + 4i QK of wave 0's page i done (its
 // codes arrived), 5 + 4i its PV done, 52 wave 0's pages done; then for the
 // whole workgroup 53 records stored, 54 stores complete, 55 ticket drawn; the
 // last workgroup of a unit: 57 its record loads folded (thread 0's), 58 split
@@ -95,6 +96,7 @@ struct AttnArgs {
   float scale_log2;
   int32_t pages_per_split;
   int32_t n_splits;
+  int32_t units_total;     // batch x hkv x head_blocks (the grid is n_splits x units_total)
   int32_t counter_stride;  // u32 words between two ticket counters
   int32_t counter_slots;   // ticket counters per unit: 1, or 1 + tier_groups
   uint32_t* counters;
@@ -989,6 +991,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   static_assert(WAVES == 8, "decode_attention_kernel assumes 8 waves per workgroup");
   __shared__ AttnShared<WAVES> sh;
   TP_STAMP(0);
+  // Every argument the prologue reads arrives in one round of scalar loads:
+  // left to itself the compiler loaded the page pointers only after waiting
+  // for the grid fields, a second round trip to fresh argument memory before
+  // the first page request.
+  asm volatile("" ::"s"(a.q), "s"(a.radii), "s"(a.angle_l1), "s"(a.angle_deep), "s"(a.v_codes), "s"(a.v_scales),
+               "s"(a.capacity), "s"(a.n_pages), "s"(a.pages_per_split), "s"(a.seq_len), "s"(a.units_total),
+               "s"(a.head_blocks), "s"(a.hkv), "s"(a.g), "s"(a.hq));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -997,15 +1006,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   const int l4 = lane >> 4;
   // 1-D grid, unit-minor: consecutive workgroup ids go to different kv heads,
   // so with round-robin dispatch over the 8 XCDs every split of one kv head
-  // runs on the same XCD and its partials stay within one L2.
-  const int units_total = (int)(gridDim.x / a.n_splits);
+  // runs on the same XCD and its partials stay within one L2.  32-bit index
+  // arithmetic (units_total * n_splits < 2^31).
+  const int units_total = a.units_total;
   const int lin = blockIdx.x;
-  const int unit_id = lin % units_total;
   const int split = lin / units_total;
-  const int64_t bkv = unit_id / a.head_blocks;
-  const int hb = unit_id % a.head_blocks;
-  const int b = (int)(bkv / a.hkv);
-  const int kv = (int)(bkv - (int64_t)b * a.hkv);
+  const int unit_id = lin - split * units_total;
+  const int bkv32 = unit_id / a.head_blocks;
+  const int hb = unit_id - bkv32 * a.head_blocks;
+  const int b = bkv32 / a.hkv;
+  const int kv = bkv32 - b * a.hkv;
+  const int64_t bkv = bkv32;
   const int h0 = hb * 16;
   const int nh = min(16, a.g - h0);
 
@@ -1039,7 +1050,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     load_k<KIND>(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, kr);
     load_v(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
   }
+  TP_STAMP(1);
   if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
+  TP_STAMP(3);
   __shared__ float qjl_sin[QJL ? kQjlBits + 1 : 1];
   uint64_t qsig = 0;
   float qnorm = 0.0f;
@@ -1792,6 +1805,7 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
   a.scale_log2 = scale * 1.4426950408889634f;
   a.pages_per_split = pages_per_split;
   a.n_splits = n_splits;
+  a.units_total = (int32_t)(batch * hkv * a.head_blocks);
   if (n_splits > 1) {
     const size_t need = tp_decode_workspace_bytes(batch, hq, hkv, n_pages, tail_len, pages_per_split);
     if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u)) {
