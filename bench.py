@@ -935,7 +935,8 @@ def run_timeline(args, layout) -> dict:
     start = t[:, 0]
     us = (t - start.min()) / 100.0
     valid = t >= start[:, None]  # stamps written by this launch
-    names = {0: "start", 1: "wave 0: first page loads issued", 3: "wave 0: code table entries built",
+    names = {0: "start", 59: "wave 0: kernel arguments loaded", 60: "wave 0: q loads issued",
+             1: "wave 0: first page loads issued", 3: "wave 0: code table entries built",
              2: "barrier passed (all waves' first loads issued, tables ready)"}
     for i in range(12):
         names[4 + 4 * i] = f"wave 0 page {i}: codes arrived, scored"

@@ -56,8 +56,8 @@ __device__ unsigned long long g_timeline[kTimelineGroups][kTimelineStamps];
   do {              \
   } while (0)
 #endif
-// Stamp slots (thread 0, i.e. wave 0, of each workgroup): 0 start, 1 its
-// first page loads issued, 3 its share of the code tables built, 2 the barrier
+// Stamp slots (thread 0, i.e. wave 0, of each workgroup): 0 start, 59 kernel
+// arguments loaded, 60 q loads issued, 1 its first page loads issued, 3 its share of the code tables built, 2 the barrier
 // after them passed, 4 + 4i QK of wave 0's page i done (its
 // codes arrived), 5 + 4i its PV done, 52 wave 0's pages done; then for the
 // whole workgroup 53 records stored, 54 stores complete, 55 ticket drawn; the
@@ -998,6 +998,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   asm volatile("" ::"s"(a.q), "s"(a.radii), "s"(a.angle_l1), "s"(a.angle_deep), "s"(a.v_codes), "s"(a.v_scales),
                "s"(a.capacity), "s"(a.n_pages), "s"(a.pages_per_split), "s"(a.seq_len), "s"(a.units_total),
                "s"(a.head_blocks), "s"(a.hkv), "s"(a.g), "s"(a.hq));
+  TP_STAMP(59);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1029,6 +1030,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   // barrier, and nothing before the barrier uses them.
   half8v qb[4];
   load_q(a, b, kv, h0, nh, l16, l4, qb);
+  TP_STAMP(60);
   int page = p_begin + wave;
   KRegs<KIND> kr;
   VRegs vr;
