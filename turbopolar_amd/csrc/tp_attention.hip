@@ -66,6 +66,27 @@ __device__ unsigned long long g_timeline[kTimelineGroups][kTimelineStamps];
 
 enum LayoutKind { kKindDefault = 0, kKindFast = 1, kKindGeneric = 2 };
 
+// Division by a launch constant d as a multiply and a shift: for n < 2^31,
+// l = ceil(log2 d) and m = floor(2^(31+l) / d) + 1 (< 2^32), floor(n / d) =
+// (n * m) >> (31 + l) (Granlund and Montgomery, PLDI 1994, theorem 4.2:
+// 2^(31+l) < m d <= 2^(31+l) + 2^l).  Three scalar instructions instead of
+// the ~30-instruction integer division, on the decode kernel's critical
+// path before its first page load.
+struct FastDiv {
+  uint32_t m;
+  uint32_t sh;
+};
+
+static inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  return FastDiv{(uint32_t)(((1ull << (31 + l)) / d) + 1), 31 + l};
+}
+
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, FastDiv f) {
+  return (uint32_t)(((uint64_t)n * f.m) >> f.sh);
+}
+
 struct AttnArgs {
   const uint16_t* q;
   uint16_t* out;
@@ -97,6 +118,9 @@ struct AttnArgs {
   int32_t pages_per_split;
   int32_t n_splits;
   int32_t units_total;     // batch x hkv x head_blocks (the grid is n_splits x units_total)
+  FastDiv div_units;       // division by units_total, head_blocks, hkv
+  FastDiv div_head_blocks;
+  FastDiv div_hkv;
   int32_t counter_stride;  // u32 words between two ticket counters
   int32_t counter_slots;   // ticket counters per unit: 1, or 1 + tier_groups
   uint32_t* counters;
@@ -997,7 +1021,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   // the first page request.
   asm volatile("" ::"s"(a.q), "s"(a.radii), "s"(a.angle_l1), "s"(a.angle_deep), "s"(a.v_codes), "s"(a.v_scales),
                "s"(a.capacity), "s"(a.n_pages), "s"(a.pages_per_split), "s"(a.seq_len), "s"(a.units_total),
-               "s"(a.head_blocks), "s"(a.hkv), "s"(a.g), "s"(a.hq));
+               "s"(a.head_blocks), "s"(a.hkv), "s"(a.g), "s"(a.hq), "s"(a.div_units.m), "s"(a.div_units.sh),
+               "s"(a.div_head_blocks.m), "s"(a.div_head_blocks.sh), "s"(a.div_hkv.m), "s"(a.div_hkv.sh));
   TP_STAMP(59);
 
   const int tid = threadIdx.x;
@@ -1011,11 +1036,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   // arithmetic (units_total * n_splits < 2^31).
   const int units_total = a.units_total;
   const int lin = blockIdx.x;
-  const int split = lin / units_total;
+  const int split = (int)fast_div((uint32_t)lin, a.div_units);
   const int unit_id = lin - split * units_total;
-  const int bkv32 = unit_id / a.head_blocks;
+  const int bkv32 = (int)fast_div((uint32_t)unit_id, a.div_head_blocks);
   const int hb = unit_id - bkv32 * a.head_blocks;
-  const int b = bkv32 / a.hkv;
+  const int b = (int)fast_div((uint32_t)bkv32, a.div_hkv);
   const int kv = bkv32 - b * a.hkv;
   const int64_t bkv = bkv32;
   const int h0 = hb * 16;
@@ -1808,6 +1833,9 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
   a.pages_per_split = pages_per_split;
   a.n_splits = n_splits;
   a.units_total = (int32_t)(batch * hkv * a.head_blocks);
+  a.div_units = make_fastdiv((uint32_t)a.units_total);
+  a.div_head_blocks = make_fastdiv((uint32_t)a.head_blocks);
+  a.div_hkv = make_fastdiv((uint32_t)hkv);
   if (n_splits > 1) {
     const size_t need = tp_decode_workspace_bytes(batch, hq, hkv, n_pages, tail_len, pages_per_split);
     if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u)) {
