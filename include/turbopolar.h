@@ -292,7 +292,16 @@ int32_t tp_log_radii_rows(const void* radii, int64_t rows, int64_t n, int8_t* co
                           void* stream);
 
 /* ---- Self-test hooks: no counterpart in the reference.  They evaluate the
- * encoder's scalar fp16 helpers so tests can check them exhaustively. ---- */
+ * encoder's scalar fp16 helpers so tests can check them exhaustively, and
+ * the decode kernel's host-side index arithmetic. ---- */
+
+/* Host only (no GPU needed): for every divisor d in [1, d_max], checks the
+ * decode kernel's multiply-shift division (the constants tp_decode_attention
+ * passes for its workgroup-index divisions) against n / d at the ends of the
+ * 31-bit dividend range, around multiples of d spread over it, and for the
+ * first 3d + 5 dividends.  Returns the number of mismatches; *checks (if not
+ * NULL) receives the number of dividends checked. */
+unsigned long long tp_selftest_fastdiv(uint32_t d_max, unsigned long long* checks);
 
 /* For every 16-bit pattern b: sqrt_out[b] = fp16 sqrt of b, log_out[b] = fp16
  * log(max(b, fp16(1e-6))), codes_out[3*b + {0,1,2}] = angle code of the fp16

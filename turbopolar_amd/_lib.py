@@ -116,6 +116,7 @@ _SIGNATURES = {
     "tp_quantize_v_groups": (c_i32, [c_vp, c_i32, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
     "tp_log_radii_rows": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "tp_selftest_f16_tables": (c_i32, [c_vp, c_vp, c_vp, c_vp]),
+    "tp_selftest_fastdiv": (ctypes.c_ulonglong, [ctypes.c_uint32, c_vp]),
     "tp_selftest_atan2_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
     "tp_selftest_div_f16_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
     "tp_selftest_vcode_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),

@@ -83,7 +83,7 @@ static inline FastDiv make_fastdiv(uint32_t d) {
   return FastDiv{(uint32_t)(((1ull << (31 + l)) / d) + 1), 31 + l};
 }
 
-__device__ __forceinline__ uint32_t fast_div(uint32_t n, FastDiv f) {
+__host__ __device__ __forceinline__ uint32_t fast_div(uint32_t n, FastDiv f) {
   return (uint32_t)(((uint64_t)n * f.m) >> f.sh);
 }
 
@@ -2000,6 +2000,29 @@ extern "C" int32_t tp_decode_attention_noalloc(const void* q, int64_t batch, int
   }
   return tp_decode_attention(q, batch, hq, hkv, layout, pages, n_pages, tail_k, tail_v, tail_len, tail_stride,
                              actual_seq_len, scale, pages_per_split, ws, ws_bytes, out, stream);
+}
+
+extern "C" unsigned long long tp_selftest_fastdiv(uint32_t d_max, unsigned long long* checks) {
+  unsigned long long bad = 0, n_checked = 0;
+  const uint64_t top = 1ull << 31;
+  for (uint32_t d = 1; d <= d_max && d != 0; ++d) {
+    const FastDiv f = make_fastdiv(d);
+    auto check = [&](uint64_t n) {
+      if (n >= top) return;
+      ++n_checked;
+      if (fast_div((uint32_t)n, f) != (uint32_t)n / d) ++bad;
+    };
+    for (uint64_t k = 0; k < top; k += top / 257 + d) {
+      const uint64_t base = k / d * d;
+      check(base);
+      check(base + 1);
+      if (base) check(base - 1);
+    }
+    for (uint64_t n = top - std::min<uint64_t>(top, 3ull * d); n < top; ++n) check(n);
+    for (uint64_t n = 0; n < 3ull * d + 5; ++n) check(n);
+  }
+  if (checks) *checks = n_checked;
+  return bad;
 }
 
 #ifdef TP_TIMELINE
