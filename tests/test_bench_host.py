@@ -58,3 +58,14 @@ def test_more_than_one_gpu_is_refused():
                        timeout=300, cwd=ROOT)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+def test_kernel_workloads_warm_up_past_the_clock_ramp():
+    """The kernel workloads time their steps after tens of milliseconds of
+    untimed launches (the GPU's clocks settle in between: the 32k decode step
+    read about 1 us more after 20 warm-up launches than after 2000); the
+    workloads that consume their warm-up steps as tokens keep short ones."""
+    d = bench.WARMUP_DEFAULTS
+    assert d["decode"] >= 2000 and d["qk"] >= 2000
+    assert min(d["encode"], d["decompress"], d["stream"]) >= 1000
+    assert d["prefill"] <= 8 and d["model"] <= 8
