@@ -837,7 +837,7 @@ __device__ __forceinline__ CombineItem combine_item(int tid, int nh, int waves) 
   CombineItem c;
   const int n_items = nh * 32;
   c.ish = n_items <= 32 ? 5 : (n_items <= 64 ? 6 : (n_items <= 128 ? 7 : (n_items <= 256 ? 8 : 9)));
-  c.lsg = 9 - c.ish;
+  c.lsg = (waves == 8 ? 9 : 8) - c.ish;  // log2(threads) - ish; 4-wave launches have nh <= 8
   c.it = tid & ((1 << c.ish) - 1);
   c.sg = tid >> c.ish;
   c.item = c.it < n_items && tid < waves * 64;
@@ -1010,9 +1010,11 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
 
 template <int KIND, int WAVES, int FL = 0, bool QJL = false>
 __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a) {
-  // The fold maps 512 threads onto up to 16 heads x 128 dims at 1, 2 or 4 dims
-  // per thread, and the combine sizes its split groups for 512 threads.
-  static_assert(WAVES == 8, "decode_attention_kernel assumes 8 waves per workgroup");
+  // The fold maps the threads onto heads x 128 dims at 4 dims per thread (512
+  // threads: 16 heads, 256 threads: 8), and the combine sizes its split groups
+  // for the thread count.  The host launches 4 waves only for head blocks of
+  // at most 8 query heads.
+  static_assert(WAVES == 8 || WAVES == 4, "decode_attention_kernel takes 4 or 8 waves per workgroup");
   __shared__ AttnShared<WAVES> sh;
   TP_STAMP(0);
   // Every argument the prologue reads arrives in one round of scalar loads:
@@ -1769,13 +1771,27 @@ static int32_t launch_measure_variant(const AttnArgs& a, dim3 grid, int kind, hi
 // tp_decode_attention and, with qjl, tp_decode_attention_qjl.
 // The decode kernel of a layout kind, with the two-tier combine compiled in
 // only for launches that use it.
+template <int KIND, int W, bool QJL>
+static void launch_decode_w(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  const dim3 block(W * 64);
+  if (a.tier_splits > 0)
+    hipLaunchKernelGGL((decode_attention_kernel<KIND, W, kFlTiers, QJL>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_attention_kernel<KIND, W, 0, QJL>), grid, block, 0, s, a);
+}
+
+// A split of at most 4 pages leaves waves 4-7 of an 8-wave workgroup without
+// a page (they still issue one cache line per page load and join every
+// barrier); such launches take 4-wave workgroups when every head block has at
+// most 8 query heads (the 4-wave fold and combine cover 8 heads).
+static bool four_waves(const AttnArgs& a) { return a.pages_per_split <= 4 && a.g <= 8; }
+
 template <int KIND, bool QJL>
 static void launch_decode(const AttnArgs& a, dim3 grid, hipStream_t s) {
-  const dim3 block(kDecodeWaves * 64);
-  if (a.tier_splits > 0)
-    hipLaunchKernelGGL((decode_attention_kernel<KIND, kDecodeWaves, kFlTiers, QJL>), grid, block, 0, s, a);
+  if (four_waves(a))
+    launch_decode_w<KIND, 4, QJL>(a, grid, s);
   else
-    hipLaunchKernelGGL((decode_attention_kernel<KIND, kDecodeWaves, 0, QJL>), grid, block, 0, s, a);
+    launch_decode_w<KIND, kDecodeWaves, QJL>(a, grid, s);
 }
 
 static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, int32_t hkv,
