@@ -313,6 +313,8 @@ TIERED = [
     ("default", 8, 1, 130, 11, 1, 1, 200),  # masked suffix: the last group (splits 128, 129) holds no live token
     ("fast", 32, 8, 80, 0, 1, 1, 0),  # 8 units of 5 groups
     ("default", 24, 2, 70, 9, 1, 1, 0),  # GQA 12: 384 combine items per group record
+    ("default", 4, 1, 530, 9, 8, 1, 0),  # 8-page splits, 67 of them: 4-wave workgroups, two pages per wave
+    ("fast", 8, 2, 600, 0, 6, 1, 0),  # 6-page splits, 100 per unit: 4-wave workgroups, ragged waves
 ]
 
 
