@@ -53,7 +53,9 @@ def workload_name(args):
     name, cfg = shape.get((args.hq, args.hkv), (f"{args.hq}q/{args.hkv}kv", "not a BASELINE config"))
     if (args.hq, args.hkv, args.context) == (32, 8, 4096):
         name, cfg = "llama3.2-1b-shape", "configs[0]"
-    return f"{name} single-layer decode attention, {args.context} ctx, K {args.kind} (BASELINE {cfg})"
+    tail = getattr(args, "tail", 0)
+    ctx = f"{args.context} ctx" + (f" + {tail} dense tail tokens" if tail else "")
+    return f"{name} single-layer decode attention, {ctx}, K {args.kind} (BASELINE {cfg})"
 
 
 def synthetic_k(kind, hkv, tokens, g, dev):
@@ -94,17 +96,27 @@ def build_caches(args, dev, layout):
                            k_angle_bits_level1=l1b, k_angle_bits_deep=deepb, split_dim=split)
     caches = []
     kind = getattr(args, "kind", "outlier")
+    tail = getattr(args, "tail", 0)
     for r in range(args.rotate):
         g = torch.Generator(device=dev).manual_seed(1000 + r)
-        k = synthetic_k(kind, args.hkv, args.context, g, dev)
-        v = torch.randn((1, args.hkv, args.context, 128), generator=g, device=dev, dtype=torch.float32)
+        k = synthetic_k(kind, args.hkv, args.context + tail, g, dev)
+        v = torch.randn((1, args.hkv, args.context + tail, 128), generator=g, device=dev, dtype=torch.float32)
         rt = TurboPolarKVCacheRuntime(cfg)
         rt.append(k.half(), v.half())
         del k, v
         block, qv, tk, tv, _, seq = rt.get_fused_attention_inputs()
         q = (torch.randn((1, args.hq, 128), generator=g, device=dev) / np.sqrt(128.0)).half()
-        caches.append({"rt": rt, "pages": PageSet(block, qv), "q": q, "seq": seq,
-                       "out": torch.empty((1, args.hq, 128), dtype=torch.float16, device=dev)})
+        c = {"rt": rt, "pages": PageSet(block, qv), "q": q, "seq": seq,
+             "out": torch.empty((1, args.hq, 128), dtype=torch.float16, device=dev),
+             "tail": (None, None, 0, 0)}
+        if tail:
+            from turbopolar_amd.kernels import _tail_view
+
+            (tkv, stride), (tvv, stride_v) = _tail_view(tk), _tail_view(tv)
+            if stride != stride_v or tkv.shape[2] != tail:
+                raise RuntimeError("the runtime's tail views do not share one layout")
+            c["tail"] = (tkv, tvv, tail, stride)
+        caches.append(c)
     torch.cuda.synchronize()
     return cfg, caches
 
@@ -121,7 +133,7 @@ def run_gpu(args, layout):
     L = _lib.lib()
     n_pages = caches[0]["pages"].S
     pps = args.pps or int(L.tp_default_pages_per_split(1, args.hq, args.hkv, n_pages))
-    need = int(L.tp_decode_workspace_bytes(1, args.hq, args.hkv, n_pages, 0, pps))
+    need = int(L.tp_decode_workspace_bytes(1, args.hq, args.hkv, n_pages, getattr(args, "tail", 0), pps))
     ws = torch.zeros(need, dtype=torch.uint8, device=dev)
     scale = fp16_scale(cfg.attention_scale)
     stream = torch.cuda.current_stream(dev).cuda_stream
@@ -144,9 +156,10 @@ def run_gpu(args, layout):
                           n_pages, ctypes.byref(c["qjl"].desc), None, None, 0, 0, c["seq"], scale, pps,
                           ws.data_ptr(), need, c["out"].data_ptr(), stream))
             continue
+        tkv, tvv, tlen, tstride = c["tail"]
         calls.append((c["q"].data_ptr(), 1, args.hq, args.hkv, ctypes.byref(ps.layout), ctypes.byref(ps.pages),
-                      n_pages, None, None, 0, 0, c["seq"], scale, pps, ws.data_ptr(), need,
-                      c["out"].data_ptr(), stream))
+                      n_pages, tkv.data_ptr() if tlen else None, tvv.data_ptr() if tlen else None, tlen, tstride,
+                      c["seq"], scale, pps, ws.data_ptr(), need, c["out"].data_ptr(), stream))
 
     def step(i):
         st = fn(*calls[i % len(calls)])
@@ -224,15 +237,19 @@ def _sample(fn, budget_s: float, min_runs: int = 2):
     return float(np.median(times)), len(times), out
 
 
-def cpu_attention_all_cores(oracle, pool, cores, q, blk, qv, scale, seq):
+def cpu_attention_all_cores(oracle, pool, cores, q, blk, qv, scale, seq, tail_k, tail_v):
     """The oracle's _cpu_online_attention_dense_tail (metal.py:293-332) spread
     over ``pool``: K decode and V dequantisation per (kv head, page range),
-    then the float32 masked softmax attention per kv head.  Every element
-    takes the oracle's own arithmetic; only the work is divided."""
+    the dense tail after the pages, then the float32 masked softmax attention
+    per kv head.  Every element takes the oracle's own arithmetic; only the
+    work is divided."""
     codes, scales = qv
     B, H, S, L, D = codes.shape
-    k = np.empty((B, H, S * L, D), np.float16)
-    v = np.empty((B, H, S * L, D), np.float16)
+    T = tail_k.shape[2]
+    k = np.empty((B, H, S * L + T, D), np.float16)
+    v = np.empty((B, H, S * L + T, D), np.float16)
+    k[:, :, S * L:] = tail_k
+    v[:, :, S * L:] = tail_v
     rs = blk["radii_scales"]
 
     def dec(h, p0, p1):
@@ -278,14 +295,16 @@ def cpu_baseline(args, layout, caches, budget_s):
     }
     qv = (t["v_codes"].cpu().numpy(), t["v_scales"].cpu().numpy())
     q = c["q"].cpu().numpy()
-    empty = np.zeros((1, args.hkv, 0, 128), np.float16)
+    tkv, tvv, tlen, _ = c["tail"]
+    tail_k = tkv.cpu().numpy() if tlen else np.zeros((1, args.hkv, 0, 128), np.float16)
+    tail_v = tvv.cpu().numpy() if tlen else np.zeros((1, args.hkv, 0, 128), np.float16)
     scale = fp16_scale(1.0 / np.sqrt(128.0))
     cores = host_cores()
     with _OneBlasThread(), ThreadPoolExecutor(cores) as pool:
-        t_all, n_all, out = _sample(lambda: cpu_attention_all_cores(oracle, pool, cores, q, blk, qv, scale, c["seq"]),
-                                    budget_s)
+        t_all, n_all, out = _sample(lambda: cpu_attention_all_cores(oracle, pool, cores, q, blk, qv, scale, c["seq"],
+                                                                    tail_k, tail_v), budget_s)
         t_one, n_one, out1 = _sample(lambda: oracle.cpu_online_attention_dense_tail(
-            q, blk, qv, empty, empty, scale, c["seq"], dtype=np.float32), budget_s / 4)
+            q, blk, qv, tail_k, tail_v, scale, c["seq"], dtype=np.float32), budget_s / 4)
     gpu = c["out"].float().cpu().numpy()
     return {"us": t_all * 1e6, "runs": n_all, "cores": cores, "err": float(np.max(np.abs(gpu - out))),
             "one_thread_us": t_one * 1e6, "one_thread_runs": n_one,
@@ -924,7 +943,7 @@ def run_timeline(args, layout) -> dict:
     torch.cuda.synchronize()
     L.tp_timeline_address.restype = ctypes.c_void_p
     addr = L.tp_timeline_address()
-    stamps = np.zeros((2048, 64), np.uint64)
+    stamps = np.zeros((2048, 80), np.uint64)
     hip = ctypes.CDLL("libamdhip64.so")
     rc = hip.hipMemcpy(stamps.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(addr), ctypes.c_size_t(stamps.nbytes), 2)
     if rc != 0:
@@ -942,7 +961,11 @@ def run_timeline(args, layout) -> dict:
         names[4 + 4 * i] = f"wave 0 page {i}: codes arrived, scored"
         names[5 + 4 * i] = f"wave 0 page {i}: done"
     names.update({52: "wave 0 pages done", 53: "workgroup record stored", 54: "stores complete",
-                  55: "ticket drawn", 57: "last workgroup: records folded", 58: "last workgroup: groups merged",
+                  55: "ticket drawn", 64: "last workgroup: combine entered",
+                  65: "last workgroup: record addresses computed", 66: "last workgroup: one more stamp (its cost)",
+                  61: "last workgroup: first record loads issued",
+                  62: "last workgroup: their (m, l) pairs arrived", 57: "last workgroup: records folded",
+                  63: "last workgroup: every wave's fold in LDS", 58: "last workgroup: groups merged",
                   56: "last workgroup: output stored"})
     phases = {}
     for k, name in names.items():
@@ -950,7 +973,22 @@ def run_timeline(args, layout) -> dict:
         if col.size:
             phases[name] = {"median_us": round(float(np.median(col)), 2), "max_us": round(float(col.max()), 2),
                             "workgroups": int(col.size)}
-    return {"phases": phases, "pps": pps, "groups": groups}
+    # The combining workgroups' own ticket (they draw the last ticket of their
+    # unit), and the phases per XCD: workgroup i runs on XCD i mod 8.
+    last = valid[:, 56]
+    if last.any():
+        col = us[last & valid[:, 55], 55]
+        phases["last workgroup: ticket drawn"] = {"median_us": round(float(np.median(col)), 2),
+                                                  "max_us": round(float(col.max()), 2), "workgroups": int(col.size)}
+    xcd = np.arange(groups) % 8
+    per_xcd = {}
+    for k in (0, 1, 2, 52, 53, 55):
+        row = []
+        for x in range(8):
+            col = us[(xcd == x) & valid[:, k], k]
+            row.append([round(float(np.median(col)), 2), round(float(col.max()), 2)] if col.size else None)
+        per_xcd[names[k]] = row
+    return {"phases": phases, "per_xcd_median_max_us": per_xcd, "pps": pps, "groups": groups}
 
 
 # Bytes per page and kv head of each page field the decode kernel reads, in
@@ -1141,6 +1179,8 @@ def main():
     ap.add_argument("--hq", type=int, default=32)
     ap.add_argument("--hkv", type=int, default=8)
     ap.add_argument("--pps", type=int, default=0, help="pages per workgroup (0 = library default)")
+    ap.add_argument("--tail", type=int, default=0,
+                    help="decode: dense fp16 tail tokens after the context's pages (0-63)")
     ap.add_argument("--rotate", type=int, default=0, help="independent caches to rotate (0 = auto, >256 MB)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
@@ -1175,6 +1215,8 @@ def main():
         sys.exit(2)
     if args.context % 64:
         sys.exit("--context must be a multiple of 64")
+    if not 0 <= args.tail < 64 or (args.tail and (args.workload != "decode" or args.qjl or args.variant)):
+        sys.exit("--tail takes 0-63 tokens and only the plain decode workload")
     if args.warmup is None:
         args.warmup = WARMUP_DEFAULTS.get(args.workload, 20)
     layout = LAYOUTS[args.layout]
@@ -1276,7 +1318,8 @@ def main():
     if args.workload == "timeline":
         r = run_timeline(args, layout)
         print(json.dumps({"workload": workload_name(args) + " -- kernel phase timeline", "layout": args.layout,
-                          "pages_per_split": r["pps"], "workgroups": r["groups"], "phases": r["phases"]}))
+                          "pages_per_split": r["pps"], "workgroups": r["groups"], "phases": r["phases"],
+                          "per_xcd_median_max_us": r["per_xcd_median_max_us"]}))
         return
     if args.workload == "model":
         r = run_model(args)
@@ -1379,7 +1422,7 @@ def main():
         }))
         return
     n_pages = args.context // 64
-    step_bytes = algorithmic_bytes(args.hq, args.hkv, n_pages, layout)
+    step_bytes = algorithmic_bytes(args.hq, args.hkv, n_pages, layout, args.tail)
     if args.qjl:
         step_bytes += args.hkv * n_pages * 64 * (8 + 2) + args.hq * 8  # sketches, residual norms, query sketches
     if not args.rotate:
@@ -1413,13 +1456,13 @@ def main():
     traffic = None
     tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                          f"decode_attention_{args.layout}_8b_32k_traffic.json")
-    if os.path.exists(tpath) and args.context == 32768 and args.hq == 32 and args.hkv == 8:
+    if os.path.exists(tpath) and args.context == 32768 and args.hq == 32 and args.hkv == 8 and not args.tail:
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
     metric = METRIC
-    if (args.context, args.hq, args.hkv) != (32768, 32, 8):
+    if (args.context, args.hq, args.hkv, args.tail) != (32768, 32, 8, 0):
         metric = (f"decode-attn µs/step + achieved HBM GB/s (% peak), {args.hq} q / {args.hkv} kv heads, "
-                  f"{args.context} ctx")
+                  f"{args.context} ctx" + (f" + {args.tail} tail tokens" if args.tail else ""))
     line = {
         "metric": metric,
         "value": round(us, 3),
@@ -1440,6 +1483,7 @@ def main():
             "kv_heads": args.hkv,
             "head_dim": 128,
             "context": args.context,
+            "tail_tokens": args.tail,
             "batch": 1,
             "pages_per_split": res["pps"],
             "rotated_caches": args.rotate,

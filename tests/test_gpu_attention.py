@@ -138,6 +138,31 @@ def test_decode_attention_batched(device, B, layout_name, hq, hkv, S, tail, pps,
     assert max_abs(out[0], out[1]) > 1e-2
 
 
+@pytest.mark.parametrize("B,S,tail,pps,drop", [(1, 3, 37, 1, 0), (2, 2, 63, 0, 0), (2, 4, 1, 2, 0),
+                                                (1, 2, 37, 1, 5), (3, 0, 20, 0, 0)])
+def test_decode_attention_tail_rows_past_len(device, B, S, tail, pps, drop):
+    """The dense tail as views into 64-row buffers (the runtime's tail
+    layout: T valid rows per (b, kv) plane, planes 64 rows apart) whose rows
+    past T hold NaN: the kernel reads the T rows only (its loads are bounded
+    to them), so the output matches the oracle and stays finite; with drop > 0
+    the last tail tokens are masked by actual_seq_len as well."""
+    print(f"[attn-tailrows] B={B} S={S} tail={tail} pps={pps} drop={drop}", flush=True)
+    hq, hkv = 8, 2
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], hq, hkv, S, tail, seed=90 + S + tail, B=B)
+    seq = S * PAGE + tail - drop
+    full_k = torch.full((B, hkv, PAGE, 128), float("nan"), dtype=torch.float16, device=device)
+    full_v = torch.full_like(full_k, float("nan"))
+    full_k[:, :, :tail] = torch.from_numpy(tk).to(device)
+    full_v[:, :, :tail] = torch.from_numpy(tv).to(device)
+    tk_view, tv_view = full_k[:, :, :tail], full_v[:, :, :tail]
+    assert tk_view.stride(1) == PAGE * 128  # the views are passed as they are, not copied
+    pages = PageSet(block, qv) if block is not None else None
+    out = kernels.decode_attention(torch.from_numpy(q).to(device), pages, tk_view, tv_view, seq, SCALE16,
+                                   pages_per_split=pps)
+    torch.cuda.synchronize()
+    check(out.float().cpu().numpy(), oracle_out(host, tk, tv, q, seq), f"tail rows past len B={B}")
+
+
 @pytest.mark.parametrize("B,layout_name,hq,hkv,S", [(2, "default", 40, 2, 5), (3, "fast", 8, 2, 3)])
 def test_fused_qk_batched(device, B, layout_name, hq, hkv, S):
     print(f"[qk-batch] B={B} layout={layout_name} hq={hq} hkv={hkv} S={S}", flush=True)

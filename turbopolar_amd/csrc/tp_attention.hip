@@ -44,7 +44,7 @@ namespace tp {
 // Built only into the timeline library (TP_TIMELINE defined), never into the
 // product.
 constexpr int kTimelineGroups = 2048;
-constexpr int kTimelineStamps = 64;
+constexpr int kTimelineStamps = 80;
 __device__ unsigned long long g_timeline[kTimelineGroups][kTimelineStamps];
 #define TP_STAMP(k)                                                                            \
   do {                                                                                          \
@@ -61,8 +61,11 @@ __device__ unsigned long long g_timeline[kTimelineGroups][kTimelineStamps];
 // after them passed, 4 + 4i QK of wave 0's page i done (its
 // codes arrived), 5 + 4i its PV done, 52 wave 0's pages done; then for the
 // whole workgroup 53 records stored, 54 stores complete, 55 ticket drawn; the
-// last workgroup of a unit: 57 its record loads folded (thread 0's), 58 split
-// groups merged, 56 output stored.
+// last workgroup of a unit: 64 its combine entered (ticket read from LDS), 65
+// its record addresses computed, 66 a second stamp right after 65 (the cost of
+// one stamp), 61 its first batch of record loads issued, 62 that batch's (m, l)
+// pairs arrived, 57 its record loads folded (thread 0's), 63 every wave's fold
+// in LDS, 58 split groups merged, 56 output stored.
 
 enum LayoutKind { kKindDefault = 0, kKindFast = 1, kKindGeneric = 2 };
 
@@ -462,24 +465,6 @@ __device__ __forceinline__ void qk_regs(const AttnArgs& a, const Lut& lut, const
   }
 }
 
-// QK over the dense fp16 tail (tokens >= tail_len read as zero).
-__device__ __forceinline__ void qk_tail(const AttnArgs& a, int64_t bkv, const half8v* qb, int l16,
-                                        int l4, float4v* s) {
-  const uint16_t* tk = a.tail_k + bkv * a.tail_stride * kHeadDim + 32 * l4;
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int t = 16 * mt + l16;
-    float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      uint4 w = make_uint4(0u, 0u, 0u, 0u);
-      if (t < a.tail_len) w = *reinterpret_cast<const uint4*>(tk + t * kHeadDim + 8 * kk);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(w.x, w.y, w.z, w.w), qb[kk], acc, 0, 0, 0);
-    }
-    s[mt] = acc;
-  }
-}
-
 // ---- value pages --------------------------------------------------------------
 //
 // Lane (n = l16, l4) owns dims [8n, 8n+8) (group n/4) of the 16 tokens
@@ -557,18 +542,67 @@ __device__ __forceinline__ void pv_regs(const VRegs& v, int sbase4, uint32_t sse
   }
 }
 
+// ---- dense tail -------------------------------------------------------------------
+//
+// The dense fp16 tail's K and V rows of this (b, kv), all in registers at
+// once: raw buffer loads bounded to the tail's tail_len rows, so rows past it
+// read as zero by the buffer's range check and no load sits under a branch.
+// (Loads under a per-row branch were each waited for before their MFMA: up to
+// 32 memory round trips in a row on the last split's critical path.)
+// k[4 mt + kk] = K[16 mt + l16][32 l4 + 8 kk .. +8] (the QK A operands);
+// v[8 ks + e] = V[v_token(ks, l4, e)][8 l16 .. +8] (the PV rows).
+struct TailRegs {
+  u32x4 k[16];
+  u32x4 v[16];
+};
+
+__device__ __forceinline__ void load_tail(const AttnArgs& a, int64_t bkv, int l16, int l4, TailRegs& r) {
+  const int64_t plane = bkv * a.tail_stride * kHeadDim;
+  const int bytes = a.tail_len * kHeadDim * (int)sizeof(uint16_t);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.tail_k + plane),
+                                                                      (short)0, bytes, kRawBufferWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.tail_v + plane),
+                                                                      (short)0, bytes, kRawBufferWord3);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int off = ((16 * mt + l16) * kHeadDim + 32 * l4 + 8 * kk) * (int)sizeof(uint16_t);
+      r.k[4 * mt + kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int off = (v_token(ks, l4, e) * kHeadDim + 8 * l16) * (int)sizeof(uint16_t);
+      r.v[8 * ks + e] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+    }
+  }
+}
+
+// QK over the dense tail (rows past tail_len are zero).
+__device__ __forceinline__ void qk_tail(const TailRegs& r, const half8v* qb, float4v* s) {
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 w = r.k[4 * mt + kk];
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(w.x, w.y, w.z, w.w), qb[kk], acc, 0, 0, 0);
+    }
+    s[mt] = acc;
+  }
+}
+
 // PV over the dense fp16 tail.
-__device__ __forceinline__ void pv_tail(const AttnArgs& a, int64_t bkv, const half8v* pb, int l16,
-                                        int l4, float4v* acc) {
-  const uint16_t* tv = a.tail_v + bkv * a.tail_stride * kHeadDim + 8 * l16;
+__device__ __forceinline__ void pv_tail(const TailRegs& r, const half8v* pb, float4v* acc) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     half8v rows[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int t = v_token(ks, l4, e);
-      uint4 w = make_uint4(0u, 0u, 0u, 0u);
-      if (t < a.tail_len) w = *reinterpret_cast<const uint4*>(tv + t * kHeadDim);
+      const u32x4 w = r.v[8 * ks + e];
       rows[e] = as_half8(w.x, w.y, w.z, w.w);
     }
 #pragma unroll
@@ -756,11 +790,13 @@ __device__ __forceinline__ void fold_records(const float* pml, const float* pac,
       const int ru = min(r0 + u, mine - 1);
       x[u] = *reinterpret_cast<const float4v*>(pac + ru * rstride);
     }
+    if (r0 == 0) TP_STAMP(61);
 #pragma unroll
     for (int u = 0; u < B; ++u) {
       r[u].x = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(half_base + 4 * u, __builtin_bit_cast(int, mlk.x)));
       r[u].y = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(half_base + 4 * u, __builtin_bit_cast(int, mlk.y)));
     }
+    if (r0 == 0) TP_STAMP(62);
 #pragma unroll
     for (int u = 0; u < B; ++u) {
       if (r0 + u >= mine) {
@@ -863,6 +899,8 @@ __device__ __forceinline__ void combine_records(Merge& sh, const CombineItem& ci
   const float* pac = part_acc + ((unit * S_area + first + ci.sg) * 16 + ci.hh) * kHeadDim + 4 * ci.c4;
   const float* pml = part_ml + ((unit * 16 + ci.hh) * Sp_area + first + ci.sg) * 2;
   const int64_t rstride = (int64_t)SG * 16 * kHeadDim;
+  TP_STAMP(65);
+  TP_STAMP(66);
   Mc = -INFINITY;
   Lc = 0.0f;
   Ac = float4v{0.0f, 0.0f, 0.0f, 0.0f};
@@ -880,6 +918,7 @@ __device__ __forceinline__ void combine_records(Merge& sh, const CombineItem& ci
       redml[tid] = make_float2(Mc, Lc);
     }
     lds_barrier();
+    TP_STAMP(63);
     if (ci.sg == 0 && ci.item) {
       if (ci.lsg == 1)
         merge_groups<2>(red, redml, ci.it, ci.ish, Mc, Lc, Ac);
@@ -970,6 +1009,7 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
   __syncthreads();
   TP_STAMP(55);
   if (!sh.last) return;
+  TP_STAMP(64);
 
   // Last workgroup of this (b, kv, head block), or of its split group:
   // combine the records.
@@ -1136,11 +1176,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
       const int64_t tok0 = (int64_t)a.n_pages * kPageTokens;
       const int valid = (int)min((int64_t)a.tail_len, a.seq_len - tok0);
       if (valid > 0) {
+        TailRegs tr;
+        load_tail(a, bkv, l16, l4, tr);
+        __builtin_amdgcn_sched_barrier(0);  // all 32 loads out before the first MFMA waits
         float4v s[4];
-        qk_tail(a, bkv, qb, l16, l4, s);
+        qk_tail(tr, qb, s);
         half8v pb[2];
         softmax_page(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
-        pv_tail(a, bkv, pb, l16, l4, acc);
+        pv_tail(tr, pb, acc);
       }
     }
   }
