@@ -117,7 +117,8 @@ def test_workspace_sizes():
     counters = L.tp_decode_counter_bytes(1, 32, 8)
     assert counters == 65536  # fixed area: records start at the same offset for every shape
     splits = 32
-    assert n == counters + 8 * splits * 16 * 2 * 4 + 8 * splits * 16 * 128 * 4
+    # (m, l) rows in fp32, the splits' normalised outputs in fp16
+    assert n == counters + 8 * splits * 16 * 2 * 4 + 8 * splits * 16 * 128 * 2
     # GQA group > 16 uses two head blocks
     assert L.tp_decode_counter_bytes(2, 40, 2) == 65536
     assert L.tp_decode_counter_bytes(4096, 8, 8) == 32768 * 4  # beyond 16384 units the area grows

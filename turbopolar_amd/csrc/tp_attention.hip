@@ -127,15 +127,17 @@ struct AttnArgs {
   int32_t counter_stride;  // u32 words between two ticket counters
   int32_t counter_slots;   // ticket counters per unit: 1, or 1 + tier_groups
   uint32_t* counters;
+  // Split records: (m, l) of each head in fp32 (part_ml) and the split's
+  // normalised output acc / l of each head in fp16 (part_acc).
   float* part_ml;
-  float* part_acc;
+  uint16_t* part_acc;
   // Two-tier combine (tier_splits > 0): splits [g * tier_splits, ...) form
   // group g of tier_groups; group records in the same layout as part_ml /
   // part_acc with tier_groups records per unit.
   int32_t tier_splits;
   int32_t tier_groups;
   float* tier_ml;
-  float* tier_acc;
+  uint16_t* tier_acc;
   // QJL (tp_fused_qk_qjl, tp_decode_attention_qjl): per-token sketch and
   // residual norm in the page slots, the queries' sketches.
   const uint64_t* qjl_signs;
@@ -684,8 +686,18 @@ __device__ __forceinline__ void softmax_page(const float4v* s, int valid, float 
 // which measured 1.0-1.7 us per step here, while these stores leave nothing
 // of the record in any cache to write back.
 
-__device__ __forceinline__ void st_agent4(float* p, float4v v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+// fp16 pair of two fp32 values (round to nearest even).
+__device__ __forceinline__ uint32_t pack_f2h2(float x, float y) {
+  return (uint32_t)f2h(x) | ((uint32_t)f2h(y) << 16);
+}
+// 1 / l of a record: an empty split (l = 0, m = -inf) stores zeros; a NaN l
+// stays NaN.
+__device__ __forceinline__ float record_inv(float l) { return l == 0.0f ? 0.0f : __builtin_amdgcn_rcpf(l); }
+// 4 dims of a record's normalised output v * inv as fp16, one 8-byte store.
+__device__ __forceinline__ void st_agent_h4(uint16_t* p, float4v v, float inv) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 w = {pack_f2h2(v[0] * inv, v[1] * inv), pack_f2h2(v[2] * inv, v[3] * inv)};
+  asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(w) : "memory");
 }
 __device__ __forceinline__ void st_agent2(float* p, float x, float y) {
   typedef float float2v __attribute__((ext_vector_type(2)));
@@ -742,11 +754,16 @@ __device__ __forceinline__ void fold_waves(const Shared& sh, int h, int d0, floa
 
 // Merges the partial folds of split groups 1 .. SG-1 of item `it` (LDS slot
 // (g << ish) + it) into group 0's state, in group order.
+// The fold state of a combining thread's 8 dims.
+struct Acc8 {
+  float4v lo, hi;
+};
+
 template <int SG>
-__device__ __forceinline__ void merge_groups(const float4v* red, const float2* redml, int it, int ish, float& Mc,
-                                             float& Lc, float4v& Ac) {
+__device__ __forceinline__ void merge_groups(const Acc8* red, const float2* redml, int it, int ish, float& Mc,
+                                             float& Lc, Acc8& Ac) {
   float2 r[SG];
-  float4v x[SG];
+  Acc8 x[SG];
 #pragma unroll
   for (int g2 = 1; g2 < SG; ++g2) {
     r[g2] = redml[(g2 << ish) + it];
@@ -757,12 +774,14 @@ __device__ __forceinline__ void merge_groups(const float4v* red, const float2* r
   for (int g2 = 1; g2 < SG; ++g2) Mx = fmaxf(Mx, r[g2].x);
   const float w0 = Mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mc - Mx);
   Lc *= w0;
-  Ac *= w0;
+  Ac.lo *= w0;
+  Ac.hi *= w0;
 #pragma unroll
   for (int g2 = 1; g2 < SG; ++g2) {
     const float w = r[g2].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r[g2].x - Mx);
     Lc += r[g2].y * w;
-    Ac += x[g2] * w;
+    Ac.lo += x[g2].lo * w;
+    Ac.hi += x[g2].hi * w;
   }
   Mc = Mx;
 }
@@ -770,38 +789,42 @@ __device__ __forceinline__ void merge_groups(const float4v* red, const float2* r
 // Online fold of records 0 .. mine-1 (record r at pml + 2*SG*r, pac + r*rstride)
 // in batches of B, all B + 1 loads of a batch in flight together: a record
 // past `mine` rereads the last one and is then given weight 0, so the loads
-// are unconditional.  Records and states with m = -inf weigh 0 (NaN they carry
-// survives).
+// are unconditional.  A record holds its split's (m, l) and its normalised
+// output o = acc / l in fp16, so it enters the fold as acc = o * l; a lane
+// reads 8 dims (16 bytes) of o per record, which halves the load
+// instructions of fp32 records at 4 dims per lane (the combining CU's load
+// instructions bound the combine).  Records and states with m = -inf weigh 0
+// (NaN they carry survives).
 template <int B>
-__device__ __forceinline__ void fold_records(const float* pml, const float* pac, int SG, int64_t rstride, int mine,
-                                             float& Mc, float& Lc, float4v& Ac) {
-  // The 32 lanes of each half wave share (head, split group) and `mine` (nh * 32
-  // items in whole halves), so one load per batch fetches the B (m, l) pairs,
-  // lane k of the half holding record k, and lane permutes within the half,
-  // whose lanes are all active or all idle, hand them to every lane.
+__device__ __forceinline__ void fold_records(const float* pml, const uint16_t* pac, int SG, int64_t rstride,
+                                             int mine, float& Mc, float& Lc, Acc8& Ac) {
+  // The 16 lanes of each lane group share (head, split group) and `mine`
+  // (16 items per head, groups of 16 lanes all active or all idle), so one load
+  // per batch fetches the B (m, l) pairs, lane k of the group holding record
+  // k, and lane permutes within the group hand them to every lane.
   const int lane = threadIdx.x & 63;
-  const int half_base = (lane & 32) * 4;  // byte address of lane 0 of this half
+  const int group_base = (lane & 48) * 4;  // byte address of lane 0 of this group
   for (int r0 = 0; r0 < mine; r0 += B) {
     float2 r[B];
-    float4v x[B];
+    uint4 x[B];
     const float2 mlk = *reinterpret_cast<const float2*>(pml + 2 * SG * min(r0 + (lane & (B - 1)), mine - 1));
 #pragma unroll
     for (int u = 0; u < B; ++u) {
       const int ru = min(r0 + u, mine - 1);
-      x[u] = *reinterpret_cast<const float4v*>(pac + ru * rstride);
+      x[u] = *reinterpret_cast<const uint4*>(pac + ru * rstride);
     }
     if (r0 == 0) TP_STAMP(61);
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-      r[u].x = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(half_base + 4 * u, __builtin_bit_cast(int, mlk.x)));
-      r[u].y = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(half_base + 4 * u, __builtin_bit_cast(int, mlk.y)));
+      r[u].x = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(group_base + 4 * u, __builtin_bit_cast(int, mlk.x)));
+      r[u].y = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(group_base + 4 * u, __builtin_bit_cast(int, mlk.y)));
     }
     if (r0 == 0) TP_STAMP(62);
 #pragma unroll
     for (int u = 0; u < B; ++u) {
       if (r0 + u >= mine) {
         r[u] = make_float2(-INFINITY, 0.0f);
-        x[u] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        x[u] = make_uint4(0u, 0u, 0u, 0u);
       }
     }
     float Mn = Mc;
@@ -809,12 +832,19 @@ __device__ __forceinline__ void fold_records(const float* pml, const float* pac,
     for (int u = 0; u < B; ++u) Mn = fmaxf(Mn, r[u].x);
     const float w0 = Mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mc - Mn);
     Lc *= w0;
-    Ac *= w0;
+    Ac.lo *= w0;
+    Ac.hi *= w0;
 #pragma unroll
     for (int u = 0; u < B; ++u) {
       const float w = r[u].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(r[u].x - Mn);
-      Lc += r[u].y * w;
-      Ac += x[u] * w;
+      const float wl = r[u].y * w;
+      const half2v o0 = __builtin_bit_cast(half2v, x[u].x);
+      const half2v o1 = __builtin_bit_cast(half2v, x[u].y);
+      const half2v o2 = __builtin_bit_cast(half2v, x[u].z);
+      const half2v o3 = __builtin_bit_cast(half2v, x[u].w);
+      Lc += wl;
+      Ac.lo += float4v{(float)o0[0], (float)o0[1], (float)o1[0], (float)o1[1]} * wl;
+      Ac.hi += float4v{(float)o2[0], (float)o2[1], (float)o3[0], (float)o3[1]} * wl;
     }
     Mc = Mn;
   }
@@ -861,24 +891,24 @@ __device__ __forceinline__ bool draw_ticket(uint32_t* ctr, uint32_t count) {
   return last;
 }
 
-// A combining thread's item: (head hh, 4-dim chunk c4), nh * 32 items padded
-// to a power of two 2^ish; thread (item, sg), sg < SG = 2^lsg = 512 / 2^ish,
-// folds records sg, sg + SG, ...
+// A combining thread's item: (head hh, 8-dim chunk c8), nh * 16 items padded
+// to a power of two 2^ish >= 32; thread (item, sg), sg < SG = 2^lsg = threads /
+// 2^ish, folds records sg, sg + SG, ...
 struct CombineItem {
-  int it, sg, hh, c4, ish, lsg;
+  int it, sg, hh, c8, ish, lsg;
   bool item;
 };
 
 __device__ __forceinline__ CombineItem combine_item(int tid, int nh, int waves) {
   CombineItem c;
-  const int n_items = nh * 32;
-  c.ish = n_items <= 32 ? 5 : (n_items <= 64 ? 6 : (n_items <= 128 ? 7 : (n_items <= 256 ? 8 : 9)));
+  const int n_items = nh * 16;
+  c.ish = n_items <= 32 ? 5 : (n_items <= 64 ? 6 : (n_items <= 128 ? 7 : 8));
   c.lsg = (waves == 8 ? 9 : 8) - c.ish;  // log2(threads) - ish; 4-wave launches have nh <= 8
   c.it = tid & ((1 << c.ish) - 1);
   c.sg = tid >> c.ish;
   c.item = c.it < n_items && tid < waves * 64;
-  c.hh = c.it >> 5;
-  c.c4 = c.it & 31;
+  c.hh = c.it >> 4;
+  c.c8 = c.it & 15;
   return c;
 }
 
@@ -886,45 +916,49 @@ __device__ __forceinline__ CombineItem combine_item(int tid, int nh, int waves) 
 // unit; (m, l) rows of Sp_area pairs per head): every thread folds its share
 // online (running max, rescaled sums) with all loads of a batch of records in
 // flight together (batches of 4 when no thread has more than 4 records, else
-// 8: every load of a batch costs load bandwidth of the one CU that combines);
-// the SG partial folds then meet in LDS and are merged in sg order.  The
+// 8); the SG partial folds then meet in LDS and are merged in sg order.  The
 // threads with sg == 0 return the item's (M, L, A).
 template <class Merge>
 __device__ __forceinline__ void combine_records(Merge& sh, const CombineItem& ci, const float* part_ml,
-                                                const float* part_acc, int64_t unit, int S_area, int Sp_area,
-                                                int first, int count, float& Mc, float& Lc, float4v& Ac) {
+                                                const uint16_t* part_acc, int64_t unit, int S_area, int Sp_area,
+                                                int first, int count, float& Mc, float& Lc, Acc8& Ac) {
   constexpr int WAVES = sizeof(sh.ml) / sizeof(sh.ml[0]);
-  const int SG = 1 << ci.lsg;
-  const int mine = ci.item ? (count - ci.sg + SG - 1) >> ci.lsg : 0;
-  const float* pac = part_acc + ((unit * S_area + first + ci.sg) * 16 + ci.hh) * kHeadDim + 4 * ci.c4;
+  // As many split groups as the threads allow: the record loads then spread
+  // over every wave (fewer groups with more records each were slower).
+  const int lsg = ci.lsg;
+  const int SG = 1 << lsg;
+  const bool active = ci.item;
+  const int mine = active ? (count - ci.sg + SG - 1) >> lsg : 0;
+  const uint16_t* pac = part_acc + ((unit * S_area + first + ci.sg) * 16 + ci.hh) * kHeadDim + 8 * ci.c8;
   const float* pml = part_ml + ((unit * 16 + ci.hh) * Sp_area + first + ci.sg) * 2;
   const int64_t rstride = (int64_t)SG * 16 * kHeadDim;
   TP_STAMP(65);
   TP_STAMP(66);
   Mc = -INFINITY;
   Lc = 0.0f;
-  Ac = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-  if (((count + SG - 1) >> ci.lsg) <= 4)
+  Ac.lo = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  Ac.hi = Ac.lo;
+  if (((count + SG - 1) >> lsg) <= 4)
     fold_records<4>(pml, pac, SG, rstride, mine, Mc, Lc, Ac);
   else
     fold_records<8>(pml, pac, SG, rstride, mine, Mc, Lc, Ac);
   TP_STAMP(57);
   if (SG > 1) {
     const int tid = threadIdx.x;
-    float4v* red = reinterpret_cast<float4v*>(&sh.acc[0][0]);
+    Acc8* red = reinterpret_cast<Acc8*>(&sh.acc[0][0]);
     float2* redml = reinterpret_cast<float2*>(red + (WAVES * 64));
-    if (ci.item) {
+    if (active) {
       red[tid] = Ac;
       redml[tid] = make_float2(Mc, Lc);
     }
     lds_barrier();
     TP_STAMP(63);
     if (ci.sg == 0 && ci.item) {
-      if (ci.lsg == 1)
+      if (lsg == 1)
         merge_groups<2>(red, redml, ci.it, ci.ish, Mc, Lc, Ac);
-      else if (ci.lsg == 2)
+      else if (lsg == 2)
         merge_groups<4>(red, redml, ci.it, ci.ish, Mc, Lc, Ac);
-      else if (ci.lsg == 3)
+      else if (lsg == 3)
         merge_groups<8>(red, redml, ci.it, ci.ish, Mc, Lc, Ac);
       else
         merge_groups<16>(red, redml, ci.it, ci.ish, Mc, Lc, Ac);
@@ -989,7 +1023,8 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
   const int Sp = (S + 1) & ~1;  // (m, l) row length in pairs
   if (live) {
     if (d0 == 0) st_agent2(a.part_ml + ((unit * 16 + h) * Sp + split) * 2, M, L);
-    st_agent4(a.part_acc + ((unit * S + split) * 16 + h) * kHeadDim + d0, float4v{A[0], A[1], A[2], A[3]});
+    st_agent_h4(a.part_acc + ((unit * S + split) * 16 + h) * kHeadDim + d0, float4v{A[0], A[1], A[2], A[3]},
+                record_inv(L));
   }
   TP_STAMP(53);
   wait_stores();
@@ -1015,15 +1050,18 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
   // combine the records.
   const CombineItem ci = combine_item(tid, nh, WAVES);
   float Mc, Lc;
-  float4v Ac;
+  Acc8 Ac;
   combine_records(sh, ci, a.part_ml, a.part_acc, unit, S, Sp, first, count, Mc, Lc, Ac);
   if constexpr (kTiers) {
     // Publish the group's record, then the unit's ticket over the groups.
     const int G = a.tier_groups;
     const int Gp = (G + 1) & ~1;
     if (ci.sg == 0 && ci.item) {
-      if (ci.c4 == 0) st_agent2(a.tier_ml + ((unit * 16 + ci.hh) * Gp + grp) * 2, Mc, Lc);
-      st_agent4(a.tier_acc + ((unit * G + grp) * 16 + ci.hh) * kHeadDim + 4 * ci.c4, Ac);
+      if (ci.c8 == 0) st_agent2(a.tier_ml + ((unit * 16 + ci.hh) * Gp + grp) * 2, Mc, Lc);
+      const float inv = record_inv(Lc);
+      uint16_t* trow = a.tier_acc + ((unit * G + grp) * 16 + ci.hh) * kHeadDim + 8 * ci.c8;
+      st_agent_h4(trow, Ac.lo, inv);
+      st_agent_h4(trow + 4, Ac.hi, inv);
     }
     wait_stores();
     __syncthreads();
@@ -1038,9 +1076,11 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
   TP_STAMP(58);
   if (ci.sg == 0 && ci.item) {
     const float inv = __builtin_amdgcn_rcpf(Lc);
-    uint16_t* orow3 = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + ci.hh) * kHeadDim + 4 * ci.c4;
-    *reinterpret_cast<uint2*>(orow3) = make_uint2((uint32_t)f2h(Ac[0] * inv) | ((uint32_t)f2h(Ac[1] * inv) << 16),
-                                                  (uint32_t)f2h(Ac[2] * inv) | ((uint32_t)f2h(Ac[3] * inv) << 16));
+    uint16_t* orow = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + ci.hh) * kHeadDim + 8 * ci.c8;
+    *reinterpret_cast<uint4*>(orow) = make_uint4(pack_f2h2(Ac.lo[0] * inv, Ac.lo[1] * inv),
+                                                 pack_f2h2(Ac.lo[2] * inv, Ac.lo[3] * inv),
+                                                 pack_f2h2(Ac.hi[0] * inv, Ac.hi[1] * inv),
+                                                 pack_f2h2(Ac.hi[2] * inv, Ac.hi[3] * inv));
   }
   if (tid == 0) __hip_atomic_store(unit_ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   TP_STAMP(56);
@@ -1684,9 +1724,9 @@ size_t tp_decode_workspace_bytes(int64_t batch, int32_t hq, int32_t hkv, int32_t
   const size_t splits = (size_t)n_splits_of(n_pages, pages_per_split);
   const size_t groups = (size_t)tiers_of((int64_t)units, (int32_t)splits).groups;
   return tp_decode_counter_bytes(batch, hq, hkv) + align256(units * 16 * ((splits + 1) & ~(size_t)1) * 2 * sizeof(float)) +
-         align256(units * splits * 16 * kHeadDim * sizeof(float)) +
+         align256(units * splits * 16 * kHeadDim * sizeof(uint16_t)) +
          align256(units * 16 * ((groups + 1) & ~(size_t)1) * 2 * sizeof(float)) +
-         align256(units * groups * 16 * kHeadDim * sizeof(float));
+         align256(units * groups * 16 * kHeadDim * sizeof(uint16_t));
 }
 
 int32_t tp_fused_qk(const void* q, int64_t batch, int32_t hq, int32_t hkv,
@@ -1918,11 +1958,11 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
     ws += tp_decode_counter_bytes(batch, hq, hkv);
     a.part_ml = reinterpret_cast<float*>(ws);
     ws += align256(units * 16 * (((size_t)n_splits + 1) & ~(size_t)1) * 2 * sizeof(float));
-    a.part_acc = reinterpret_cast<float*>(ws);
-    ws += align256(units * (size_t)n_splits * 16 * kHeadDim * sizeof(float));
+    a.part_acc = reinterpret_cast<uint16_t*>(ws);
+    ws += align256(units * (size_t)n_splits * 16 * kHeadDim * sizeof(uint16_t));
     a.tier_ml = reinterpret_cast<float*>(ws);
     ws += align256(units * 16 * (((size_t)tiers.groups + 1) & ~(size_t)1) * 2 * sizeof(float));
-    a.tier_acc = reinterpret_cast<float*>(ws);
+    a.tier_acc = reinterpret_cast<uint16_t*>(ws);
   }
   const dim3 grid((unsigned)n_groups);
   hipStream_t s = static_cast<hipStream_t>(stream);
