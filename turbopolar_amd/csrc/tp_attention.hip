@@ -5,9 +5,9 @@
 // consecutive pages of one kv head and scores ALL g query heads of that kv head
 // from a single read of the page codes.  Each wave walks its own pages with a
 // private online softmax; the waves are merged through LDS, then the
-// workgroup's partial (m, l, acc[128]) per head goes to the workspace and the
-// last workgroup of the kv head to arrive (atomic ticket) combines all
-// partials -- one launch per step.  Above 64 splits per kv head the combine
+// workgroup's partial per head -- (m, l) and its normalised output acc / l in
+// fp16 -- goes to the workspace and the last workgroup of the kv head to
+// arrive (atomic ticket) combines all partials -- one launch per step.  Above 64 splits per kv head the combine
 // has two tiers: groups of 16 splits combine first, and the last group's
 // combiner folds the group results.  The 1-D grid is unit-minor, so with the
 // hardware's round-robin dispatch over the 8 XCDs every split of one kv head
@@ -863,9 +863,9 @@ struct AttnShared {
 // Every wave holds an online-softmax state (m_run, l_run, acc) of its tokens:
 // lane (head l16, lane group l4) holds dims 32*l4 + 8*i + j of head l16 in
 // acc[j][i] and a partial l over its own scores.  The waves merge through LDS
-// into one (m, l, acc[128]) per head; with one split that is the output,
-// otherwise it becomes the split's record and the last split of the unit to
-// arrive combines all records.
+// into one (m, l, acc[128]) per head; with one split acc / l is the output,
+// otherwise (m, l) and acc / l in fp16 become the split's record and the last
+// split of the unit to arrive combines all records.
 //
 // Cross-workgroup ordering: every wave's agent-scope record stores complete
 // (s_waitcnt) before the workgroup barrier, then one thread draws the ticket
