@@ -100,6 +100,9 @@ CASES = [
     ("default", 12, 2, 4, 0, 1),  # GQA 6: combine items in 192 of 256 slots, 2 split groups
     ("default", 24, 2, 3, 9, 1),  # GQA 12: 384 combine items, 1 split group
     ("default", 2, 2, 600, 3, 1),  # 600 splits of one head: two-tier combine, 38 groups
+    ("default", 32, 8, 21, 5, 8),  # 8-page splits, one tier: 4-wave workgroups, two pages per wave, ragged last split
+    ("fast", 16, 4, 13, 0, 6),  # 6-page splits, one tier, 4 waves: waves with one and two pages
+    ("default", 64, 8, 10, 37, 5),  # GQA 8, 5-page splits on 4 waves, a dense tail
 ]
 
 

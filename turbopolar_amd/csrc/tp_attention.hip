@@ -1865,15 +1865,15 @@ static void launch_decode_w(const AttnArgs& a, dim3 grid, hipStream_t s) {
 
 // A split of at most 4 pages leaves waves 4-7 of an 8-wave workgroup without
 // a page (they still issue one cache line per page load and join every
-// barrier); such launches take 4-wave workgroups when every head block has at
-// most 8 query heads (the 4-wave fold and combine cover 8 heads).  Splits of
-// 5-8 pages take them too when the combine has two tiers (few kv heads, long
-// context): measured 15.28 -> 14.85 us for one kv head at 131k, 14.98 ->
-// 14.30 for two at 65k; with one tier they were not faster (16k, 8 kv heads:
-// 13.24 -> 13.12; 32k, 4 kv heads: 14.09 -> 14.68).
-static bool four_waves(const AttnArgs& a) {
-  return a.g <= 8 && (a.pages_per_split <= 4 || (a.pages_per_split <= 8 && a.tier_splits > 0));
-}
+// barrier); splits of 5-8 pages give each of 4 waves two pages instead of one
+// page per wave.  Such launches take 4-wave workgroups when every head block
+// has at most 8 query heads (the 4-wave fold and combine cover 8 heads):
+// measured 15.28 -> 14.85 us for one kv head at 131k (8-page splits, two-tier
+// combine), 13.12 -> 12.61 at 16k and 11.98 -> 11.41 at 12k (8 kv heads, 8-
+// and 6-page splits), 13.10 -> 12.20 for batch 2 at 8k; longer splits stay on
+// 8 waves (at 32k, 4-wave workgroups with 8-page splits took 20.68 us against
+// 18.40 for the default 16-page splits on 8 waves).
+static bool four_waves(const AttnArgs& a) { return a.g <= 8 && a.pages_per_split <= 8; }
 
 template <int KIND, bool QJL>
 static void launch_decode(const AttnArgs& a, dim3 grid, hipStream_t s) {
