@@ -358,6 +358,32 @@ def test_two_tier_combine(device, layout_name, hq, hkv, S, tail, pps, B, drop):
     check(out, oracle_out(host, tk, tv, q, seq), f"tiers S={S}")
 
 
+COMBINE_MAPS = [
+    # hq, hkv, S pages, pages_per_split: the combine's items are (head, 8-dim
+    # chunk) = GQA x 16 per head block, padded to 32 / 64 / 128 / 256 slots,
+    # and the rest of the threads form 2-16 split groups; splits of <= 8 pages
+    # at GQA <= 8 run on 4-wave workgroups (256 threads), longer ones on 8.
+    (1, 1, 23, 2), (2, 1, 23, 9),  # GQA 1 / 2: 16 / 32 items in 32 slots, 8 / 16 split groups
+    (3, 1, 19, 3), (3, 1, 19, 10),  # GQA 3: 48 items in 64 slots
+    (5, 1, 33, 4), (7, 1, 33, 11),  # GQA 5 / 7: 80 / 112 items in 128 slots
+    (8, 1, 40, 5), (8, 1, 40, 12),  # GQA 8: 128 items, 2 / 4 split groups
+    (9, 1, 21, 2), (12, 1, 21, 1),  # GQA 9 / 12 (8 waves): 144 / 192 items in 256 slots, 2 split groups
+    (16, 1, 17, 1), (16, 2, 30, 13),  # GQA 16: 256 items, 2 split groups; 3 splits per unit
+]
+
+
+@pytest.mark.parametrize("hq,hkv,S,pps", COMBINE_MAPS)
+def test_combine_item_maps(device, hq, hkv, S, pps):
+    """Every mapping of the split combine (items per head block, slot
+    padding, split groups on 4- and 8-wave workgroups) against the oracle,
+    with record counts that leave the split groups ragged and a dense tail."""
+    print(f"[attn-combine] hq={hq} hkv={hkv} S={S} pps={pps}", flush=True)
+    block, qv, host, tk, tv, q = build_case(device, LAYOUTS["default"], hq, hkv, S, 11, seed=200 + hq + S)
+    seq = S * PAGE + 11
+    out = run_gpu(device, block, qv, tk, tv, q, seq, pps)
+    check(out, oracle_out(host, tk, tv, q, seq), f"combine map hq={hq} hkv={hkv} pps={pps}")
+
+
 def test_two_tier_launches_repeat_exactly(device):
     """200 launches alternating a two-tier and a one-tier shape on one
     workspace: every output is bit-identical to that shape's first output, so
