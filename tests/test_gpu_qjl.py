@@ -105,6 +105,8 @@ def test_fused_qk_qjl_matches_oracle(device, layout_name, hq, hkv, S):
     ("default", 8, 2, 7, 0, 3, 21, 2),
     ("fast", 4, 4, 3, 63, 0, 0, 1),
     ("default", 8, 1, 70, 5, 1, 0, 1),  # 70 splits: two-tier combine
+    ("fast", 32, 8, 17, 11, 6, 0, 1),  # 6-page splits, one tier: 4-wave workgroups, two pages per wave
+    ("default", 16, 2, 16, 0, 8, 0, 2),  # 8-page splits on 4 waves, batch 2
 ])
 def test_decode_attention_qjl_matches_oracle(device, layout_name, hq, hkv, S, tail, pps, masked, B):
     print(f"[qjl attn] {layout_name} hq={hq} hkv={hkv} S={S} tail={tail} pps={pps} masked={masked} B={B}", flush=True)
