@@ -420,12 +420,24 @@ def run_model(args) -> dict:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    cfg = LlamaConfig(vocab_size=128256, hidden_size=args.hq * 128, intermediate_size=8192,
-                      num_hidden_layers=args.layers, num_attention_heads=args.hq, num_key_value_heads=args.hkv,
-                      head_dim=128, max_position_embeddings=args.context + 4096, attn_implementation="eager")
-    torch.manual_seed(0)
-    with torch.device(dev):
-        model = LlamaForCausalLM(cfg).eval()
+    if args.model_path:
+        # A local checkpoint (run_fast_attention_bench.py:155 loads its --model
+        # the same way, by path), in the dtype it was saved in; its shape
+        # replaces --layers / --hq / --hkv.
+        model = tl.load_local_llama(args.model_path, device=dev, dtype="auto", patch=False)
+        cfg = model.config
+        head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        if head_dim != 128:
+            raise SystemExit(f"--model-path: the decode kernel takes head_dim 128, the checkpoint has {head_dim}")
+        args.layers, args.hq = cfg.num_hidden_layers, cfg.num_attention_heads
+        args.hkv = getattr(cfg, "num_key_value_heads", None) or args.hq
+    else:
+        cfg = LlamaConfig(vocab_size=128256, hidden_size=args.hq * 128, intermediate_size=8192,
+                          num_hidden_layers=args.layers, num_attention_heads=args.hq, num_key_value_heads=args.hkv,
+                          head_dim=128, max_position_embeddings=args.context + 4096, attn_implementation="eager")
+        torch.manual_seed(0)
+        with torch.device(dev):
+            model = LlamaForCausalLM(cfg).eval()
     turbo = tl.make_turbo_cache(model)
     dense = DynamicCache(config=model.config)
     g = torch.Generator(device=dev).manual_seed(7)
@@ -434,7 +446,7 @@ def run_model(args) -> dict:
             k = synthetic_k("loguniform", args.hkv, args.context, g, dev).half()
             v = torch.randn(k.shape, generator=g, device=dev).half()
             turbo.fast(layer).runtime.append(k, v)
-            dense.update(k.float(), v.float(), layer)
+            dense.update(k.to(model.dtype), v.to(model.dtype), layer)
             del k, v
     tokens = torch.randint(0, cfg.vocab_size, (1, args.warmup + args.steps), generator=g, device=dev)
     res = {}
@@ -462,7 +474,8 @@ def run_model(args) -> dict:
     a, b = logits["turbo"], logits["dense"]
     cos = torch.nn.functional.cosine_similarity(a, b, dim=-1)
     top1 = (a.argmax(-1) == b.argmax(-1)).double().mean()
-    return {"turbo_s": res["turbo"], "dense_s": res["dense"], "cos_min": float(cos.min()), "top1": float(top1),
+    return {"weights": str(model.dtype).replace("torch.", ""),
+            "turbo_s": res["turbo"], "dense_s": res["dense"], "cos_min": float(cos.min()), "top1": float(top1),
             "turbo_busy_ms": busy.get("turbo"), "dense_busy_ms": busy.get("dense"),
             "turbo_bytes": int(turbo.nbytes), "dense_bytes": int(sum(x.numel() * x.element_size() for x in (
                 *[layer.keys for layer in dense.layers], *[layer.values for layer in dense.layers])))}
@@ -1197,6 +1210,9 @@ def main():
     ap.add_argument("--kind", choices=["outlier", "loguniform", "studentt", "normal"], default=None,
                     help="K distribution (default: outlier for decode, loguniform for layers)")
     ap.add_argument("--layers", type=int, default=16)
+    ap.add_argument("--model-path", default=None,
+                    help="model: a local Llama checkpoint directory (config.json + safetensors) instead of the "
+                         "randomly initialised configs[1] shape; never downloads")
     ap.add_argument("--graph", action="store_true", help="layers: replay the step as one HIP graph")
     ap.add_argument("--qjl", action="store_true",
                     help="decode: tp_decode_attention_qjl (QJL correction on every page token; synthetic sketches)")
@@ -1327,13 +1343,17 @@ def main():
             "metric": "Llama decode tokens/s through the transformers hook (fused decode attention)",
             "value": round(1.0 / r["turbo_s"], 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(r["turbo_s"] * 1e3, 3), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "f32 weights, f16 cache", "data": "synthetic",
-            "config": {"workload": f"random-init Llama, {args.layers} layers, {args.hq} q / {args.hkv} kv heads, "
-                                   f"head_dim 128, {args.context} cached tokens per layer (BASELINE configs[1] "
-                                   f"shape), teacher-forced single-token decode", "layout": "fast (make_turbo_caches)"},
+            "scaling": "weak", "vs_baseline": None, "dtype": f"{r['weights']} weights, f16 cache",
+            "data": "synthetic tokens and cache" if args.model_path else "synthetic",
+            "config": {"workload": (f"Llama checkpoint {args.model_path}" if args.model_path else "random-init Llama")
+                                   + f", {args.layers} layers, {args.hq} q / {args.hkv} kv heads, "
+                                   f"head_dim 128, {args.context} cached tokens per layer"
+                                   + ("" if args.model_path else " (BASELINE configs[1] shape)")
+                                   + ", teacher-forced single-token decode", "layout": "fast (make_turbo_caches)"},
             "dense_baseline": {"tokens_per_s": round(1.0 / r["dense_s"], 2), "ms_per_token": round(r["dense_s"] * 1e3, 3),
                                "kv_bytes": r["dense_bytes"], "note": "the model's own DynamicCache (the same fp16 "
-                                                                      "K/V values held as fp32), eager attention"},
+                                                                      f"K/V values held as {r['weights']}), eager "
+                                                                      "attention"},
             "turbo_kv_bytes": r["turbo_bytes"],
             "gpu_busy_ms_per_token": {"turbo": r["turbo_busy_ms"], "dense": r["dense_busy_ms"],
                                       "note": "sum of device kernel durations of one forward (torch.profiler), "

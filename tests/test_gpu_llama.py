@@ -200,3 +200,43 @@ def test_nonfinite_kv_in_one_layer_undoes_the_token_everywhere(device):
             tl.unpatch_llama_attention(model)
     assert torch.equal(la, lb)
     assert [cache.fast(i).offset for i in range(2)] == [21, 21]
+
+
+def test_local_checkpoint_decodes_through_the_fused_path(device, tmp_path):
+    """A Llama saved to a local directory and loaded with load_local_llama
+    (the offline counterpart of run_fast_attention_bench.py:155's
+    mlx_lm.load(path)) decodes through tp_decode_attention, and its logits are
+    those of the same weights run in memory through the same hook."""
+    model = _model(device)
+    model.save_pretrained(tmp_path)
+    g = torch.Generator().manual_seed(3)
+    tokens = torch.randint(0, 512, (1, 90), generator=g).to(device)
+    prompt = 60
+    calls = {"n": 0}
+    orig = TurboPolarFastCache.decode_attention
+
+    def counted(self, *a, **k):
+        calls["n"] += 1
+        return orig(self, *a, **k)
+
+    def run(m):
+        cache = tl.make_turbo_cache(m)
+        with torch.no_grad():
+            out = [m(tokens[:, :prompt], past_key_values=cache, use_cache=True).logits[0, -1]]
+            for t in range(prompt, tokens.shape[1]):
+                out.append(m(tokens[:, t:t + 1], past_key_values=cache, use_cache=True).logits[0, -1])
+        torch.cuda.synchronize()
+        return torch.stack(out)
+
+    TurboPolarFastCache.decode_attention = counted
+    try:
+        loaded = tl.load_local_llama(tmp_path, device=device, dtype=torch.float32)  # patches the hook
+        from_disk = run(loaded)
+        in_memory = run(model)
+    finally:
+        tl.unpatch_llama_attention()
+        TurboPolarFastCache.decode_attention = orig
+    steps = tokens.shape[1] - prompt
+    assert calls["n"] == 2 * steps * 2  # both runs, every decode step of both layers
+    assert torch.isfinite(from_disk).all()
+    assert (from_disk - in_memory).abs().max().item() <= 1e-4

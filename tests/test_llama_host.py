@@ -76,3 +76,26 @@ def test_unpatched_model_ignores_turbo_forward():
         finally:
             tl.unpatch_llama_attention()
     assert torch.equal(a, b)
+
+
+def test_load_local_llama(tmp_path):
+    """A checkpoint saved to a local directory loads with its weights intact,
+    eager attention and the requested dtype (the counterpart of
+    run_fast_attention_bench.py:155's mlx_lm.load(path)); patch=True installs
+    the decode hook; a missing directory is an error, never a download."""
+    model = _tiny_model()
+    model.save_pretrained(tmp_path)
+    loaded = tl.load_local_llama(tmp_path, device="cpu", dtype=torch.float32, patch=False)
+    assert not tl.is_patched()
+    assert loaded.dtype == torch.float32 and loaded.config._attn_implementation == "eager"
+    ref = model.state_dict()
+    got = loaded.state_dict()
+    assert ref.keys() == got.keys() and all(torch.equal(ref[k], got[k]) for k in ref)
+    half = tl.load_local_llama(tmp_path, device="cpu", dtype=torch.float16, patch=True)
+    try:
+        assert tl.is_patched() and half.dtype == torch.float16
+    finally:
+        tl.unpatch_llama_attention()
+    assert not tl.is_patched()
+    with pytest.raises(OSError):
+        tl.load_local_llama(tmp_path / "missing", device="cpu", patch=False)

@@ -40,6 +40,7 @@ __all__ = [
     "TurboPolarCache",
     "TurboPolarLayer",
     "make_turbo_cache",
+    "load_local_llama",
     "patch_llama_attention",
     "unpatch_llama_attention",
     "is_patched",
@@ -233,6 +234,25 @@ def unpatch_llama_attention(model=None) -> None:
     if _orig_llama_model_forward is not None:
         _llama.LlamaModel.forward = _orig_llama_model_forward
         _orig_llama_model_forward = None
+
+
+def load_local_llama(path, device="cuda", dtype=torch.float16, patch: bool = True):
+    """A Llama checkpoint from a local directory (``save_pretrained`` layout:
+    ``config.json`` plus safetensors weights), ready for TurboPolar decode: the
+    model in eval mode on ``device`` in ``dtype`` with eager attention, and the
+    decode hook patched in (``patch``).  The counterpart of the reference
+    benchmark's ``mlx_lm.load(path)`` (run_fast_attention_bench.py:155) for a
+    local path only: ``local_files_only`` makes a missing file an error instead
+    of a download.  Returns the model; ``make_turbo_cache(model)`` gives its
+    cache."""
+    from transformers import LlamaForCausalLM
+
+    model = LlamaForCausalLM.from_pretrained(str(path), local_files_only=True, dtype=dtype,
+                                             attn_implementation="eager", use_safetensors=True)
+    model = model.to(device).eval()
+    if patch:
+        patch_llama_attention(model)
+    return model
 
 
 def is_patched() -> bool:
