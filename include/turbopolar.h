@@ -277,6 +277,20 @@ int32_t tp_decode_attention_qjl(const void* q, int64_t batch, int32_t hq, int32_
                                 int32_t pages_per_split, void* workspace, size_t workspace_bytes,
                                 void* out, void* stream);
 
+/* Decode attention over compressed K pages and dense fp16 V
+ * (MetalKernelBridge.execute_online_attention_dense_v, metal.py:586-649,
+ * kernel tqpolar_online_attention_dense_v, tqpolar_online_attention.metal:10-196;
+ * the reference's dense_v_debug storage).  pages: the K fields only (v_codes
+ * and v_scales are not read); v_dense: fp16 [batch*hkv][v_capacity][64][128],
+ * 16-byte aligned, v_capacity >= n_pages; qjl: NULL, or the sketches for
+ * use_qjl=True.  No dense tail (the reference's method takes none); n_pages >=
+ * 1.  Other arguments, workspace and errors as tp_decode_attention. */
+int32_t tp_decode_attention_dense_v(const void* q, int64_t batch, int32_t hq, int32_t hkv,
+                                    const tp_page_layout* layout, const tp_pages* pages, int32_t n_pages,
+                                    const tp_qjl* qjl, const void* v_dense, int64_t v_capacity,
+                                    int64_t actual_seq_len, float scale, int32_t pages_per_split, void* workspace,
+                                    size_t workspace_bytes, void* out, void* stream);
+
 /* GroupedVQuantizer.quantize_block (rfsn_v11/quant/v_quant/encoder.py:16-30)
  * for any group size dividing the row: v is [rows][dim] of in_dtype (0 fp16,
  * 1 fp32); codes int8 [rows][dim], scales fp16 [rows][dim / group_size].  The

@@ -24,7 +24,7 @@ Parity status per function (what pins it is listed in ``tests/test_oracle_*.py``
   quantisation error bound |v - dequantize(quantize(v))| <= 0.53125 s + half
   an fp16 ulp on groups whose magnitudes differ by up to 2^16.
 * ``cpu_fused_qk`` / ``cpu_online_attention`` /
-  ``cpu_online_attention_dense_tail`` -- pinned against textbook softmax
+  ``cpu_online_attention_dense_v`` / ``cpu_online_attention_dense_tail`` -- pinned against textbook softmax
   attention computed independently with torch float64 SDPA on the decoded
   K/V, and against brute-force loops on tiny inputs.
 """

@@ -48,7 +48,7 @@ tests/test_oracle_attention.py, tests/test_golden.py):
   bound 0.53125 s + half an fp16 ulp.
 * decode_block: radius invariant sqrt(kx^2 + ky^2) ~ r, decode->encode
   idempotence.
-* softmax_attention, cpu_fused_qk, cpu_online_attention[_dense_tail]: torch
+* softmax_attention, cpu_fused_qk, cpu_online_attention[_dense_v|_dense_tail]: torch
   float64 scaled_dot_product_attention, brute-force loops on one page, the
   split-K merge algebra.
 
@@ -78,6 +78,7 @@ __all__ = [
     "dequantize_block",
     "cpu_fused_qk",
     "cpu_online_attention",
+    "cpu_online_attention_dense_v",
     "cpu_online_attention_dense_tail",
     "softmax_attention",
     "fp16_scale",
@@ -475,6 +476,19 @@ def cpu_online_attention(q, block, quant_v, scale, actual_seq_len, dtype=F64):
     v = dequantize_block(codes, scales)
     B, H, S, L, D = codes.shape
     return softmax_attention(q, k, v.reshape(B, H, S * L, D), scale, actual_seq_len, dtype)
+
+
+def cpu_online_attention_dense_v(q, block, v_dense, scale, actual_seq_len, dtype=F64, qjl=None):
+    """``execute_online_attention_dense_v``'s CPU path (metal.py:586-601: V
+    reshaped to ``[B, H_kv, S*L, D]`` and repeated over the GQA group, then
+    ``_cpu_online_attention``, metal.py:267-291): decoded K, dense fp16 V, the
+    QJL correction times ``scale`` on every token when ``qjl`` = (packed
+    signs, norms, packed query signs, proj_dim)."""
+    k = decode_block(*_block_fields(block))
+    B, H, T, D = k.shape
+    v = np.asarray(v_dense, np.float16).reshape(B, H, T, D)
+    bias = None if qjl is None else qjl_dot_estimate(q, *qjl) * F64(scale)
+    return softmax_attention(q, k, v, scale, actual_seq_len, dtype, score_bias=bias)
 
 
 def cpu_online_attention_dense_tail(q, block, quant_v, tail_k, tail_v, scale, actual_seq_len, dtype=F64,

@@ -116,3 +116,53 @@ def test_dense_tail_equals_concatenated_attention():
     vd = oracle.dequantize_block(*qv).reshape(1, 2, 128, 128)
     ref = _sdpa(q, np.concatenate([kd, k[:, :, 128:]], 2), np.concatenate([vd, v[:, :, 128:]], 2), 0.08837890625)
     assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def _sdpa_bias(q, k, v, scale, bias, seq_len):
+    """torch float64 SDPA with an additive float mask: the bias on valid tokens, -inf past seq_len."""
+    qt = torch.from_numpy(q.astype(np.float64))[:, :, None, :]
+    g = q.shape[1] // k.shape[1]
+    kt = torch.from_numpy(k.astype(np.float64)).repeat_interleave(g, dim=1)
+    vt = torch.from_numpy(v.astype(np.float64)).repeat_interleave(g, dim=1)
+    mask = torch.from_numpy(bias.astype(np.float64))[:, :, None, :].clone()
+    mask[..., seq_len:] = -math.inf
+    out = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask, scale=scale)
+    return out[:, :, 0].numpy()
+
+
+@pytest.mark.parametrize("hq,hkv,pages,seq", [(8, 2, 2, 128), (4, 4, 3, 150), (12, 3, 1, 1)])
+def test_dense_v_matches_torch_sdpa(hq, hkv, pages, seq):
+    """Decoded K pages with a dense fp16 V of shape [B, Hkv, S, 64, 128]:
+    torch float64 SDPA on the same K and V, tokens past ``seq`` masked."""
+    k, v = gen_kv(5 + pages, 2, hkv, pages * 64, "normal", np.float16)
+    q = gen_q(5 + pages, 2, hq)
+    blk, _ = oracle_pages(k, v, LAYOUTS["default"])
+    v5 = v.reshape(2, hkv, pages, 64, 128)
+    scale = 0.08837890625
+    got = oracle.cpu_online_attention_dense_v(q, blk, v5, scale, seq)
+    kd = oracle.decode_block(blk["radii"], None, blk["angle_codes_l1"], blk["angle_codes_deep"], blk["metadata"])
+    ref = _sdpa(q, kd, v, scale, seq)
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+    # A V that differs from the quantised one: the dense values themselves are used.
+    q_only = oracle.cpu_online_attention(q, blk, oracle.quantize_block(v5), scale, seq)
+    assert not np.allclose(got, q_only, rtol=1e-9, atol=1e-9)
+
+
+def test_dense_v_qjl_bias_is_scaled_estimate_on_every_token():
+    """With QJL the estimate times ``scale`` is added to every page token's
+    score: SDPA with that additive float mask."""
+    k, v = gen_kv(9, 1, 2, 128, "normal", np.float16)
+    q = gen_q(9, 1, 4)
+    blk, _ = oracle_pages(k, v, LAYOUTS["default"])
+    kd = oracle.decode_block(blk["radii"], None, blk["angle_codes_l1"], blk["angle_codes_deep"], blk["metadata"])
+    w = oracle.qjl_projection(42, 128, 64)
+    res = (k.astype(np.float64) - kd.astype(np.float64)).reshape(1, 2, 2, 64, 128)
+    packed, norms = oracle.qjl_residual_sketch(res, w)
+    qp, _ = oracle.qjl_residual_sketch(q, w)
+    qjl = (packed, norms, qp, 64)
+    scale = 0.125
+    got = oracle.cpu_online_attention_dense_v(q, blk, v.reshape(1, 2, 2, 64, 128), scale, 100, qjl=qjl)
+    bias = oracle.qjl_dot_estimate(q, *qjl) * scale
+    assert np.abs(bias[..., :100]).max() > 1e-3
+    ref = _sdpa_bias(q, kd, v, scale, bias, 100)
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)

@@ -111,6 +111,13 @@ _SIGNATURES = {
             c_vp, c_vp, c_i32, c_i64, c_i64, c_float, c_i32, c_vp, c_size, c_vp, c_vp,
         ],
     ),
+    "tp_decode_attention_dense_v": (
+        c_i32,
+        [
+            c_vp, c_i64, c_i32, c_i32, _P_LAYOUT, _P_PAGES, c_i32, _P_QJL,
+            c_vp, c_i64, c_i64, c_float, c_i32, c_vp, c_size, c_vp, c_vp,
+        ],
+    ),
     "tp_qjl_sketch": (c_i32, [c_vp, c_i32, c_i64, c_i32, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "tp_qjl_dot_estimate": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_i32, c_vp, c_vp]),
     "tp_quantize_v_groups": (c_i32, [c_vp, c_i32, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),

@@ -6,6 +6,7 @@ rfsn_v11/kernels/turbo_polar/metal.py:57-792 for the supported path:
 * ``execute_fused_qk(q, block, config) -> scores``            (metal.py:494-530)
 * ``execute_online_attention_quant_v(...) -> (out, trace)``    (metal.py:651-715)
 * ``execute_online_attention_quant_v_dense_tail(...)``         (metal.py:717-792)
+* ``execute_online_attention_dense_v(...) -> (out, trace)``    (metal.py:586-649)
 
 * ``execute_fused_qk_qjl(q, block, qjl_payload, q_proj_signs, config)`` (metal.py:532-571)
 
@@ -24,7 +25,7 @@ from typing import Any, Dict, Optional, Tuple
 import torch
 
 from . import _lib
-from .kernels import PageSet, decode_attention, fp16_scale, fused_qk
+from .kernels import PageSet, decode_attention, decode_attention_dense_v, fp16_scale, fused_qk
 from .payload import PolarKeyBlock, QuantizedVBlock
 from .qjl import QJLPages
 
@@ -105,6 +106,36 @@ class HipKernelBridge:
             "fallback_used": False,
             "qjl_used": bool(use_qjl),
             "quant_v_used": True,
+            "actual_seq_len": actual_seq_len,
+            "num_queries_per_kv": q.shape[1] // pages.H,
+        }
+        return out, trace
+
+    def execute_online_attention_dense_v(
+        self,
+        q: torch.Tensor,
+        block: PolarKeyBlock,
+        v_dense: torch.Tensor,
+        qjl_payload: Optional[Any],
+        q_proj_signs: Optional[torch.Tensor],
+        config,
+        actual_seq_len: int,
+        use_qjl: bool = False,
+    ) -> Tuple[torch.Tensor, Dict[str, Any]]:
+        """Compressed K with dense V (metal.py:586-649, the dense_v_debug
+        storage): ``v_dense`` ``[B, H_kv, S, 64, 128]`` (or ``[B, H_kv, S * 64,
+        128]``), tp_decode_attention_dense_v."""
+        qjl = self._qjl(use_qjl, qjl_payload, q_proj_signs)
+        self._supports_block(block)
+        pages = _pages_of(block, None, config.head_dim)
+        out = decode_attention_dense_v(q, pages, v_dense, actual_seq_len, fp16_scale(config.attention_scale), qjl=qjl)
+        trace = {
+            "kernel_name": "tqpolar_online_attention_dense_v",
+            "hip_kernel": "tp_decode_attention_dense_v",
+            "hip_used": True,
+            "fallback_used": False,
+            "qjl_used": bool(use_qjl),
+            "quant_v_used": False,
             "actual_seq_len": actual_seq_len,
             "num_queries_per_kv": q.shape[1] // pages.H,
         }

@@ -33,6 +33,7 @@
 // global index >= actual_seq_len are masked, the dense fp16 tail follows the
 // pages, fp32 softmax statistics and accumulation, fp16 output.
 #include <mutex>
+#include <type_traits>
 
 #include "tp_common.h"
 
@@ -144,6 +145,11 @@ struct AttnArgs {
   const uint16_t* qjl_norms;
   const uint64_t* q_signs;
   int64_t qjl_capacity;  // sketch slots per bh
+  // Dense fp16 values instead of the V codes (tp_decode_attention_dense_v):
+  // [bkv][v_capacity pages][64][128].  Last, so the other fields keep their
+  // argument offsets.
+  const uint16_t* v_dense;
+  int64_t v_capacity;
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -597,14 +603,15 @@ __device__ __forceinline__ void qk_tail(const TailRegs& r, const half8v* qb, flo
   }
 }
 
-// PV over the dense fp16 tail.
-__device__ __forceinline__ void pv_tail(const TailRegs& r, const half8v* pb, float4v* acc) {
+// PV over 64 dense fp16 V rows held as in TailRegs::v (row v_token(ks, l4, e)
+// in element 8 ks + e, dims 8 l16 .. +8).
+__device__ __forceinline__ void pv_rows(const u32x4* v, const half8v* pb, float4v* acc) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     half8v rows[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const u32x4 w = r.v[8 * ks + e];
+      const u32x4 w = v[8 * ks + e];
       rows[e] = as_half8(w.x, w.y, w.z, w.w);
     }
 #pragma unroll
@@ -615,6 +622,37 @@ __device__ __forceinline__ void pv_tail(const TailRegs& r, const half8v* pb, flo
       acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, pb[ks], acc[j], 0, 0, 0);
     }
   }
+}
+
+// PV over the dense fp16 tail.
+__device__ __forceinline__ void pv_tail(const TailRegs& r, const half8v* pb, float4v* acc) { pv_rows(r.v, pb, acc); }
+
+// ---- dense values (execute_online_attention_dense_v, metal.py:586-649) --------------
+//
+// The pages' V as fp16 rows instead of codes and scales: a page's rows in the
+// PV layout of the dense tail, 16-byte non-temporal loads.
+struct DenseVRegs {
+  u32x4 w[16];
+};
+
+__device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16, int l4, int lane, DenseVRegs& v) {
+  (void)lane;
+  const uint16_t* vbase = a.v_dense + slot * (kPageTokens * kHeadDim) + 8 * l16;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint4 w = ldnt4(vbase + v_token(ks, l4, e) * kHeadDim);
+      v.w[8 * ks + e] = u32x4{w.x, w.y, w.z, w.w};
+    }
+  }
+}
+
+__device__ __forceinline__ void pv_regs(const DenseVRegs& v, int sbase4, uint32_t ssel, const half8v* pb,
+                                        float4v* acc) {
+  (void)sbase4;
+  (void)ssel;
+  pv_rows(v.w, pb, acc);
 }
 
 // ---- online softmax ------------------------------------------------------------
@@ -1088,7 +1126,7 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
 
 // ---- decode attention kernel ---------------------------------------------------
 
-template <int KIND, int WAVES, int FL = 0, bool QJL = false>
+template <int KIND, int WAVES, int FL = 0, bool QJL = false, bool DV = false>
 __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a) {
   // The fold maps the threads onto heads x 128 dims at 4 dims per thread (512
   // threads: 16 heads, 256 threads: 8), and the combine sizes its split groups
@@ -1140,11 +1178,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   TP_STAMP(60);
   int page = p_begin + wave;
   KRegs<KIND> kr;
-  VRegs vr;
+  // V: the page store's codes, or the dense V planes' rows (DV).
+  typename std::conditional<DV, DenseVRegs, VRegs>::type vr;
   if constexpr (KIND == kKindGeneric) {  // also the launch for a call without pages
     if (page < p_end) {
       load_k<KIND>(a, bkv * a.capacity + page, l16, l4, kr);
-      load_v(a, bkv * a.capacity + page, l16, l4, lane, vr);
+      if constexpr (DV)
+        load_v(a, bkv * a.v_capacity + page, l16, l4, lane, vr);
+      else
+        load_v(a, bkv * a.capacity + page, l16, l4, lane, vr);
     }
   } else {
     // The specialised layouts always have pages (p_begin < n_pages).  A wave
@@ -1157,7 +1199,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     const int p_load = has_page ? page : p_begin;
     const int lane_e = has_page ? lane : 0;
     load_k<KIND>(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, kr);
-    load_v(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
+    if constexpr (DV)
+      load_v(a, bkv * a.v_capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
+    else
+      load_v(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
   }
   TP_STAMP(1);
   if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
@@ -1195,7 +1240,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     half8v pb[2];
     softmax_page(s, kPageTokens, a.scale_log2, l4, m_run, l_run, acc, pb);
     pv_regs(vr, sbase4, ssel, pb, acc);
-    load_v(a, bkv * a.capacity + page + WAVES, l16, l4, lane, vr);
+    if constexpr (DV)
+      load_v(a, bkv * a.v_capacity + page + WAVES, l16, l4, lane, vr);
+    else
+      load_v(a, bkv * a.capacity + page + WAVES, l16, l4, lane, vr);
     if (it < 12) TP_STAMP(5 + 4 * it);
   }
   if (page < p_end) {
@@ -1854,13 +1902,13 @@ static int32_t launch_measure_variant(const AttnArgs& a, dim3 grid, int kind, hi
 // tp_decode_attention and, with qjl, tp_decode_attention_qjl.
 // The decode kernel of a layout kind, with the two-tier combine compiled in
 // only for launches that use it.
-template <int KIND, int W, bool QJL>
+template <int KIND, int W, bool QJL, bool DV = false>
 static void launch_decode_w(const AttnArgs& a, dim3 grid, hipStream_t s) {
   const dim3 block(W * 64);
   if (a.tier_splits > 0)
-    hipLaunchKernelGGL((decode_attention_kernel<KIND, W, kFlTiers, QJL>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((decode_attention_kernel<KIND, W, kFlTiers, QJL, DV>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((decode_attention_kernel<KIND, W, 0, QJL>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((decode_attention_kernel<KIND, W, 0, QJL, DV>), grid, block, 0, s, a);
 }
 
 // A split of at most 4 pages leaves waves 4-7 of an 8-wave workgroup without
@@ -1883,16 +1931,39 @@ static void launch_decode(const AttnArgs& a, dim3 grid, hipStream_t s) {
     launch_decode_w<KIND, kDecodeWaves, QJL>(a, grid, s);
 }
 
+// Dense V (the reference's dense_v_debug storage) runs on 8-wave workgroups
+// only: one instantiation per layout and QJL choice keeps the build short.
+template <bool QJL>
+static void launch_decode_dense_v(const AttnArgs& a, int kind, dim3 grid, hipStream_t s) {
+  switch (kind) {
+    case kKindDefault: launch_decode_w<kKindDefault, kDecodeWaves, QJL, true>(a, grid, s); break;
+    case kKindFast: launch_decode_w<kKindFast, kDecodeWaves, QJL, true>(a, grid, s); break;
+    default: launch_decode_w<kKindGeneric, kDecodeWaves, QJL, true>(a, grid, s); break;
+  }
+}
+
 static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, int32_t hkv,
                                      const tp_page_layout* layout, const tp_pages* pages, int32_t n_pages,
                                      const tp_qjl* qjl, const void* tail_k, const void* tail_v, int32_t tail_len,
                                      int64_t tail_stride, int64_t actual_seq_len, float scale,
                                      int32_t pages_per_split, void* workspace, size_t workspace_bytes, void* out,
-                                     void* stream, bool use_qjl) {
+                                     void* stream, bool use_qjl, const void* v_dense = nullptr,
+                                     int64_t v_capacity = 0) {
   clear_error();
   AttnArgs a{};
-  if (!fill_common(a, q, batch, hq, hkv, layout, pages, n_pages, true)) return TP_ERR_INVALID;
+  if (!fill_common(a, q, batch, hq, hkv, layout, pages, n_pages, v_dense == nullptr)) return TP_ERR_INVALID;
   if (use_qjl && !fill_qjl(a, qjl, n_pages)) return TP_ERR_INVALID;
+  if (v_dense) {
+    if (((uintptr_t)v_dense & 15u) || v_capacity < n_pages) {
+      set_error("dense V must be 16-byte aligned with v_capacity >= n_pages (got %lld < %d)", (long long)v_capacity,
+                n_pages);
+      return TP_ERR_INVALID;
+    }
+    a.v_codes = nullptr;
+    a.v_scales = nullptr;
+    a.v_dense = static_cast<const uint16_t*>(v_dense);
+    a.v_capacity = v_capacity;
+  }
   if (!out || ((uintptr_t)out & 15u)) {
     set_error("out must be a non-NULL 16-byte aligned buffer");
     return TP_ERR_INVALID;
@@ -1966,6 +2037,14 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
   }
   const dim3 grid((unsigned)n_groups);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (v_dense) {
+    const int kind = layout_kind(layout);
+    if (use_qjl)
+      launch_decode_dense_v<true>(a, kind, grid, s);
+    else
+      launch_decode_dense_v<false>(a, kind, grid, s);
+    return launch_status("tp_decode_attention_dense_v");
+  }
   if (use_qjl) {
     switch (n_pages > 0 ? layout_kind(layout) : (int)kKindGeneric) {
       case kKindDefault: launch_decode<kKindDefault, true>(a, grid, s); break;
@@ -2012,6 +2091,21 @@ int32_t tp_decode_attention_qjl(const void* q, int64_t batch, int32_t hq, int32_
   return decode_attention_impl(q, batch, hq, hkv, layout, pages, n_pages, qjl, tail_k, tail_v, tail_len,
                                tail_stride, actual_seq_len, scale, pages_per_split, workspace, workspace_bytes, out,
                                stream, true);
+}
+
+int32_t tp_decode_attention_dense_v(const void* q, int64_t batch, int32_t hq, int32_t hkv,
+                                    const tp_page_layout* layout, const tp_pages* pages, int32_t n_pages,
+                                    const tp_qjl* qjl, const void* v_dense, int64_t v_capacity,
+                                    int64_t actual_seq_len, float scale, int32_t pages_per_split, void* workspace,
+                                    size_t workspace_bytes, void* out, void* stream) {
+  if (n_pages < 1 || !v_dense) {
+    clear_error();
+    set_error("tp_decode_attention_dense_v needs pages and their dense V");
+    return TP_ERR_INVALID;
+  }
+  return decode_attention_impl(q, batch, hq, hkv, layout, pages, n_pages, qjl, nullptr, nullptr, 0, 0,
+                               actual_seq_len, scale, pages_per_split, workspace, workspace_bytes, out, stream,
+                               qjl != nullptr, v_dense, v_capacity);
 }
 
 }  // extern "C"

@@ -347,6 +347,64 @@ def _launch_decode(q16, Hkv, layout, pages, n_pages, tk, tv, tail_len, tail_stri
     return out
 
 
+def decode_attention_dense_v(
+    q: torch.Tensor,
+    pageset: PageSet,
+    v_dense: torch.Tensor,
+    actual_seq_len: int,
+    scale: float,
+    pages_per_split: int = 0,
+    out: Optional[torch.Tensor] = None,
+    qjl=None,
+) -> torch.Tensor:
+    """tp_decode_attention_dense_v -> fp16 ``[B, H_q, 128]``: attention over
+    the compressed K pages of ``pageset`` (its V fields are not read) and dense
+    V ``v_dense`` ``[B, H_kv, S, 64, 128]`` or ``[B, H_kv, S * 64, 128]`` (any
+    float dtype; converted to fp16), the reference's
+    execute_online_attention_dense_v (metal.py:586-649).  ``qjl``: a
+    ``qjl.QJLPages`` of the pages (use_qjl=True)."""
+    q16 = _q16(q)
+    B, Hq, _ = q16.shape
+    Hkv, n_pages = pageset.H, pageset.S
+    if pageset.B != B:
+        raise ValueError(f"batch of q ({B}) and pages ({pageset.B}) differ")
+    if Hq % Hkv:
+        raise ValueError(f"H_q={Hq} is not a multiple of H_kv={Hkv}")
+    require_hip(v_dense, "v_dense")
+    if v_dense.ndim == 5:
+        if tuple(v_dense.shape[:2]) != (B, Hkv) or v_dense.shape[3] != PAGE or v_dense.shape[4] != HEAD_DIM:
+            raise ValueError(f"v_dense shape {tuple(v_dense.shape)} does not match [B={B}, H_kv={Hkv}, S, "
+                             f"{PAGE}, {HEAD_DIM}]")
+        v_cap = int(v_dense.shape[2])
+    elif v_dense.ndim == 4:
+        if tuple(v_dense.shape[:2]) != (B, Hkv) or v_dense.shape[3] != HEAD_DIM or v_dense.shape[2] % PAGE:
+            raise ValueError(f"v_dense shape {tuple(v_dense.shape)} does not match [B={B}, H_kv={Hkv}, S * {PAGE}, "
+                             f"{HEAD_DIM}]")
+        v_cap = int(v_dense.shape[2]) // PAGE
+    else:
+        raise ValueError(f"v_dense must be 4-D or 5-D, got shape {tuple(v_dense.shape)}")
+    if v_cap < n_pages:
+        raise ValueError(f"v_dense holds {v_cap} pages, the key block {n_pages}")
+    v16 = v_dense.to(torch.float16).contiguous()
+    if qjl is not None:
+        qjl.check_against(B, Hkv, n_pages, Hq)
+    dev = q16.device
+    if out is None:
+        out = torch.empty((B, Hq, HEAD_DIM), dtype=torch.float16, device=dev)
+    L = lib()
+    pps = int(pages_per_split) or int(L.tp_default_pages_per_split(B, Hq, Hkv, n_pages))
+    need = int(L.tp_decode_workspace_bytes(B, Hq, Hkv, n_pages, 0, pps))
+    ws = _Workspace.get(dev, need)
+    with on_device(dev):
+        st = L.tp_decode_attention_dense_v(
+            ptr(q16), B, Hq, Hkv, ctypes.byref(pageset.layout), ctypes.byref(pageset.pages), n_pages,
+            ctypes.byref(qjl.desc) if qjl is not None else None, ptr(v16), v_cap, int(actual_seq_len),
+            float(scale), pps, ws.data_ptr(), ws.numel(), ptr(out), stream_handle(dev),
+        )
+    check(st, "tp_decode_attention_dense_v")
+    return out
+
+
 def decode_attention_store(q: torch.Tensor, layout, pages: TPPages, n_pages: int, num_kv_heads: int,
                            tail_k: Optional[torch.Tensor], tail_v: Optional[torch.Tensor], seq_len: int,
                            scale: float) -> torch.Tensor:
