@@ -103,12 +103,17 @@ def build_caches(args, dev, layout):
         v = torch.randn((1, args.hkv, args.context + tail, 128), generator=g, device=dev, dtype=torch.float32)
         rt = TurboPolarKVCacheRuntime(cfg)
         rt.append(k.half(), v.half())
+        v_dense = None
+        if getattr(args, "dense_v", False):
+            # The same V rows, dense fp16 [1, hkv, pages, 64, 128]: the dense-V
+            # attention reads these in place of the runtime's quantised pages.
+            v_dense = v.half().reshape(1, args.hkv, args.context // 64, 64, 128).contiguous()
         del k, v
         block, qv, tk, tv, _, seq = rt.get_fused_attention_inputs()
         q = (torch.randn((1, args.hq, 128), generator=g, device=dev) / np.sqrt(128.0)).half()
         c = {"rt": rt, "pages": PageSet(block, qv), "q": q, "seq": seq,
              "out": torch.empty((1, args.hq, 128), dtype=torch.float16, device=dev),
-             "tail": (None, None, 0, 0)}
+             "tail": (None, None, 0, 0), "v_dense": v_dense}
         if tail:
             from turbopolar_amd.kernels import _tail_view
 
@@ -155,6 +160,12 @@ def run_gpu(args, layout):
             calls.append((c["q"].data_ptr(), 1, args.hq, args.hkv, ctypes.byref(ps.layout), ctypes.byref(ps.pages),
                           n_pages, ctypes.byref(c["qjl"].desc), None, None, 0, 0, c["seq"], scale, pps,
                           ws.data_ptr(), need, c["out"].data_ptr(), stream))
+            continue
+        if getattr(args, "dense_v", False):
+            fn = L.tp_decode_attention_dense_v
+            calls.append((c["q"].data_ptr(), 1, args.hq, args.hkv, ctypes.byref(ps.layout), ctypes.byref(ps.pages),
+                          n_pages, None, c["v_dense"].data_ptr(), n_pages, c["seq"], scale, pps, ws.data_ptr(), need,
+                          c["out"].data_ptr(), stream))
             continue
         tkv, tvv, tlen, tstride = c["tail"]
         calls.append((c["q"].data_ptr(), 1, args.hq, args.hkv, ctypes.byref(ps.layout), ctypes.byref(ps.pages),
@@ -1214,6 +1225,8 @@ def main():
                     help="model: a local Llama checkpoint directory (config.json + safetensors) instead of the "
                          "randomly initialised configs[1] shape; never downloads")
     ap.add_argument("--graph", action="store_true", help="layers: replay the step as one HIP graph")
+    ap.add_argument("--dense-v", action="store_true",
+                    help="decode: tp_decode_attention_dense_v (compressed K pages, dense fp16 V pages)")
     ap.add_argument("--qjl", action="store_true",
                     help="decode: tp_decode_attention_qjl (QJL correction on every page token; synthetic sketches)")
     ap.add_argument("--variant", choices=sorted(VARIANTS), default=None,
@@ -1233,6 +1246,8 @@ def main():
         sys.exit("--context must be a multiple of 64")
     if not 0 <= args.tail < 64 or (args.tail and (args.workload != "decode" or args.qjl or args.variant)):
         sys.exit("--tail takes 0-63 tokens and only the plain decode workload")
+    if args.dense_v and (args.workload != "decode" or args.qjl or args.variant or args.tail):
+        sys.exit("--dense-v takes only the plain decode workload")
     if args.warmup is None:
         args.warmup = WARMUP_DEFAULTS.get(args.workload, 20)
     layout = LAYOUTS[args.layout]
@@ -1445,6 +1460,8 @@ def main():
     step_bytes = algorithmic_bytes(args.hq, args.hkv, n_pages, layout, args.tail)
     if args.qjl:
         step_bytes += args.hkv * n_pages * 64 * (8 + 2) + args.hq * 8  # sketches, residual norms, query sketches
+    if args.dense_v:
+        step_bytes += args.hkv * n_pages * 64 * (256 - 136)  # dense fp16 V rows in place of V codes and scales
     if not args.rotate:
         args.rotate = max(4, int(np.ceil(320e6 / step_bytes)))
 
@@ -1463,7 +1480,7 @@ def main():
     us = ms * 1e3
     gbps = step_bytes / (ms * 1e-3) / 1e9
     cpu = None
-    if not args.no_cpu and not args.qjl:
+    if not args.no_cpu and not args.qjl and not args.dense_v:
         cb = cpu_baseline(args, layout, res["caches"], args.cpu_budget)
         cpu = {"value": round(cb["us"], 1), "unit": "us/step", "cores": cb["cores"], "kind": "port",
                "sample": f"{cb['runs']} full decode steps of the {args.hq}-head/{args.hkv}-kv-head {args.context}-token "
@@ -1519,6 +1536,11 @@ def main():
     }
     if args.variant is not None:
         line["kernel_variant"] = f"{args.variant} (measurement library: phase stamps compiled in)"
+    if args.dense_v:
+        line["metric"] = "decode-attn with dense V µs/step + achieved HBM GB/s, Llama-3-8B shape"
+        line["config"]["workload"] += " + dense fp16 V (tp_decode_attention_dense_v)"
+        line["cpu_baseline"] = None
+        line["roofline"]["traffic"] = None
     if args.qjl:
         line["metric"] = "decode-attn with QJL correction µs/step + achieved HBM GB/s, Llama-3-8B shape"
         line["config"]["workload"] += " + QJL (tp_decode_attention_qjl, 64-bit sketches, synthetic)"
