@@ -1492,7 +1492,7 @@ def main():
                               "outputs_identical": cb["same_as_one_thread"]}}
     traffic = None
     tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                         f"decode_attention_{args.layout}_8b_32k_traffic.json")
+                         f"decode_attention_{'dense_v_' if args.dense_v else ''}{args.layout}_8b_32k_traffic.json")
     if os.path.exists(tpath) and args.context == 32768 and args.hq == 32 and args.hkv == 8 and not args.tail:
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
@@ -1540,7 +1540,6 @@ def main():
         line["metric"] = "decode-attn with dense V µs/step + achieved HBM GB/s, Llama-3-8B shape"
         line["config"]["workload"] += " + dense fp16 V (tp_decode_attention_dense_v)"
         line["cpu_baseline"] = None
-        line["roofline"]["traffic"] = None
     if args.qjl:
         line["metric"] = "decode-attn with QJL correction µs/step + achieved HBM GB/s, Llama-3-8B shape"
         line["config"]["workload"] += " + QJL (tp_decode_attention_qjl, 64-bit sketches, synthetic)"
