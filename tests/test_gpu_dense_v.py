@@ -159,3 +159,14 @@ def test_bridge_dense_v(device):
     assert trace_q["qjl_used"]
     ref = oracle.cpu_online_attention_dense_v(q, _blk(host), vt.cpu().numpy(), SCALE16, 3 * PAGE, qjl=tup)
     _check(out_q.float().cpu().numpy(), ref, "bridge dense_v qjl")
+
+
+def test_dense_v_seq_len_beyond_stored_tokens(device):
+    """A length past the stored tokens attends every stored token, as the
+    reference's mask (global index >= actual_seq_len) does."""
+    block, _, host, _, _, q = build_case(device, LAYOUTS["default"], 8, 2, 2, 0, seed=12)
+    vt = torch.from_numpy(_dense_v(13, 1, 2, 2, 2)).to(device)
+    qd = torch.from_numpy(q).to(device)
+    full = kernels.decode_attention_dense_v(qd, PageSet(block, None), vt, 2 * PAGE, SCALE16)
+    longer = kernels.decode_attention_dense_v(qd, PageSet(block, None), vt, 2 * PAGE + 100, SCALE16)
+    assert torch.equal(full, longer)
