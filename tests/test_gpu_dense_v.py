@@ -170,3 +170,50 @@ def test_dense_v_seq_len_beyond_stored_tokens(device):
     full = kernels.decode_attention_dense_v(qd, PageSet(block, None), vt, 2 * PAGE, SCALE16)
     longer = kernels.decode_attention_dense_v(qd, PageSet(block, None), vt, 2 * PAGE + 100, SCALE16)
     assert torch.equal(full, longer)
+
+
+def test_dense_v_graph_replay_matches_eager(device):
+    """Two dense-V launches (6 one-page splits each, so the combine and the
+    ticket reset run inside the graph) captured into one HIP graph: each of
+    three replays, with eager launches and syncs between them, reproduces the
+    eager outputs bit for bit, and the eager outputs match the oracle."""
+    cases = []
+    for seed in (60, 61):
+        block, _, host, _, _, q = build_case(device, LAYOUTS["fast"], 32, 8, 6, 0, seed=seed)
+        vd = _dense_v(seed + 7, 1, 8, 6, 6)
+        cases.append((PageSet(block, None), torch.from_numpy(q).to(device), torch.from_numpy(vd).to(device),
+                      torch.empty((1, 32, 128), dtype=torch.float16, device=device), host, q, vd))
+    seq = 6 * PAGE - 1
+
+    def step():
+        for ps, qt, vt, out, *_ in cases:
+            kernels.decode_attention_dense_v(qt, ps, vt, seq, SCALE16, pages_per_split=1, out=out)
+
+    step()
+    torch.cuda.synchronize()
+    eager = [c[3].clone() for c in cases]
+    for (ps, qt, vt, out, host, q, vd), e in zip(cases, eager):
+        _check(e.float().cpu().numpy(), oracle.cpu_online_attention_dense_v(q, _blk(host), vd, SCALE16, seq),
+               "graph eager")
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    # Captured on the warmed-up side stream: the library's per-stream
+    # workspace already exists, so nothing is allocated inside the capture.
+    with torch.cuda.graph(graph, stream=side):
+        step()
+    for rep in range(3):
+        for c in cases:
+            c[3].fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        for c, e in zip(cases, eager):
+            assert torch.equal(c[3], e), f"replay {rep} differs from eager"
+        step()
+        torch.cuda.synchronize()
+        for c, e in zip(cases, eager):
+            assert torch.equal(c[3], e), f"eager launch after replay {rep} differs"
