@@ -1931,14 +1931,30 @@ static void launch_decode(const AttnArgs& a, dim3 grid, hipStream_t s) {
     launch_decode_w<KIND, kDecodeWaves, QJL>(a, grid, s);
 }
 
-// Dense V (the reference's dense_v_debug storage) runs on 8-wave workgroups
-// only: one instantiation per layout and QJL choice keeps the build short.
+// Dense V (the reference's dense_v_debug storage) takes the same workgroup
+// size rule as the quantised V pages.
 template <bool QJL>
 static void launch_decode_dense_v(const AttnArgs& a, int kind, dim3 grid, hipStream_t s) {
+  const bool w4 = four_waves(a);
   switch (kind) {
-    case kKindDefault: launch_decode_w<kKindDefault, kDecodeWaves, QJL, true>(a, grid, s); break;
-    case kKindFast: launch_decode_w<kKindFast, kDecodeWaves, QJL, true>(a, grid, s); break;
-    default: launch_decode_w<kKindGeneric, kDecodeWaves, QJL, true>(a, grid, s); break;
+    case kKindDefault:
+      if (w4)
+        launch_decode_w<kKindDefault, 4, QJL, true>(a, grid, s);
+      else
+        launch_decode_w<kKindDefault, kDecodeWaves, QJL, true>(a, grid, s);
+      break;
+    case kKindFast:
+      if (w4)
+        launch_decode_w<kKindFast, 4, QJL, true>(a, grid, s);
+      else
+        launch_decode_w<kKindFast, kDecodeWaves, QJL, true>(a, grid, s);
+      break;
+    default:
+      if (w4)
+        launch_decode_w<kKindGeneric, 4, QJL, true>(a, grid, s);
+      else
+        launch_decode_w<kKindGeneric, kDecodeWaves, QJL, true>(a, grid, s);
+      break;
   }
 }
 
