@@ -109,6 +109,34 @@ def test_decode_attention_argument_validation():
     assert st == _lib.TP_ERR_WORKSPACE  # any number of splits that fits the grid is accepted
 
 
+def test_decode_attention_dense_v_argument_validation():
+    """tp_decode_attention_dense_v: dense V is required, 16-byte aligned and
+    at least n_pages deep; the page structure's V fields are not needed.
+    Every rejected call returns before any device access."""
+    L = _lib.lib()
+    lay = _lib.make_layout(False, 4, 4, 64)
+    pages = _lib.TPPages(4096, 8192, 12288, 16384, None, None, 8)
+
+    def call(**kw):
+        a = dict(n_pages=4, v=32768, vcap=4, seq=256, pps=0)
+        a.update(kw)
+        st = L.tp_decode_attention_dense_v(4096, 1, 8, 2, ctypes.byref(lay), ctypes.byref(pages), a["n_pages"],
+                                           None, a["v"], a["vcap"], a["seq"], 0.088, a["pps"], None, 0, 8192, None)
+        return st, L.tp_last_error().decode()
+
+    assert call(v=None)[0] == _lib.TP_ERR_INVALID
+    assert call(n_pages=0)[0] == _lib.TP_ERR_INVALID
+    st, msg = call(vcap=3)
+    assert st == _lib.TP_ERR_INVALID and "v_capacity" in msg
+    st, msg = call(v=32770)
+    assert st == _lib.TP_ERR_INVALID and "aligned" in msg
+    assert call(seq=0)[0] == _lib.TP_ERR_INVALID
+    # Valid arguments with NULL V codes and scales reach the workspace check
+    # (4 one-page splits need one), still before any launch.
+    st, msg = call(pps=1)
+    assert st == _lib.TP_ERR_WORKSPACE and "workspace" in msg
+
+
 def test_workspace_sizes():
     L = _lib.lib()
     # Llama-3-8B shape at 32k: one workgroup per CU -> 16 pages per split
