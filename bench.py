@@ -189,8 +189,8 @@ def run_gpu(args, layout):
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / args.steps
 
-    # Correctness guard on the timed configuration (first cache vs its own
-    # re-run with one split per workgroup: split-K invariance).
+    # Determinism guard on the timed configuration: the first cache's output
+    # from the timed launches against one more launch of the same call.
     ref_out = caches[0]["out"].clone()
     step(0)
     torch.cuda.synchronize()
@@ -200,14 +200,30 @@ def run_gpu(args, layout):
 
 
 def host_cores() -> int:
-    """Host threads the CPU baselines use: every core this process may run on,
-    at most ``TP_BENCH_CPU_THREADS`` (default 16, one GPU's share of a
-    GPU box's host)."""
+    """Host threads the CPU baselines use: every core this process may run on
+    (its CPU affinity), or ``TP_BENCH_CPU_THREADS`` when set."""
+    env = os.environ.get("TP_BENCH_CPU_THREADS")
+    if env:
+        return max(1, int(env))
+    return affinity_cores()
+
+
+def affinity_cores() -> int:
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
-        n = os.cpu_count() or 1
-    return max(1, min(n, int(os.environ.get("TP_BENCH_CPU_THREADS", "16"))))
+        return os.cpu_count() or 1
+
+
+def cgroup_cpu_quota():
+    """CPUs' worth of time the process's cgroup grants (cgroup v2 cpu.max), or
+    None when unlimited or unknown."""
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()
+        return None if quota == "max" else round(int(quota) / int(period), 2)
+    except (OSError, ValueError):
+        return None
 
 
 class _OneBlasThread:
@@ -314,12 +330,21 @@ def cpu_baseline(args, layout, caches, budget_s):
     with _OneBlasThread(), ThreadPoolExecutor(cores) as pool:
         t_all, n_all, out = _sample(lambda: cpu_attention_all_cores(oracle, pool, cores, q, blk, qv, scale, c["seq"],
                                                                     tail_k, tail_v), budget_s)
+    t16 = n16 = None
+    if cores != 16:
+        # The 16-thread figure of earlier runs (one GPU's share of a GPU box's
+        # host), beside the all-core one.
+        with _OneBlasThread(), ThreadPoolExecutor(16) as pool:
+            t16, n16, _ = _sample(lambda: cpu_attention_all_cores(oracle, pool, 16, q, blk, qv, scale, c["seq"],
+                                                                  tail_k, tail_v), budget_s / 4)
+    with _OneBlasThread():
         t_one, n_one, out1 = _sample(lambda: oracle.cpu_online_attention_dense_tail(
             q, blk, qv, tail_k, tail_v, scale, c["seq"], dtype=np.float32), budget_s / 4)
     gpu = c["out"].float().cpu().numpy()
     return {"us": t_all * 1e6, "runs": n_all, "cores": cores, "err": float(np.max(np.abs(gpu - out))),
             "one_thread_us": t_one * 1e6, "one_thread_runs": n_one,
-            "same_as_one_thread": bool(np.array_equal(out, out1))}
+            "same_as_one_thread": bool(np.array_equal(out, out1)),
+            "sixteen_us": None if t16 is None else t16 * 1e6, "sixteen_runs": n16}
 
 
 def run_layers(args, layout) -> dict:
@@ -1489,7 +1514,12 @@ def main():
                          f"threads; max-abs vs GPU {cb['err']:.2e})",
                "one_thread": {"value": round(cb["one_thread_us"], 1), "unit": "us/step", "cores": 1,
                               "sample": f"{cb['one_thread_runs']} steps of the unsplit oracle call",
-                              "outputs_identical": cb["same_as_one_thread"]}}
+                              "outputs_identical": cb["same_as_one_thread"]},
+               "host": {"affinity_cores": affinity_cores(), "os_cpu_count": os.cpu_count(),
+                        "cgroup_cpu_quota": cgroup_cpu_quota()}}
+        if cb["sixteen_us"] is not None:
+            cpu["sixteen_threads"] = {"value": round(cb["sixteen_us"], 1), "unit": "us/step", "cores": 16,
+                                      "sample": f"{cb['sixteen_runs']} full decode steps on 16 threads"}
     traffic = None
     tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                          f"decode_attention_{'dense_v_' if args.dense_v else ''}{args.layout}_8b_32k_traffic.json")

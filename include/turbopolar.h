@@ -211,6 +211,17 @@ int32_t tp_decode_pages_into(const tp_page_layout* layout, const tp_pages* pages
                              int64_t page_begin, int32_t n_pages, void* k_out, void* v_out,
                              int64_t out_tokens, int64_t out_offset, void* stream);
 
+/* Selected pages in one launch: output page j of every (batch, head) row is
+ * stored page page_index[j] (page_index: device int32 array of n_index
+ * entries; entries outside [0, n_stored) are clamped into it, so the launch
+ * never reads past the first n_stored pages -- callers check the indices
+ * first).  k_out, v_out: fp16 [bh][n_index*64][128] (either may be NULL).
+ * Replaces the per-page decode_block loop of
+ * TurboPolarKVCacheRuntime.fetch_blocks (turbo_polar_cache.py:321-346). */
+int32_t tp_decode_pages_gather(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
+                               int32_t n_stored, const int32_t* page_index, int32_t n_index, void* k_out,
+                               void* v_out, void* stream);
+
 /* Append staging (replaces the per-input mx.isfinite(...).all() check of
  * TurboPolarKVCacheRuntime._validate_append_inputs, turbo_polar_cache.py:69,
  * and the dense-tail concatenation of append, :114-115).

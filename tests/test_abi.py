@@ -69,6 +69,24 @@ def test_encode_argument_validation():
     assert L.tp_encode_pages(4096, 8192, 0, 1, 64, 0, 0, ctypes.byref(lay), ctypes.byref(pages), 0, None) == 0
 
 
+def test_decode_pages_gather_argument_validation():
+    """tp_decode_pages_gather (fetch_blocks' one launch) rejects a missing
+    index array, a stored-page count outside the capacity, a misaligned index
+    array and a bad output before any device access; no indices is a no-op."""
+    L = _lib.lib()
+    lay = _lib.make_layout(False, 4, 4, 64)
+    pages = _fake_pages(capacity=8)
+    g = L.tp_decode_pages_gather
+    assert g(ctypes.byref(lay), ctypes.byref(pages), 2, 4, None, 3, 4096, None, None) == _lib.TP_ERR_INVALID
+    assert b"index array" in L.tp_last_error()
+    for n_stored in (0, 9):
+        assert g(ctypes.byref(lay), ctypes.byref(pages), 2, n_stored, 4096, 3, 4096, None, None) == _lib.TP_ERR_INVALID
+        assert b"bad page range" in L.tp_last_error()
+    assert g(ctypes.byref(lay), ctypes.byref(pages), 2, 4, 4098, 3, 4096, None, None) == _lib.TP_ERR_INVALID
+    assert g(ctypes.byref(lay), ctypes.byref(pages), 2, 4, 4096, 3, 4100, None, None) == _lib.TP_ERR_INVALID
+    assert g(ctypes.byref(lay), ctypes.byref(pages), 2, 4, None, 0, None, None, None) == _lib.TP_OK
+
+
 def test_decode_attention_argument_validation():
     L = _lib.lib()
     lay = _lib.make_layout(False, 4, 4, 64)

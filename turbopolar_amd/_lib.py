@@ -99,6 +99,7 @@ _SIGNATURES = {
     "tp_default_pages_per_split": (c_i32, [c_i64, c_i32, c_i32, c_i32]),
     "tp_decode_pages": (c_i32, [_P_LAYOUT, _P_PAGES, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp]),
     "tp_decode_pages_into": (c_i32, [_P_LAYOUT, _P_PAGES, c_i64, c_i64, c_i32, c_vp, c_vp, c_i64, c_i64, c_vp]),
+    "tp_decode_pages_gather": (c_i32, [_P_LAYOUT, _P_PAGES, c_i64, c_i32, c_vp, c_i32, c_vp, c_vp, c_vp]),
     "tp_append_stage": (
         c_i32,
         [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i32, c_vp, ctypes.c_uint32, c_vp],

@@ -37,8 +37,20 @@ struct DecodeArgs {
   uint16_t* v_out;
   int64_t out_tokens;  // tokens per (batch, head) row of k_out / v_out
   int64_t out_offset;  // token of that row where page page_begin lands
+  // Gather launches (tp_decode_pages_gather): output page j is stored page
+  // page_index[j], clamped to [0, n_stored), instead of page_begin + j.
+  const int32_t* page_index;
+  int32_t n_stored;
 };
 
+// The stored page that output page `page` of a launch decodes.
+template <bool GATHER>
+__device__ __forceinline__ int64_t source_page(const DecodeArgs& a, int page) {
+  if constexpr (GATHER) return (int64_t)min(max(a.page_index[page], 0), a.n_stored - 1);
+  return a.page_begin + page;
+}
+
+template <bool GATHER>
 __global__ __launch_bounds__(256) void decode_pages_kernel(DecodeArgs a) {
   __shared__ float2 s_cs_l1[256];
   __shared__ float2 s_cs_deep[256];
@@ -50,7 +62,7 @@ __global__ __launch_bounds__(256) void decode_pages_kernel(DecodeArgs a) {
   const int tid = threadIdx.x;
   const int t = tid >> 2;
   const int qq = tid & 3;
-  const int64_t slot = bh * a.capacity + a.page_begin + page;
+  const int64_t slot = bh * a.capacity + source_page<GATHER>(a, page);
   const int64_t row = slot * kPageTokens + t;
   const int64_t out_off = (bh * a.out_tokens + a.out_offset + (int64_t)page * kPageTokens + t) * kHeadDim + 32 * qq;
 
@@ -151,7 +163,7 @@ __device__ __forceinline__ uint32_t i8pair_to_h2(uint32_t w, int first) {
 // template parameters, not branches on the pointers: a register set under a
 // branch made the compiler wait for the K loads at its join, so the V loads
 // went out one memory round trip late.
-template <int KIND, bool WANT_K, bool WANT_V>
+template <int KIND, bool WANT_K, bool WANT_V, bool GATHER = false>
 __global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
   constexpr bool kFast = KIND == kDecFast;
   constexpr int kCodes = kFast ? 256 : 16;
@@ -163,7 +175,7 @@ __global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
   const int t0 = tid >> 4;   // first token; the others are t0 + 16 k
   const int64_t bh = blockIdx.y;
   const int page = blockIdx.x;
-  const int64_t slot = bh * a.capacity + a.page_begin + page;
+  const int64_t slot = bh * a.capacity + source_page<GATHER>(a, page);
   const int64_t row0 = slot * kPageTokens;
   const int64_t out0 = bh * a.out_tokens + a.out_offset + (int64_t)page * kPageTokens;
   constexpr bool want_k = WANT_K;
@@ -249,24 +261,29 @@ __global__ __launch_bounds__(256) void decode_pages_spec_kernel(DecodeArgs a) {
 
 using namespace tp;
 
-template <int KIND>
+template <int KIND, bool GATHER>
 static void launch_spec(const DecodeArgs& a, dim3 grid, hipStream_t s) {
   if (a.k_out && a.v_out)
-    hipLaunchKernelGGL((decode_pages_spec_kernel<KIND, true, true>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((decode_pages_spec_kernel<KIND, true, true, GATHER>), grid, dim3(256), 0, s, a);
   else if (a.k_out)
-    hipLaunchKernelGGL((decode_pages_spec_kernel<KIND, true, false>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((decode_pages_spec_kernel<KIND, true, false, GATHER>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((decode_pages_spec_kernel<KIND, false, true>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((decode_pages_spec_kernel<KIND, false, true, GATHER>), grid, dim3(256), 0, s, a);
 }
 
-extern "C" int32_t tp_decode_pages_into(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
-                                        int64_t page_begin, int32_t n_pages, void* k_out, void* v_out,
-                                        int64_t out_tokens, int64_t out_offset, void* stream) {
+// Pages [page_begin, page_begin + n_pages) (page_index NULL), or the stored
+// pages page_index[0 .. n_pages) of the first n_stored (a device array), of
+// every (batch, head) row into output tokens [out_offset, out_offset + 64
+// n_pages) of rows of out_tokens tokens.
+static int32_t decode_pages_impl(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
+                                 int64_t page_begin, int32_t n_pages, const int32_t* page_index, int32_t n_stored,
+                                 void* k_out, void* v_out, int64_t out_tokens, int64_t out_offset, void* stream) {
   clear_error();
   int l1_row = 0, deep_row = 0;
   if (!check_layout(layout, &l1_row, &deep_row)) return TP_ERR_UNSUPPORTED;
   if (!pages || bh < 1 || bh > 65535 || n_pages < 0 || page_begin < 0 ||
-      page_begin + n_pages > pages->capacity) {
+      (page_index ? (n_stored < 1 || n_stored > pages->capacity || ((uintptr_t)page_index & 3u))
+                  : page_begin + n_pages > pages->capacity)) {
     set_error("bad page range");
     return TP_ERR_INVALID;
   }
@@ -309,6 +326,8 @@ extern "C" int32_t tp_decode_pages_into(const tp_page_layout* layout, const tp_p
   a.v_out = static_cast<uint16_t*>(v_out);
   a.out_tokens = out_tokens;
   a.out_offset = out_offset;
+  a.page_index = page_index;
+  a.n_stored = n_stored;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool is_default = !layout->int8_radii && layout->l1_bits == 4 && layout->deep_bits == 4 && layout->split_dim == 64;
   const bool is_fast = layout->int8_radii && layout->deep_bits == 8 && layout->split_dim == 0;
@@ -318,13 +337,46 @@ extern "C" int32_t tp_decode_pages_into(const tp_page_layout* layout, const tp_p
                        (!v_out || ((uintptr_t)pages->v_codes & 7u) == 0);
   const dim3 grid((unsigned)n_pages, (unsigned)bh);
   if ((is_default || is_fast) && aligned) {
-    if (is_default)
-      launch_spec<kDecDefault>(a, grid, s);
-    else
-      launch_spec<kDecFast>(a, grid, s);
-  } else
-    hipLaunchKernelGGL(decode_pages_kernel, grid, dim3(256), 0, s, a);
+    if (page_index) {
+      if (is_default)
+        launch_spec<kDecDefault, true>(a, grid, s);
+      else
+        launch_spec<kDecFast, true>(a, grid, s);
+    } else {
+      if (is_default)
+        launch_spec<kDecDefault, false>(a, grid, s);
+      else
+        launch_spec<kDecFast, false>(a, grid, s);
+    }
+  } else if (page_index) {
+    hipLaunchKernelGGL(decode_pages_kernel<true>, grid, dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(decode_pages_kernel<false>, grid, dim3(256), 0, s, a);
+  }
   return launch_status("tp_decode_pages");
+}
+
+extern "C" int32_t tp_decode_pages_into(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
+                                        int64_t page_begin, int32_t n_pages, void* k_out, void* v_out,
+                                        int64_t out_tokens, int64_t out_offset, void* stream) {
+  return decode_pages_impl(layout, pages, bh, page_begin, n_pages, nullptr, 0, k_out, v_out, out_tokens, out_offset,
+                           stream);
+}
+
+extern "C" int32_t tp_decode_pages_gather(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,
+                                          int32_t n_stored, const int32_t* page_index, int32_t n_index, void* k_out,
+                                          void* v_out, void* stream) {
+  if (!page_index && n_index > 0) {
+    clear_error();
+    set_error("tp_decode_pages_gather needs a page index array");
+    return TP_ERR_INVALID;
+  }
+  if (n_index == 0) {
+    clear_error();
+    return TP_OK;
+  }
+  return decode_pages_impl(layout, pages, bh, 0, n_index, page_index, n_stored, k_out, v_out,
+                           (int64_t)(n_index > 0 ? n_index : 0) * kPageTokens, 0, stream);
 }
 
 extern "C" int32_t tp_decode_pages(const tp_page_layout* layout, const tp_pages* pages, int64_t bh,

@@ -203,6 +203,28 @@ def decode_pages_into(layout, pages: TPPages, bh: int, page_begin: int, n_pages:
     check(st, "tp_decode_pages_into")
 
 
+def decode_pages_gather(layout, pages: TPPages, B: int, H: int, n_stored: int, page_index: torch.Tensor,
+                        want_k: bool = True, want_v: bool = False):
+    """tp_decode_pages_gather: the stored pages ``page_index`` (a device int32
+    tensor, every entry in [0, n_stored)) of every (batch, head) row, in that
+    order, as dense fp16 ``[B, H, len(page_index)*64, 128]`` K and/or V."""
+    if page_index.dtype != torch.int32 or page_index.dim() != 1 or not page_index.is_contiguous():
+        raise ValueError("page_index must be a contiguous 1-D int32 tensor")
+    require_hip(page_index, "page_index")
+    n = int(page_index.shape[0])
+    dev = page_index.device
+    shape = (B, H, n * PAGE, HEAD_DIM)
+    k_out = torch.empty(shape, dtype=torch.float16, device=dev) if want_k else None
+    v_out = torch.empty(shape, dtype=torch.float16, device=dev) if want_v else None
+    with on_device(dev):
+        st = lib().tp_decode_pages_gather(
+            ctypes.byref(layout), ctypes.byref(pages), B * H, int(n_stored), ptr(page_index), n, ptr(k_out),
+            ptr(v_out), stream_handle(dev),
+        )
+    check(st, "tp_decode_pages_gather")
+    return k_out, v_out
+
+
 def decode_pages(pageset: PageSet, want_k: bool = True, want_v: bool = True):
     """tp_decode_pages -> dense fp16 ``[B, H, S*64, 128]`` K and/or V."""
     B, H, S = pageset.B, pageset.H, pageset.S

@@ -25,7 +25,7 @@ import torch
 from . import _lib
 from .codecs import GroupedVQuantizer, PolarQuantDecoder, PolarQuantEncoder
 from .config import TurboPolarConfig
-from .kernels import PAGE, encode_pages
+from .kernels import PAGE, decode_pages_gather, encode_pages
 from .payload import PolarKeyBlock, QuantizedVBlock
 from .storage import PolarKBlockStorage, QuantVBlockStorage, pages_of
 
@@ -436,29 +436,36 @@ class TurboPolarKVCacheRuntime:
         return key, QuantizedVBlock(codes=codes, scales=scales, group_size=32), None, None, self.actual_seq_len
 
     def fetch_blocks(self, indices: Optional[list] = None) -> torch.Tensor:
-        """turbo_polar_cache.py:321-346: decode selected pages to dense fp16 keys."""
-        if self.k_storage.block_count == 0:
-            return torch.empty(0)
-        if indices is None:
-            indices = list(range(self.k_storage.block_count))
+        """turbo_polar_cache.py:321-346: the selected stored pages (all of
+        them by default), in the given order, decoded to dense fp16 keys
+        ``[B, H, 64 * len(indices), D]`` by one gather launch
+        (tp_decode_pages_gather) over the index list.  ``bytes_read`` grows by
+        each fetched page's key bytes (radii, both angle rows and, for int8
+        radii, the page scale), as the reference counts them per page.
+
+        An index outside [0, block_count) raises IndexError (the reference's
+        slice there is empty and its decode of it fails); an empty list
+        returns an empty tensor."""
         ks = self.k_storage
-        fetched = []
-        for idx in indices:
-            block = PolarKeyBlock(
-                radii=ks.radii[:, :, idx : idx + 1],
-                angle_codes_l1=ks.angle_codes_l1[:, :, idx : idx + 1],
-                angle_codes_deep=ks.angle_codes_deep[:, :, idx : idx + 1],
-                radii_scales=ks.radii_scales[:, :, idx : idx + 1] if ks.radii_scales is not None else None,
-                shape=(self._batch_size, self._num_kv_heads, self.config.block_size, self._head_dim),
-                block_size=self.config.block_size,
-                head_dim=self._head_dim,
-                metadata=ks.metadata,
-            )
-            self.bytes_read += _nbytes(block.radii) + _nbytes(block.angle_codes_l1) + _nbytes(block.angle_codes_deep)
-            if block.radii_scales is not None:
-                self.bytes_read += _nbytes(block.radii_scales)
-            fetched.append(self.decoder.decode_block(block))
-        return torch.cat(fetched, dim=2)
+        n = ks.block_count
+        if n == 0:
+            return torch.empty(0)
+        idx = list(range(n)) if indices is None else [int(i) for i in indices]
+        bad = [i for i in idx if not 0 <= i < n]
+        if bad:
+            raise IndexError(f"page indices {bad} outside the {n} stored pages")
+        B, H, D = self._batch_size, self._num_kv_heads, self._head_dim
+        dev = ks.radii.device
+        if not idx:
+            return torch.empty((B, H, 0, D), dtype=torch.float16, device=dev)
+        # Per stored page of every (batch, head): the same per-slice byte counts
+        # as _nbytes of the reference's one-page slices.
+        per_page = (_nbytes(ks.radii) + _nbytes(ks.angle_codes_l1) + _nbytes(ks.angle_codes_deep)
+                    + (_nbytes(ks.radii_scales) if ks.radii_scales is not None else 0)) // ks.capacity
+        page_index = torch.tensor(idx, dtype=torch.int32).to(dev, non_blocking=True)
+        k, _ = decode_pages_gather(self.polar_encoder.layout, pages_of(ks, self.v_storage), B, H, n, page_index)
+        self.bytes_read += per_page * len(idx)
+        return k
 
     def get_io_telemetry(self) -> Dict[str, Any]:
         """turbo_polar_cache.py:348-377 (same keys and closed forms)."""
