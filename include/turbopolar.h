@@ -188,6 +188,40 @@ size_t tp_decode_workspace_bytes(int64_t batch, int32_t hq, int32_t hkv, int32_t
  * workspace, zeroed once, serves calls of any shape. */
 size_t tp_decode_counter_bytes(int64_t batch, int32_t hq, int32_t hkv);
 
+/* Host-side bounds check of the decode kernels (no GPU work, no counterpart in
+ * the reference): for one launch of tp_decode_attention (kernel 0; with
+ * qjl != 0 tp_decode_attention_qjl, with dense_v != 0
+ * tp_decode_attention_dense_v) or tp_fused_qk (kernel 1) of this shape,
+ * enumerates every workgroup's, wave's and lane's global loads and stores --
+ * page fields, q, the dense tail, QJL sketches, dense V, split-K records,
+ * tickets and the output -- from the kernels' own address functions, and
+ * returns how many fall outside their buffers (msg: the first of them).
+ * Buffers take the smallest sizes the ABI admits: page fields of `capacity`
+ * slots per bh, the dense tail ending right after the last row's tail_len
+ * tokens, the workspace of tp_decode_workspace_bytes.  mutate is a test hook
+ * that plants a known fault in the enumeration only: 1 moves every lane's
+ * second V-scale dword 512 bytes on (one page's scales), 2 points a wave
+ * without a page at the next split's first page instead of its own split's. */
+typedef struct tp_bounds_case {
+  int64_t batch;
+  int32_t hq;
+  int32_t hkv;
+  tp_page_layout layout;
+  int32_t n_pages;
+  int64_t capacity;
+  int32_t tail_len;
+  int64_t tail_stride;
+  int64_t seq_len;
+  int32_t pages_per_split;
+  int32_t qjl;
+  int64_t qjl_capacity;
+  int32_t dense_v;
+  int64_t v_capacity;
+  int32_t kernel;
+  int32_t mutate;
+} tp_bounds_case;
+unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c, char* msg, int32_t msg_len);
+
 /* Pages per workgroup that tp_decode_attention uses when given 0. */
 int32_t tp_default_pages_per_split(int64_t batch, int32_t hq, int32_t hkv, int32_t n_pages);
 

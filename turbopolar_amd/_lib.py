@@ -63,6 +63,29 @@ class TPQjl(ctypes.Structure):
     ]
 
 
+class TPBoundsCase(ctypes.Structure):
+    """tp_bounds_case: one launch shape for tp_selftest_decode_bounds."""
+
+    _fields_ = [
+        ("batch", c_i64),
+        ("hq", c_i32),
+        ("hkv", c_i32),
+        ("layout", TPPageLayout),
+        ("n_pages", c_i32),
+        ("capacity", c_i64),
+        ("tail_len", c_i32),
+        ("tail_stride", c_i64),
+        ("seq_len", c_i64),
+        ("pages_per_split", c_i32),
+        ("qjl", c_i32),
+        ("qjl_capacity", c_i64),
+        ("dense_v", c_i32),
+        ("v_capacity", c_i64),
+        ("kernel", c_i32),
+        ("mutate", c_i32),
+    ]
+
+
 class TurboPolarHipError(RuntimeError):
     """A HIP runtime or launch failure inside the TurboPolar library."""
 
@@ -125,6 +148,7 @@ _SIGNATURES = {
     "tp_log_radii_rows": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "tp_selftest_f16_tables": (c_i32, [c_vp, c_vp, c_vp, c_vp]),
     "tp_selftest_fastdiv": (ctypes.c_ulonglong, [ctypes.c_uint32, c_vp]),
+    "tp_selftest_decode_bounds": (ctypes.c_ulonglong, [ctypes.POINTER(TPBoundsCase), ctypes.c_char_p, c_i32]),
     "tp_selftest_atan2_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
     "tp_selftest_div_f16_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
     "tp_selftest_vcode_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),

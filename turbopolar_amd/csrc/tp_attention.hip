@@ -32,6 +32,8 @@
 // _dense_tail (tqpolar_online_attention.metal:197-390,393-629): tokens with
 // global index >= actual_seq_len are masked, the dense fp16 tail follows the
 // pages, fp32 softmax statistics and accumulation, fp16 output.
+#include <algorithm>
+#include <cstdio>
 #include <mutex>
 #include <type_traits>
 
@@ -280,6 +282,74 @@ __device__ __forceinline__ void load_q(const AttnArgs& a, int b, int kv, int h0,
   }
 }
 
+// ---- load addresses ------------------------------------------------------------------
+//
+// Byte offsets, from each page field's base pointer, of one lane's loads of
+// page slot `slot` (slot = bkv * capacity + page), as a per-lane base plus a
+// per-load offset.  The kernels form their load pointers from these
+// functions, and the host-side bounds check (tp_selftest_decode_bounds)
+// enumerates the same functions over every lane, wave and workgroup of a
+// launch, so the check sees the kernels' own address arithmetic.
+
+__host__ __device__ inline int v_token(int ks, int l4, int e) { return 32 * ks + 4 * l4 + (e & 3) + 16 * (e >> 2); }
+
+// Key radii: default layout (fp16), the 32 bytes of pairs 16*l4 .. +15 of
+// token t = 16*mt + l16 at base + k_radii_row(t) (two 16-byte loads); fast
+// layout (int8 codes), 16 bytes at fast_radii_base + fast_row(t).
+__host__ __device__ inline int64_t k_radii_base(int64_t slot, int l4) { return (slot * (kPageTokens * kPairs) + 16 * l4) * 2; }
+__host__ __device__ inline int k_radii_row(int t) { return t * kPairs * 2; }
+// Key angle codes, default layout: 8 bytes of token t from angle_l1 (l4 < 2)
+// or angle_deep, at k_code_base + k_code_row(t).
+__host__ __device__ inline bool k_code_from_l1(int l4) { return l4 < 2; }
+__host__ __device__ inline int64_t k_code_base(int64_t slot, int l4) { return 8 * (l4 & 1) + slot * (kPageTokens * 16); }
+__host__ __device__ inline int k_code_row(int t) { return t * 16; }
+// Fast layout: int8 log radii and 8-bit angle codes share the row layout
+// (64 bytes per token): 16 bytes of token t at fast_base + fast_row(t); the
+// page's fp16 radius scale at fast_scale(slot).
+__host__ __device__ inline int64_t fast_base(int64_t slot, int l4) { return slot * (kPageTokens * kPairs) + 16 * l4; }
+__host__ __device__ inline int fast_row(int t) { return t * kPairs; }
+__host__ __device__ inline int64_t fast_scale(int64_t slot) { return slot * 2; }
+// Value codes: 8 bytes of token v_token(ks, l4, e), dims 8*l16 .. +7, at
+// v_code_base + v_code_row(ks, l4, e); the page's 512 bytes of scales as the
+// dwords `lane` and `lane + 64` at v_scale_base + 4*lane (+256).
+__host__ __device__ inline int64_t v_code_base(int64_t slot, int l16) { return slot * (kPageTokens * kHeadDim) + 8 * l16; }
+__host__ __device__ inline int v_code_row(int ks, int l4, int e) { return v_token(ks, l4, e) * kHeadDim; }
+__host__ __device__ inline int64_t v_scale_base(int64_t slot) { return slot * (kPageTokens * kVGroups) * 2; }
+// Dense fp16 V rows (tp_decode_attention_dense_v): 16 bytes of the same rows.
+__host__ __device__ inline int64_t dense_v_base(int64_t slot, int l16) { return (slot * (kPageTokens * kHeadDim) + 8 * l16) * 2; }
+__host__ __device__ inline int dense_v_row(int ks, int l4, int e) { return v_token(ks, l4, e) * kHeadDim * 2; }
+// QJL sketches of tokens 16*mt + 4*l4 .. +3: 16 bytes at qjl_sign_base +
+// 128*mt and 16 bytes after them (8 bytes per token), and the tokens' fp16
+// norms, 8 bytes at qjl_norm_base + 32*mt.
+__host__ __device__ inline int64_t qjl_sign_base(int64_t slot, int l4) { return (slot * kPageTokens + 4 * l4) * 8; }
+__host__ __device__ inline int64_t qjl_norm_base(int64_t slot, int l4) { return (slot * kPageTokens + 4 * l4) * 2; }
+
+// A wave's first page loads: a wave with a page of its own (page < p_end)
+// loads it; a wave without one issues the same loads with every lane on lane
+// 0's addresses of the split's first page (one cache line per load) instead
+// of branching around them.  The specialised layouts always have pages
+// (p_begin < n_pages).
+__host__ __device__ inline void first_page_load(int page, int p_begin, int p_end, int lane, int& p_load,
+                                                int& lane_e) {
+  const bool has_page = page < p_end;
+  p_load = has_page ? page : p_begin;
+  lane_e = has_page ? lane : 0;
+}
+
+// Split records in the workspace: record r of unit `unit` (S_area records per
+// unit, (m, l) rows of Sp_area pairs per head) holds head h's (m, l) at float
+// offset record_ml(unit, h, Sp_area, r) and its normalised output (128 fp16)
+// at half offset record_acc(unit, S_area, r, h).
+__host__ __device__ inline int64_t record_ml(int64_t unit, int h, int Sp_area, int r) {
+  return ((unit * 16 + h) * Sp_area + r) * 2;
+}
+__host__ __device__ inline int64_t record_acc(int64_t unit, int S_area, int r, int h) {
+  return ((unit * S_area + r) * 16 + h) * kHeadDim;
+}
+// The combine's record of batch position u (records r0 + u past the thread's
+// `mine` reread its last one, then weigh 0).
+__host__ __device__ inline int fold_record(int r0, int u, int mine) { return r0 + u < mine - 1 ? r0 + u : mine - 1; }
+
 // ---- QJL correction ---------------------------------------------------------------
 //
 // tqpolar_fused_qk.metal:200-231, metal.py:262-275 and score_estimate.py:6-54:
@@ -316,13 +386,13 @@ __device__ __forceinline__ void qjl_query(const AttnArgs& a, int b, int kv, int 
 // head l16) of page slot `slot`.
 __device__ __forceinline__ void qjl_correct(const AttnArgs& a, int64_t slot, int l4, uint64_t qsig, float qnorm,
                                             const float* sin_tab, float4v* s) {
-  const uint64_t* sg = a.qjl_signs + slot * kPageTokens + 4 * l4;
-  const uint16_t* nm = a.qjl_norms + slot * kPageTokens + 4 * l4;
+  const char* sg = reinterpret_cast<const char*>(a.qjl_signs) + qjl_sign_base(slot, l4);
+  const char* nm = reinterpret_cast<const char*>(a.qjl_norms) + qjl_norm_base(slot, l4);
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
-    const u32x4 w01 = *reinterpret_cast<const u32x4*>(sg + 16 * mt);
-    const u32x4 w23 = *reinterpret_cast<const u32x4*>(sg + 16 * mt + 2);
-    const uint2 nn = *reinterpret_cast<const uint2*>(nm + 16 * mt);
+    const u32x4 w01 = *reinterpret_cast<const u32x4*>(sg + 128 * mt);
+    const u32x4 w23 = *reinterpret_cast<const u32x4*>(sg + 128 * mt + 16);
+    const uint2 nn = *reinterpret_cast<const uint2*>(nm + 32 * mt);
     const uint64_t k[4] = {((uint64_t)w01.y << 32) | w01.x, ((uint64_t)w01.w << 32) | w01.z,
                            ((uint64_t)w23.y << 32) | w23.x, ((uint64_t)w23.w << 32) | w23.z};
     const float n[4] = {h2f((uint16_t)(nn.x & 0xffffu)), h2f((uint16_t)(nn.x >> 16)), h2f((uint16_t)(nn.y & 0xffffu)),
@@ -361,27 +431,27 @@ struct KRegs<kKindGeneric> {  // any layout: codes are gathered during the math
 template <int KIND>
 __device__ __forceinline__ void load_k(const AttnArgs& a, int64_t slot, int l16, int l4, KRegs<KIND>& k) {
   if constexpr (KIND == kKindDefault) {
-    const uint16_t* rbase = static_cast<const uint16_t*>(a.radii) + slot * (kPageTokens * kPairs) + 16 * l4;
-    const uint8_t* cbase = (l4 < 2 ? a.angle_l1 + 8 * l4 : a.angle_deep + 8 * (l4 - 2)) +
-                           slot * (kPageTokens * 16);
+    const char* rbase = static_cast<const char*>(a.radii) + k_radii_base(slot, l4);
+    const char* cbase = reinterpret_cast<const char*>(k_code_from_l1(l4) ? a.angle_l1 : a.angle_deep) +
+                        k_code_base(slot, l4);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int t = 16 * mt + l16;
-      const uint4* rp = reinterpret_cast<const uint4*>(rbase + t * kPairs);
+      const char* rp = rbase + k_radii_row(t);
       k.r[mt][0] = ldnt4(rp);
-      k.r[mt][1] = ldnt4(rp + 1);
-      k.c[mt] = ldnt2(cbase + t * 16);
+      k.r[mt][1] = ldnt4(rp + 16);
+      k.c[mt] = ldnt2(cbase + k_code_row(t));
     }
   } else if constexpr (KIND == kKindFast) {
-    const int8_t* rbase = static_cast<const int8_t*>(a.radii) + slot * (kPageTokens * kPairs) + 16 * l4;
-    const uint8_t* cbase = a.angle_deep + slot * (kPageTokens * kPairs) + 16 * l4;
+    const char* rbase = static_cast<const char*>(a.radii) + fast_base(slot, l4);
+    const char* cbase = reinterpret_cast<const char*>(a.angle_deep) + fast_base(slot, l4);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int t = 16 * mt + l16;
-      k.r[mt] = ldnt4(rbase + t * kPairs);
-      k.c[mt] = ldnt4(cbase + t * kPairs);
+      k.r[mt] = ldnt4(rbase + fast_row(t));
+      k.c[mt] = ldnt4(cbase + fast_row(t));
     }
-    k.ls_bits = a.radii_scales[slot];
+    k.ls_bits = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(a.radii_scales) + fast_scale(slot));
   } else {
     k.slot = slot;
   }
@@ -483,25 +553,20 @@ struct VRegs {
   uint32_t sd[2];  // dwords `lane` and `lane + 64` of the page's 128-dword scale block
 };
 
-__device__ __forceinline__ int v_token(int ks, int l4, int e) { return 32 * ks + 4 * l4 + (e & 3) + 16 * (e >> 2); }
-
 // Issues the V code loads of one page and loads its 512 bytes of scales as
 // two coalesced dwords per lane (the scale of token t, group g is half g & 1
 // of dword 2t + g / 2); PV gathers each lane's scales from these with lane
 // permutes, so the scales hold two registers, not one per token.
 __device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16, int l4, int lane, VRegs& v) {
-  const int8_t* vbase = a.v_codes + slot * (kPageTokens * kHeadDim) + 8 * l16;
+  const char* vbase = reinterpret_cast<const char*>(a.v_codes) + v_code_base(slot, l16);
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int t = v_token(ks, l4, e);
-      v.w[8 * ks + e] = ldnt2(vbase + t * kHeadDim);
-    }
+    for (int e = 0; e < 8; ++e) v.w[8 * ks + e] = ldnt2(vbase + v_code_row(ks, l4, e));
   }
-  const uint32_t* sbase = reinterpret_cast<const uint32_t*>(a.v_scales + slot * (kPageTokens * kVGroups));
-  v.sd[0] = ldnt1(sbase + lane);
-  v.sd[1] = ldnt1(sbase + lane + 64);
+  const char* sbase = reinterpret_cast<const char*>(a.v_scales) + v_scale_base(slot);
+  v.sd[0] = ldnt1(sbase + 4 * lane);
+  v.sd[1] = ldnt1(sbase + 4 * (lane + 64));
 }
 
 // acc[j] += Vhat^T tile j x P, Vhat = f16(code * scale) exactly: codes become
@@ -637,12 +702,12 @@ struct DenseVRegs {
 
 __device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16, int l4, int lane, DenseVRegs& v) {
   (void)lane;
-  const uint16_t* vbase = a.v_dense + slot * (kPageTokens * kHeadDim) + 8 * l16;
+  const char* vbase = reinterpret_cast<const char*>(a.v_dense) + dense_v_base(slot, l16);
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const uint4 w = ldnt4(vbase + v_token(ks, l4, e) * kHeadDim);
+      const uint4 w = ldnt4(vbase + dense_v_row(ks, l4, e));
       v.w[8 * ks + e] = u32x4{w.x, w.y, w.z, w.w};
     }
   }
@@ -845,12 +910,9 @@ __device__ __forceinline__ void fold_records(const float* pml, const uint16_t* p
   for (int r0 = 0; r0 < mine; r0 += B) {
     float2 r[B];
     uint4 x[B];
-    const float2 mlk = *reinterpret_cast<const float2*>(pml + 2 * SG * min(r0 + (lane & (B - 1)), mine - 1));
+    const float2 mlk = *reinterpret_cast<const float2*>(pml + 2 * SG * fold_record(r0, lane & (B - 1), mine));
 #pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const int ru = min(r0 + u, mine - 1);
-      x[u] = *reinterpret_cast<const uint4*>(pac + ru * rstride);
-    }
+    for (int u = 0; u < B; ++u) x[u] = *reinterpret_cast<const uint4*>(pac + fold_record(r0, u, mine) * rstride);
     if (r0 == 0) TP_STAMP(61);
 #pragma unroll
     for (int u = 0; u < B; ++u) {
@@ -937,7 +999,7 @@ struct CombineItem {
   bool item;
 };
 
-__device__ __forceinline__ CombineItem combine_item(int tid, int nh, int waves) {
+__host__ __device__ inline CombineItem combine_item(int tid, int nh, int waves) {
   CombineItem c;
   const int n_items = nh * 16;
   c.ish = n_items <= 32 ? 5 : (n_items <= 64 ? 6 : (n_items <= 128 ? 7 : 8));
@@ -967,8 +1029,8 @@ __device__ __forceinline__ void combine_records(Merge& sh, const CombineItem& ci
   const int SG = 1 << lsg;
   const bool active = ci.item;
   const int mine = active ? (count - ci.sg + SG - 1) >> lsg : 0;
-  const uint16_t* pac = part_acc + ((unit * S_area + first + ci.sg) * 16 + ci.hh) * kHeadDim + 8 * ci.c8;
-  const float* pml = part_ml + ((unit * 16 + ci.hh) * Sp_area + first + ci.sg) * 2;
+  const uint16_t* pac = part_acc + record_acc(unit, S_area, first + ci.sg, ci.hh) + 8 * ci.c8;
+  const float* pml = part_ml + record_ml(unit, ci.hh, Sp_area, first + ci.sg);
   const int64_t rstride = (int64_t)SG * 16 * kHeadDim;
   TP_STAMP(65);
   TP_STAMP(66);
@@ -1060,9 +1122,8 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
   const int S = a.n_splits;
   const int Sp = (S + 1) & ~1;  // (m, l) row length in pairs
   if (live) {
-    if (d0 == 0) st_agent2(a.part_ml + ((unit * 16 + h) * Sp + split) * 2, M, L);
-    st_agent_h4(a.part_acc + ((unit * S + split) * 16 + h) * kHeadDim + d0, float4v{A[0], A[1], A[2], A[3]},
-                record_inv(L));
+    if (d0 == 0) st_agent2(a.part_ml + record_ml(unit, h, Sp, split), M, L);
+    st_agent_h4(a.part_acc + record_acc(unit, S, split, h) + d0, float4v{A[0], A[1], A[2], A[3]}, record_inv(L));
   }
   TP_STAMP(53);
   wait_stores();
@@ -1095,9 +1156,9 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
     const int G = a.tier_groups;
     const int Gp = (G + 1) & ~1;
     if (ci.sg == 0 && ci.item) {
-      if (ci.c8 == 0) st_agent2(a.tier_ml + ((unit * 16 + ci.hh) * Gp + grp) * 2, Mc, Lc);
+      if (ci.c8 == 0) st_agent2(a.tier_ml + record_ml(unit, ci.hh, Gp, grp), Mc, Lc);
       const float inv = record_inv(Lc);
-      uint16_t* trow = a.tier_acc + ((unit * G + grp) * 16 + ci.hh) * kHeadDim + 8 * ci.c8;
+      uint16_t* trow = a.tier_acc + record_acc(unit, G, grp, ci.hh) + 8 * ci.c8;
       st_agent_h4(trow, Ac.lo, inv);
       st_agent_h4(trow + 4, Ac.hi, inv);
     }
@@ -1195,9 +1256,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     // of branching around them: a load under a branch would make the
     // compiler's wait counting treat Q as the newest load, so every QK would
     // wait for all loads in flight.
-    const bool has_page = page < p_end;
-    const int p_load = has_page ? page : p_begin;
-    const int lane_e = has_page ? lane : 0;
+    int p_load, lane_e;
+    first_page_load(page, p_begin, p_end, lane, p_load, lane_e);
     load_k<KIND>(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, kr);
     if constexpr (DV)
       load_v(a, bkv * a.v_capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
@@ -2125,6 +2185,303 @@ int32_t tp_decode_attention_dense_v(const void* q, int64_t batch, int32_t hq, in
 }
 
 }  // extern "C"
+
+// ---- host-side bounds check of the decode kernels' memory accesses ----------------------
+//
+// tp_selftest_decode_bounds enumerates, for every workgroup, wave and lane of
+// one launch, the byte range of every global load and store of
+// decode_attention_kernel (or fused_qk_kernel) from the address functions
+// the kernels themselves use (k_radii_base ... record_acc, first_page_load,
+// combine_item, fold_record), and counts the ranges outside their buffers.
+// Buffers take the smallest sizes the C ABI admits for the shape: page fields
+// of `capacity` slots per (batch, kv head), the dense tail ending right after
+// the last row's tail_len tokens, the workspace of tp_decode_workspace_bytes.
+// Loads through bounded raw buffer resources (q, the dense tail) are checked
+// by their resource's range.  No GPU work.
+
+namespace {
+
+struct BoundsLog {
+  unsigned long long bad = 0;
+  unsigned long long checked = 0;
+  char first[512] = {0};
+  void check(const char* what, int64_t off, int64_t bytes, int64_t size, int lin, int wave, int lane) {
+    ++checked;
+    if (off >= 0 && off + bytes <= size) return;
+    if (!bad)
+      snprintf(first, sizeof(first), "%s: bytes [%lld, %lld) outside a %lld-byte buffer (workgroup %d, wave %d, lane %d)",
+               what, (long long)off, (long long)(off + bytes), (long long)size, lin, wave, lane);
+    ++bad;
+  }
+};
+
+}  // namespace
+
+extern "C" unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c, char* msg, int32_t msg_len) {
+  BoundsLog log;
+  if (msg && msg_len > 0) msg[0] = 0;
+  int l1_row = 0, deep_row = 0;
+  if (!c || !check_layout(&c->layout, &l1_row, &deep_row) || c->batch < 1 || c->hq < 1 || c->hkv < 1 ||
+      c->hq % c->hkv || c->n_pages < 1 || c->capacity < c->n_pages || c->seq_len < 1) {
+    if (msg && msg_len > 0) snprintf(msg, msg_len, "bad case");
+    return ~0ull;
+  }
+  const int kind = layout_kind(&c->layout);
+  const int64_t BH = c->batch * c->hkv;
+  const int g = c->hq / c->hkv;
+  const int head_blocks = head_blocks_of(c->hq, c->hkv);
+  const int n_pages = c->n_pages;
+  const int64_t cap = c->capacity;
+  const bool int8r = c->layout.int8_radii != 0;
+  const int pps = c->pages_per_split > 0 ? c->pages_per_split
+                                         : tp_default_pages_per_split(c->batch, c->hq, c->hkv, n_pages);
+  const int S = n_splits_of(n_pages, pps);
+  const int64_t units = BH * head_blocks;
+  const int64_t total = (int64_t)n_pages * kPageTokens + c->tail_len;
+  const int64_t seq = std::min(c->seq_len, total);
+  // Buffer sizes in bytes.
+  const int64_t sz_q = c->batch * c->hq * kHeadDim * 2;
+  const int64_t sz_out = sz_q;
+  const int64_t sz_radii = BH * cap * kPageTokens * kPairs * (int8r ? 1 : 2);
+  const int64_t sz_rs = BH * cap * 2;
+  const int64_t sz_l1 = BH * cap * kPageTokens * l1_row;
+  const int64_t sz_deep = BH * cap * kPageTokens * deep_row;
+  const int64_t sz_vc = BH * cap * kPageTokens * kHeadDim;
+  const int64_t sz_vs = BH * cap * kPageTokens * kVGroups * 2;
+  const int64_t sz_dv = BH * c->v_capacity * kPageTokens * kHeadDim * 2;
+  const int64_t sz_tail = c->tail_len > 0 ? ((BH - 1) * c->tail_stride + c->tail_len) * kHeadDim * 2 : 0;
+  const int64_t sz_sig = BH * c->qjl_capacity * kPageTokens * 8;
+  const int64_t sz_nrm = BH * c->qjl_capacity * kPageTokens * 2;
+  const int64_t sz_qs = c->batch * c->hq * 8;
+
+  // One lane's loads of page `page` (lane addresses of lane_e), as the kernels issue them.
+  auto page_loads = [&](int lin, int wave, int lane, int64_t bkv, int page, int lane_e) {
+    const int64_t slot = bkv * cap + page;
+    const int l16 = lane_e & 15, l4 = lane_e >> 4;
+    if (kind == kKindDefault) {
+      for (int mt = 0; mt < 4; ++mt) {
+        const int t = 16 * mt + l16;
+        log.check("radii", k_radii_base(slot, l4) + k_radii_row(t), 32, sz_radii, lin, wave, lane);
+        log.check(k_code_from_l1(l4) ? "angle_l1" : "angle_deep", k_code_base(slot, l4) + k_code_row(t), 8,
+                  k_code_from_l1(l4) ? sz_l1 : sz_deep, lin, wave, lane);
+      }
+    } else if (kind == kKindFast) {
+      for (int mt = 0; mt < 4; ++mt) {
+        const int t = 16 * mt + l16;
+        log.check("radii", fast_base(slot, l4) + fast_row(t), 16, sz_radii, lin, wave, lane);
+        log.check("angle_deep", fast_base(slot, l4) + fast_row(t), 16, sz_deep, lin, wave, lane);
+      }
+      log.check("radii_scales", fast_scale(slot), 2, sz_rs, lin, wave, lane);
+    }
+    if (c->dense_v) {
+      for (int ks = 0; ks < 2; ++ks)
+        for (int e = 0; e < 8; ++e)
+          log.check("dense V", dense_v_base(bkv * c->v_capacity + page, l16) + dense_v_row(ks, l4, e), 16, sz_dv, lin,
+                    wave, lane);
+    } else {
+      for (int ks = 0; ks < 2; ++ks)
+        for (int e = 0; e < 8; ++e)
+          log.check("v_codes", v_code_base(slot, l16) + v_code_row(ks, l4, e), 8, sz_vc, lin, wave, lane);
+      const int64_t sb = v_scale_base(slot);
+      log.check("v_scales", sb + 4 * lane_e, 4, sz_vs, lin, wave, lane);
+      log.check("v_scales", sb + 4 * (lane_e + 64) + (c->mutate == 1 ? 512 : 0), 4, sz_vs, lin, wave, lane);
+    }
+  };
+  // The generic layout's codes, gathered during the math of a page it owns.
+  auto generic_loads = [&](int lin, int wave, int lane, int64_t bkv, int page) {
+    const int64_t slot = bkv * cap + page;
+    const int l16 = lane & 15, l4 = lane >> 4;
+    const int split_half = c->layout.split_dim / 2;
+    if (int8r) log.check("radii_scales", slot * 2, 2, sz_rs, lin, wave, lane);
+    for (int mt = 0; mt < 4; ++mt) {
+      const int64_t row = slot * kPageTokens + 16 * mt + l16;
+      for (int kk = 0; kk < 4; ++kk)
+        for (int i = 0; i < 4; ++i) {
+          const int p = 16 * l4 + 4 * kk + i;
+          log.check("radii", (row * kPairs + p) * (int8r ? 1 : 2), int8r ? 1 : 2, sz_radii, lin, wave, lane);
+          if (p < split_half)
+            log.check("angle_l1", row * l1_row + (p * c->layout.l1_bits) / 8, 1, sz_l1, lin, wave, lane);
+          else
+            log.check("angle_deep", row * deep_row + ((p - split_half) * c->layout.deep_bits) / 8, 1, sz_deep, lin, wave,
+                      lane);
+        }
+    }
+  };
+
+  if (c->kernel == 1) {  // fused_qk_kernel: one page per wave, the last page reloaded past n_pages
+    const int gx = (n_pages + kQkWaves - 1) / kQkWaves;
+    for (int64_t bkv = 0; bkv < BH; ++bkv)
+      for (int hb = 0; hb < head_blocks; ++hb)
+        for (int bx = 0; bx < gx; ++bx)
+          for (int wave = 0; wave < kQkWaves; ++wave)
+            for (int lane = 0; lane < 64; ++lane) {
+              const int page = bx * kQkWaves + wave;
+              const int b = (int)(bkv / c->hkv), kv = (int)(bkv % c->hkv), h0 = hb * 16, nh = std::min(16, g - h0);
+              const int lin = (int)((bkv * head_blocks + hb) * gx + bx);
+              log.check("q (buffer range)", ((int64_t)b * c->hq + (int64_t)kv * g + h0) * kHeadDim * 2,
+                        (int64_t)nh * kHeadDim * 2, sz_q, lin, wave, lane);
+              if (kind != kKindGeneric) {
+                const int64_t slot_page = std::min(page, n_pages - 1);
+                const int l16 = lane & 15, l4 = lane >> 4;
+                const int64_t slot = bkv * cap + slot_page;
+                for (int mt = 0; mt < 4; ++mt) {
+                  const int t = 16 * mt + l16;
+                  if (kind == kKindDefault) {
+                    log.check("radii", k_radii_base(slot, l4) + k_radii_row(t), 32, sz_radii, lin, wave, lane);
+                    log.check("angle codes", k_code_base(slot, l4) + k_code_row(t), 8,
+                              k_code_from_l1(l4) ? sz_l1 : sz_deep, lin, wave, lane);
+                  } else {
+                    log.check("radii", fast_base(slot, l4) + fast_row(t), 16, sz_radii, lin, wave, lane);
+                    log.check("angle_deep", fast_base(slot, l4) + fast_row(t), 16, sz_deep, lin, wave, lane);
+                  }
+                }
+              } else if (page < n_pages) {
+                generic_loads(lin, wave, lane, bkv, page);
+              }
+              if (page < n_pages) {
+                const int64_t sz_scores = c->batch * c->hq * (int64_t)n_pages * kPageTokens * 2;
+                for (int r0 = 0; r0 < 16; r0 += 8) {
+                  const int h = r0 + (lane >> 3), cc = lane & 7;
+                  if (h < nh)
+                    log.check("scores",
+                              ((((int64_t)b * c->hq + (int64_t)kv * g + h0) * n_pages * kPageTokens +
+                                (int64_t)page * kPageTokens) + (int64_t)h * n_pages * kPageTokens + 8 * cc) * 2,
+                              16, sz_scores, lin, wave, lane);
+                }
+              }
+            }
+  } else {  // decode_attention_kernel
+    AttnArgs a{};
+    a.g = g;
+    a.pages_per_split = pps;
+    const int waves = four_waves(a) ? 4 : kDecodeWaves;
+    const Tiers tiers = S > 1 ? tiers_of(units, S) : Tiers{0, 0};
+    const int slots = 1 + tiers.groups;
+    const int32_t cstride = counter_stride_of(units * slots);
+    const int64_t sz_ws = S > 1 ? (int64_t)tp_decode_workspace_bytes(c->batch, c->hq, c->hkv, n_pages, c->tail_len, pps) : 0;
+    const int64_t cbytes = (int64_t)tp_decode_counter_bytes(c->batch, c->hq, c->hkv);
+    const int Sp = (S + 1) & ~1;
+    const int64_t ml_off = cbytes;
+    const int64_t acc_off = ml_off + (int64_t)align256(units * 16 * Sp * 2 * sizeof(float));
+    const int64_t tml_off = acc_off + (int64_t)align256(units * S * 16 * kHeadDim * 2);
+    const int G = tiers.groups;
+    const int Gp = (G + 1) & ~1;
+    const int64_t tacc_off = tml_off + (int64_t)align256(units * 16 * Gp * 2 * sizeof(float));
+    const int64_t live_pages = (seq + kPageTokens - 1) / kPageTokens;
+    // The combine of records first .. first+count-1 of an area, by every thread of one workgroup.
+    auto combine_loads = [&](int lin, int64_t unit, int nh, int64_t mlb, int64_t acb, int S_area, int Sp_area,
+                             int first, int count) {
+      for (int tid = 0; tid < waves * 64; ++tid) {
+        const CombineItem ci = combine_item(tid, nh, waves);
+        const int SG = 1 << ci.lsg;
+        const int mine = ci.item ? (count - ci.sg + SG - 1) >> ci.lsg : 0;
+        const int B = ((count + SG - 1) >> ci.lsg) <= 4 ? 4 : 8;
+        const int lane = tid & 63;
+        for (int r0 = 0; r0 < mine; r0 += B) {
+          log.check("records (m, l)",
+                    mlb + (record_ml(unit, ci.hh, Sp_area, first + ci.sg) + 2 * SG * fold_record(r0, lane & (B - 1), mine)) * 4,
+                    8, sz_ws, lin, tid >> 6, lane);
+          for (int u = 0; u < B; ++u)
+            log.check("records o",
+                      acb + (record_acc(unit, S_area, first + ci.sg, ci.hh) + 8 * ci.c8 +
+                             (int64_t)fold_record(r0, u, mine) * SG * 16 * kHeadDim) * 2,
+                      16, sz_ws, lin, tid >> 6, lane);
+        }
+      }
+    };
+    for (int64_t lin = 0; lin < (int64_t)S * units; ++lin) {
+      const int split = (int)(lin / units);
+      const int64_t unit = lin % units;
+      const int64_t bkv = unit / head_blocks;
+      const int hb = (int)(unit % head_blocks);
+      const int b = (int)(bkv / c->hkv), kv = (int)(bkv % c->hkv);
+      const int h0 = hb * 16, nh = std::min(16, g - h0);
+      const int p_begin = split * pps;
+      const int p_end = (int)std::min<int64_t>(std::min(p_begin + pps, n_pages), live_pages);
+      const int L = (int)lin;
+      for (int wave = 0; wave < waves; ++wave)
+        for (int lane = 0; lane < 64; ++lane) {
+          const int l16 = lane & 15;
+          log.check("q (buffer range)", ((int64_t)b * c->hq + (int64_t)kv * g + h0) * kHeadDim * 2,
+                    (int64_t)nh * kHeadDim * 2, sz_q, L, wave, lane);
+          int page = p_begin + wave;
+          if (kind == kKindGeneric) {
+            for (; page < p_end; page += waves) {
+              generic_loads(L, wave, lane, bkv, page);
+              page_loads(L, wave, lane, bkv, page, lane);
+            }
+          } else {
+            int p_load, lane_e;
+            first_page_load(page, p_begin, p_end, lane, p_load, lane_e);
+            if (c->mutate == 2 && page >= p_end) p_load = p_begin + pps;  // the no-page load moved one split on
+            page_loads(L, wave, lane, bkv, p_load, lane_e);
+            for (; page + waves < p_end; page += waves) page_loads(L, wave, lane, bkv, page + waves, lane);
+          }
+          if (c->qjl) {
+            for (int pg = p_begin + wave; pg < p_end; pg += waves) {
+              const int64_t qslot = bkv * c->qjl_capacity + pg;
+              const int l4 = lane >> 4;
+              for (int mt = 0; mt < 4; ++mt) {
+                log.check("qjl signs", qjl_sign_base(qslot, l4) + 128 * mt, 32, sz_sig, L, wave, lane);
+                log.check("qjl norms", qjl_norm_base(qslot, l4) + 32 * mt, 8, sz_nrm, L, wave, lane);
+              }
+            }
+            log.check("q signs", ((int64_t)b * c->hq + (int64_t)kv * g + h0 + std::min(l16, nh - 1)) * 8, 8, sz_qs, L,
+                      wave, lane);
+          }
+          if (split == S - 1 && c->tail_len > 0 && wave == std::max(p_end - p_begin, 0) % waves &&
+              std::min<int64_t>(c->tail_len, seq - (int64_t)n_pages * kPageTokens) > 0)
+            log.check("tail (buffer range)", bkv * c->tail_stride * kHeadDim * 2, (int64_t)c->tail_len * kHeadDim * 2,
+                      sz_tail, L, wave, lane);
+        }
+      // The fold's record (or, with one split, output) stores: thread t, head t/32, dims 4(t%32)..+3.
+      for (int tid = 0; tid < waves * 64; ++tid) {
+        const int h = tid >> 5, d0 = (tid & 31) << 2;
+        if (h >= nh) continue;
+        if (S == 1) {
+          log.check("out", (((int64_t)b * c->hq + (int64_t)kv * g + h0 + h) * kHeadDim + d0) * 2, 8, sz_out, L, tid >> 6,
+                    tid & 63);
+          continue;
+        }
+        if (d0 == 0) log.check("record (m, l)", ml_off + record_ml(unit, h, Sp, split) * 4, 8, sz_ws, L, tid >> 6, tid & 63);
+        log.check("record o", acc_off + (record_acc(unit, S, split, h) + d0) * 2, 8, sz_ws, L, tid >> 6, tid & 63);
+      }
+      if (S > 1) {
+        const int T = tiers.splits;
+        const int grp = T > 0 ? split / T : 0;
+        const int64_t ctr = unit * slots * cstride;
+        log.check("ticket", (ctr + (T > 0 ? (1 + grp) * cstride : 0)) * 4, 4, cbytes, L, 0, 0);
+        const bool group_last = T > 0 ? split == std::min(S, (grp + 1) * T) - 1 : split == S - 1;
+        if (group_last) {  // any workgroup may combine; its loads are the same, so check once per group
+          const int first = grp * T;
+          const int count = T > 0 ? std::min(T, S - first) : S;
+          combine_loads(L, unit, nh, ml_off, acc_off, S, Sp, first, count);
+          if (T > 0) {
+            for (int tid = 0; tid < waves * 64; ++tid) {
+              const CombineItem ci = combine_item(tid, nh, waves);
+              if (ci.sg != 0 || !ci.item) continue;
+              if (ci.c8 == 0)
+                log.check("group record (m, l)", tml_off + record_ml(unit, ci.hh, Gp, grp) * 4, 8, sz_ws, L, tid >> 6,
+                          tid & 63);
+              log.check("group record o", tacc_off + (record_acc(unit, G, grp, ci.hh) + 8 * ci.c8) * 2, 16, sz_ws, L,
+                        tid >> 6, tid & 63);
+            }
+            log.check("unit ticket", ctr * 4, 4, cbytes, L, 0, 0);
+            if (grp == G - 1) combine_loads(L, unit, nh, tml_off, tacc_off, G, Gp, 0, G);
+          }
+          for (int tid = 0; tid < waves * 64; ++tid) {
+            const CombineItem ci = combine_item(tid, nh, waves);
+            if (ci.sg == 0 && ci.item)
+              log.check("out", (((int64_t)b * c->hq + (int64_t)kv * g + h0 + ci.hh) * kHeadDim + 8 * ci.c8) * 2, 16,
+                        sz_out, L, tid >> 6, tid & 63);
+          }
+        }
+      }
+    }
+  }
+  if (msg && msg_len > 0) snprintf(msg, msg_len, "%s", log.first);
+  return log.bad;
+}
 
 // ---- entry point that allocates nothing -----------------------------------------
 //
