@@ -217,8 +217,10 @@ __device__ __forceinline__ int32_t to_int8_rne(float q) {
 }
 
 // Angle of a code, as PolarQuantDecoder computes it (decoder.py:37-55):
-// f32(code)/f32(levels-1) * f32(2*pi) - f32(pi), three separate fp32 ops.
+// f32(code)/f32(levels-1) * f32(2*pi) - f32(pi), three separate fp32 ops
+// (never contracted, also in sources compiled with FMA contraction).
 __device__ __forceinline__ float code_angle(uint32_t code, int bits) {
+#pragma clang fp contract(off)
   const float n = (float)code / (float)((1 << bits) - 1);
   const float t = n * kF32TwoPi;
   return t - kF32Pi;
