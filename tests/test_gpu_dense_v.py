@@ -84,6 +84,26 @@ def test_dense_v_matches_oracle(device, layout_name, hq, hkv, S, pps, masked, B,
     _check(out.float().cpu().numpy(), ref, "dense_v")
 
 
+@pytest.mark.parametrize("pps", [0, 1, 2])
+def test_dense_v_nonfinite_masked_rows_add_nothing(device, pps):
+    """Rows of masked tokens on the last live page and the page slots past the
+    key block hold NaN and inf: the output equals the oracle's over the valid
+    rows (masked tokens weigh 0 and their V rows add nothing, as the
+    reference's kernel skips them)."""
+    S, masked = 5, 23
+    block, _, host, _, _, q = build_case(device, LAYOUTS["default"], 32, 8, S, 0, seed=44)
+    vd = _dense_v(45, 1, 8, S, S + 2)
+    ref = oracle.cpu_online_attention_dense_v(q, _blk(host), vd[:, :, :S], SCALE16, S * PAGE - masked)
+    vd[:, :, S - 1, PAGE - masked:PAGE - masked + 11] = np.nan
+    vd[:, :, S - 1, PAGE - masked + 11:] = np.inf
+    vd[:, :, S:] = np.nan
+    out = kernels.decode_attention_dense_v(torch.from_numpy(q).to(device), PageSet(block, None),
+                                           torch.from_numpy(vd).to(device), S * PAGE - masked, SCALE16,
+                                           pages_per_split=pps)
+    torch.cuda.synchronize()
+    _check(out.float().cpu().numpy(), ref, "dense_v with non-finite masked rows")
+
+
 def test_dense_v_reads_dense_rows_not_quantised_pages(device):
     """The same key block with its quantised V and with dense V: the dense
     result follows the dense oracle, which differs from the quantised one."""

@@ -2,9 +2,11 @@
 
 bench.py --variant times these variants of the decode kernel beside the product
 kernel (libturbopolar_hip_timeline.so, tp_measure_set_decode_variant): the
-product kernel with an agent-scope release fence before the split ticket, and
-the kernel with QK and PV on the VALU instead of MFMA (default layout, 4 or 8
-query heads per kv head, no tail).  A timing of a variant is evidence only if
+product kernel with an agent-scope release fence before the split ticket, or
+without the combining workgroup's acquire fence, on the product's workgroup
+size (4 waves for splits of at most 8 pages, else 8), and the kernel with QK
+and PV on the VALU instead of MFMA (default layout, 4 or 8 query heads per kv
+head, no tail).  A timing of a variant is evidence only if
 the variant computes the same attention: each is checked here against
 oracle.cpu_online_attention_dense_tail (metal.py:293-332) at the same bar as
 the product kernel (max-abs 2e-3, relative L2 1e-3), with several splits, a
@@ -24,7 +26,7 @@ from turbopolar_amd.kernels import PageSet
 
 pytestmark = pytest.mark.gpu
 
-VARIANT = {"release": 1, "valu": 2, "valu+release": 3}
+VARIANT = {"release": 1, "valu": 2, "valu+release": 3, "no-acquire": 4}
 
 
 @pytest.fixture(scope="module")
@@ -62,6 +64,10 @@ CASES = [
     ("valu+release", "default", 64, 8, 6, 2, 5, 1),
     ("release", "default", 32, 8, 5, 2, 0, 1),
     ("release", "fast", 64, 8, 6, 2, 9, 2),
+    ("release", "default", 32, 8, 40, 16, 0, 1),     # 16-page splits: 8-wave workgroups
+    ("no-acquire", "default", 32, 8, 9, 4, 21, 1),   # 4-wave workgroups
+    ("no-acquire", "fast", 64, 8, 6, 2, 9, 2),
+    ("no-acquire", "default", 32, 8, 40, 16, 3, 1),
 ]
 
 

@@ -1313,6 +1313,21 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     const int valid = (int)min((int64_t)kPageTokens, a.seq_len - (int64_t)page * kPageTokens);
     half8v pb[2];
     softmax_page(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
+    if constexpr (DV) {
+      // Dense V rows of masked tokens get P = 0, but 0 * NaN is NaN in the
+      // MFMA: rows at or past `valid` are zeroed, so whatever a caller's
+      // buffer holds there adds nothing (the reference skips those tokens in
+      // its V sum, tqpolar_online_attention.metal:10-196).
+      if (valid < kPageTokens) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            if (v_token(ks, l4, e) >= valid) vr.w[8 * ks + e] = u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+      }
+    }
     pv_regs(vr, sbase4, ssel, pb, acc);
   }
 
@@ -1340,292 +1355,6 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   finish_unit<WAVES, FL>(sh, a, wave, tid, m_run, l_run, acc, b, kv, h0, nh, bkv, hb, split);
 }
 
-#ifdef TP_TIMELINE
-// ---- measurement variants ------------------------------------------------------------
-//
-// Built into the measurement library only (never into the product library):
-// the decode kernel above with its end-phase variant flags (kFlRelease,
-// kFlNoAcquire), and decode_attention_valu_kernel, the default-layout kernel
-// with QK and PV on the VALU (packed fp16 dot products v_dot2_f32_f16, fp32
-// accumulation) instead of MFMA, for blocks of exactly NHV = 4 or 8 query
-// heads and no dense tail.  Page loads, K decode, V dequantisation, the
-// online-softmax rules and the end phase are the product kernel's.
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
-}
-// Max / sum over the 16 lanes of a row (DPP xor 1, xor 2, half-row mirror,
-// row mirror); every lane of the row ends with the same bits.
-__device__ __forceinline__ float row_max16(float x) {
-  x = fmaxf(x, dpp_f<0xB1>(x));
-  x = fmaxf(x, dpp_f<0x4E>(x));
-  x = fmaxf(x, dpp_f<0x141>(x));
-  return fmaxf(x, dpp_f<0x140>(x));
-}
-__device__ __forceinline__ float row_sum16(float x) {
-  x = x + dpp_f<0xB1>(x);
-  x = x + dpp_f<0x4E>(x);
-  x = x + dpp_f<0x141>(x);
-  return x + dpp_f<0x140>(x);
-}
-// Sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four rows), same bits in all four.
-__device__ __forceinline__ float sum_over_rows(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(c[0]) + __uint_as_float(c[1]);
-}
-
-// QK on the VALU: s[mt][h] = score(token 16*mt + l16, head h), every row of
-// the wave holding all of them.  Lane (l16, l4) decodes the 32 dims 32*l4 ..
-// of its four tokens as the MFMA path does and dots them with q rows read
-// from LDS (qs[16 h + c] = q[h][8c .. 8c+7]); the four rows' partial dots are
-// summed across rows.
-// A zero the compiler cannot see through.  With 8 heads the q rows (128
-// registers) do not fit beside the page registers: offsetting their LDS reads
-// by it in every page keeps them from being hoisted out of the page loop.
-__device__ __forceinline__ int opaque_zero() {
-  int z;
-  asm volatile("s_mov_b32 %0, 0" : "=s"(z));
-  return z;
-}
-
-template <int NHV>
-__device__ __forceinline__ void qk_valu(const Lut& lut, const KRegs<kKindDefault>& k, const uint4* qs, int l4,
-                                        float (&s)[4][NHV]) {
-  if constexpr (NHV > 4) qs += opaque_zero();
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-    for (int h = 0; h < NHV; ++h) s[mt][h] = 0.0f;
-  }
-  // k-step outer: the q rows of one k-step (4 registers per head) are live at a time.
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    uint4 qw[NHV];
-#pragma unroll
-    for (int h = 0; h < NHV; ++h) qw[h] = qs[16 * h + 4 * l4 + kk];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const uint32_t r0 = kk < 2 ? (kk == 0 ? k.r[mt][0].x : k.r[mt][0].z) : (kk == 2 ? k.r[mt][1].x : k.r[mt][1].z);
-      const uint32_t r1 = kk < 2 ? (kk == 0 ? k.r[mt][0].y : k.r[mt][0].w) : (kk == 2 ? k.r[mt][1].y : k.r[mt][1].w);
-      const uint32_t cw = kk < 2 ? k.c[mt].x : k.c[mt].y;
-      // Code bytes 2kk and 2kk+1 hold the nibbles of pairs 4kk .. 4kk+3.
-      const uint32_t b0 = (cw >> (16 * (kk & 1))) & 0xffu;
-      const uint32_t b1 = (cw >> (16 * (kk & 1) + 8)) & 0xffu;
-      const uint2 cs01 = lut.pair[b0];
-      const uint2 cs23 = lut.pair[b1];
-      const half2v e0 = lo_lo(r0) * __builtin_bit_cast(half2v, cs01.x);
-      const half2v e1 = hi_hi(r0) * __builtin_bit_cast(half2v, cs01.y);
-      const half2v e2 = lo_lo(r1) * __builtin_bit_cast(half2v, cs23.x);
-      const half2v e3 = hi_hi(r1) * __builtin_bit_cast(half2v, cs23.y);
-#pragma unroll
-      for (int h = 0; h < NHV; ++h) {
-        float x = s[mt][h];
-        x = __builtin_amdgcn_fdot2(e0, __builtin_bit_cast(half2v, qw[h].x), x, false);
-        x = __builtin_amdgcn_fdot2(e1, __builtin_bit_cast(half2v, qw[h].y), x, false);
-        x = __builtin_amdgcn_fdot2(e2, __builtin_bit_cast(half2v, qw[h].z), x, false);
-        x = __builtin_amdgcn_fdot2(e3, __builtin_bit_cast(half2v, qw[h].w), x, false);
-        s[mt][h] = x;
-      }
-    }
-  }
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-    for (int h = 0; h < NHV; ++h) s[mt][h] = sum_over_rows(s[mt][h]);
-  }
-}
-
-// Online softmax of one page on the VALU layout (same rules as softmax_page);
-// P goes out as fp16 pairs of heads: pp[mt][i] = (P(t, 2i), P(t, 2i+1)) of
-// token t = 16*mt + l16.  l_run[h] sums the lane's own four tokens.
-template <int NHV>
-__device__ __forceinline__ void softmax_valu(const float (&s)[4][NHV], int valid, float scale_log2, int l16,
-                                             float (&m_run)[NHV], float (&l_run)[NHV], float (&acc)[NHV][8],
-                                             uint32_t (&pp)[4][NHV / 2]) {
-  f16 ph[4][NHV];
-#pragma unroll
-  for (int h = 0; h < NHV; ++h) {
-    float x[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      x[mt] = s[mt][h] * scale_log2;
-      if (16 * mt + l16 >= valid) x[mt] = -INFINITY;
-    }
-    const float pm = row_max16(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
-    if (__builtin_amdgcn_ballot_w64(pm > m_run[h] + kLazyRescale)) {
-      const float m_new = fmaxf(m_run[h], pm);
-      const float alpha = m_run[h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[h] - m_new);
-      l_run[h] *= alpha;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[h][j] *= alpha;
-      m_run[h] = m_new;
-    }
-    const float m_use = m_run[h] == -INFINITY ? 0.0f : m_run[h];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const float p = __builtin_amdgcn_exp2f(x[mt] - m_use);
-      l_run[h] += p;
-      ph[mt][h] = (f16)p;
-    }
-  }
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-    for (int i = 0; i < NHV / 2; ++i) pp[mt][i] = pack_h2(half2v{ph[mt][2 * i], ph[mt][2 * i + 1]});
-  }
-}
-
-// Dim J of the lane's 8 dims, token pair q of k-step ks: acc[h][J] +=
-// P(t_2q, h) Vhat(t_2q, J) + P(t_2q+1, h) Vhat(t_2q+1, J) by v_dot2_f32_f16.
-template <int J, int NHV>
-__device__ __forceinline__ void pv_valu_dim(const VRegs& v, int ks, int q, half2v spq, const half2v (&P2)[NHV],
-                                            float (&acc)[NHV][8]) {
-  const uint2 wa = v.w[8 * ks + 2 * q];
-  const uint2 wb = v.w[8 * ks + 2 * q + 1];
-  const uint32_t c = (J < 4) ? i8pair_f16<J & 3>(wa.x, wb.x) : i8pair_f16<J & 3>(wa.y, wb.y);
-  const half2v vv = __builtin_bit_cast(half2v, c) * spq;
-#pragma unroll
-  for (int h = 0; h < NHV; ++h) acc[h][J] = __builtin_amdgcn_fdot2(P2[h], vv, acc[h][J], false);
-}
-
-// PV on the VALU: lane (l16, l4) owns dims 8*l16 .. +7 of its 16 tokens
-// v_token(ks, l4, e), as in pv_regs; the P of token t comes by a lane permute
-// from lane 16*l4 + (t & 15) (every row holds every token's P), register
-// t >> 4, one token pair at a time.  acc[h][J] sums the lane's own tokens only.
-template <int NHV>
-__device__ __forceinline__ void pv_valu(const VRegs& v, int sbase4, uint32_t ssel, const uint32_t (&pp)[4][NHV / 2],
-                                        int l4, float (&acc)[NHV][8]) {
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    half2v sp[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int t0 = (2 * q & 3) + 16 * (q >> 1);
-      const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(sbase4 + 8 * t0, (int)v.sd[ks]);
-      const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(sbase4 + 8 * t0 + 8, (int)v.sd[ks]);
-      sp[q] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(hi, lo, ssel));
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      // tokens e = 2q, 2q + 1: lanes 16*l4 + 4*l4 + (e & 3), register 2*ks + (e >> 2)
-      const int src0 = 4 * (20 * l4 + ((2 * q) & 3));
-      const int mt = 2 * ks + (q >> 1);
-      half2v P2[NHV];
-#pragma unroll
-      for (int i = 0; i < NHV / 2; ++i) {
-        const uint32_t g0 = (uint32_t)__builtin_amdgcn_ds_bpermute(src0, (int)pp[mt][i]);
-        const uint32_t g1 = (uint32_t)__builtin_amdgcn_ds_bpermute(src0 + 4, (int)pp[mt][i]);
-        P2[2 * i] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(g1, g0, 0x05040100u));
-        P2[2 * i + 1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(g1, g0, 0x07060302u));
-      }
-      pv_valu_dim<0, NHV>(v, ks, q, sp[q], P2, acc);
-      pv_valu_dim<1, NHV>(v, ks, q, sp[q], P2, acc);
-      pv_valu_dim<2, NHV>(v, ks, q, sp[q], P2, acc);
-      pv_valu_dim<3, NHV>(v, ks, q, sp[q], P2, acc);
-      pv_valu_dim<4, NHV>(v, ks, q, sp[q], P2, acc);
-      pv_valu_dim<5, NHV>(v, ks, q, sp[q], P2, acc);
-      pv_valu_dim<6, NHV>(v, ks, q, sp[q], P2, acc);
-      pv_valu_dim<7, NHV>(v, ks, q, sp[q], P2, acc);
-    }
-  }
-}
-
-template <int NHV, bool REL>
-__global__ __launch_bounds__(512) void decode_attention_valu_kernel(AttnArgs a) {
-  constexpr int WAVES = 8;
-  __shared__ AttnShared<WAVES> sh;
-  __shared__ uint4 qs[NHV * 16];
-  TP_STAMP(0);
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l16 = lane & 15;
-  const int l4 = lane >> 4;
-  const int units_total = (int)(gridDim.x / a.n_splits);
-  const int unit_id = (int)blockIdx.x % units_total;
-  const int split = (int)blockIdx.x / units_total;
-  const int64_t bkv = unit_id / a.head_blocks;
-  const int hb = unit_id % a.head_blocks;
-  const int b = (int)(bkv / a.hkv);
-  const int kv = (int)(bkv - (int64_t)b * a.hkv);
-  const int h0 = hb * 16;
-  const int p_begin = split * a.pages_per_split;
-  const int64_t live_pages = (a.seq_len + kPageTokens - 1) / kPageTokens;
-  const int p_end = (int)min((int64_t)min(p_begin + a.pages_per_split, a.n_pages), live_pages);
-
-  if (tid < NHV * 16) {
-    const int h = tid >> 4;
-    qs[tid] = *reinterpret_cast<const uint4*>(a.q + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + h) * kHeadDim +
-                                              8 * (tid & 15));
-  }
-  int page = p_begin + wave;
-  KRegs<kKindDefault> kr;
-  VRegs vr;
-  {
-    const bool has_page = page < p_end;
-    const int p_load = has_page ? page : p_begin;
-    const int lane_e = has_page ? lane : 0;
-    load_k<kKindDefault>(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, kr);
-    load_v(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
-  }
-  if (tid < 256) build_lut<kKindDefault>(sh.lut, a, tid);
-  lds_barrier();
-  TP_STAMP(2);
-
-  const int sbase4 = 4 * (8 * l4 + (l16 >> 3));
-  const uint32_t ssel = (l16 & 4) ? 0x07060302u : 0x05040100u;
-  float m_run[NHV], l_run[NHV], acc[NHV][8];
-#pragma unroll
-  for (int h = 0; h < NHV; ++h) {
-    m_run[h] = -INFINITY;
-    l_run[h] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[h][j] = 0.0f;
-  }
-  for (; page + WAVES < p_end; page += WAVES) {
-    float s[4][NHV];
-    qk_valu<NHV>(sh.lut, kr, qs, l4, s);
-    load_k<kKindDefault>(a, bkv * a.capacity + page + WAVES, l16, l4, kr);
-    uint32_t pp[4][NHV / 2];
-    softmax_valu<NHV>(s, kPageTokens, a.scale_log2, l16, m_run, l_run, acc, pp);
-    pv_valu<NHV>(vr, sbase4, ssel, pp, l4, acc);
-    load_v(a, bkv * a.capacity + page + WAVES, l16, l4, lane, vr);
-  }
-  if (page < p_end) {
-    float s[4][NHV];
-    qk_valu<NHV>(sh.lut, kr, qs, l4, s);
-    const int valid = (int)min((int64_t)kPageTokens, a.seq_len - (int64_t)page * kPageTokens);
-    uint32_t pp[4][NHV / 2];
-    softmax_valu<NHV>(s, valid, a.scale_log2, l16, m_run, l_run, acc, pp);
-    pv_valu<NHV>(vr, sbase4, ssel, pp, l4, acc);
-  }
-  TP_STAMP(52);
-  // Wave state into LDS in the layout finish_merged folds: dims 8*l16 .. of
-  // head h summed over the rows, l over the row's 16 lanes.
-#pragma unroll
-  for (int h = 0; h < NHV; ++h) {
-    l_run[h] = row_sum16(l_run[h]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[h][j] = sum_over_rows(acc[h][j]);
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < NHV; ++h) sh.ml[wave][h] = make_float2(m_run[h], l_run[h]);
-  }
-  if (l4 == 0) {
-#pragma unroll
-    for (int h = 0; h < NHV; ++h) {
-      float* row = &sh.acc[wave][h * kRedStride + 8 * l16];
-      *reinterpret_cast<float4v*>(row) = float4v{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
-      *reinterpret_cast<float4v*>(row + 4) = float4v{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
-    }
-  }
-  finish_merged<WAVES, REL ? kFlRelease : 0>(sh, a, tid, b, kv, h0, NHV, bkv, hb, split);
-}
-#endif  // TP_TIMELINE
 
 // ---- standalone fused QK -----------------------------------------------------------
 
@@ -1911,50 +1640,9 @@ int32_t tp_fused_qk_qjl(const void* q, int64_t batch, int32_t hq, int32_t hkv, c
 }
 
 #ifdef TP_TIMELINE
-// Measurement library only: the decode-kernel variant tp_decode_attention
-// launches (0: the product kernel; 1: + agent-scope release fence before the
-// split ticket; 2: QK and PV on the VALU; 3: 2 + the release fence; 4: the
-// product kernel without the combining workgroup's acquire fence).
+// The measurement library's decode-kernel variants (tp_attention_measure.inc).
 static int32_t g_measure_variant = 0;
-
-int32_t tp_measure_set_decode_variant(int32_t variant) {
-  if (variant < 0 || variant > 4) return TP_ERR_INVALID;
-  g_measure_variant = variant;
-  return TP_OK;
-}
-
-static int32_t launch_measure_variant(const AttnArgs& a, dim3 grid, int kind, hipStream_t s) {
-  const dim3 block(kDecodeWaves * 64);
-  if (g_measure_variant == 1) {
-    switch (kind) {
-      case kKindDefault: hipLaunchKernelGGL((decode_attention_kernel<kKindDefault, kDecodeWaves, kFlRelease>), grid, block, 0, s, a); break;
-      case kKindFast: hipLaunchKernelGGL((decode_attention_kernel<kKindFast, kDecodeWaves, kFlRelease>), grid, block, 0, s, a); break;
-      default: hipLaunchKernelGGL((decode_attention_kernel<kKindGeneric, kDecodeWaves, kFlRelease>), grid, block, 0, s, a); break;
-    }
-    return launch_status("tp_decode_attention (release variant)");
-  }
-  if (g_measure_variant == 4) {
-    switch (kind) {
-      case kKindDefault: hipLaunchKernelGGL((decode_attention_kernel<kKindDefault, kDecodeWaves, kFlNoAcquire>), grid, block, 0, s, a); break;
-      case kKindFast: hipLaunchKernelGGL((decode_attention_kernel<kKindFast, kDecodeWaves, kFlNoAcquire>), grid, block, 0, s, a); break;
-      default: hipLaunchKernelGGL((decode_attention_kernel<kKindGeneric, kDecodeWaves, kFlNoAcquire>), grid, block, 0, s, a); break;
-    }
-    return launch_status("tp_decode_attention (no-acquire variant)");
-  }
-  if (kind != kKindDefault || a.tail_len != 0 || a.head_blocks != 1 || (a.g != 4 && a.g != 8)) {
-    set_error("the VALU variant takes the default layout, no tail and 4 or 8 query heads per kv head");
-    return TP_ERR_INVALID;
-  }
-  const bool rel = g_measure_variant == 3;
-  if (a.g == 4) {
-    if (rel) hipLaunchKernelGGL((decode_attention_valu_kernel<4, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((decode_attention_valu_kernel<4, false>), grid, block, 0, s, a);
-  } else {
-    if (rel) hipLaunchKernelGGL((decode_attention_valu_kernel<8, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((decode_attention_valu_kernel<8, false>), grid, block, 0, s, a);
-  }
-  return launch_status("tp_decode_attention (VALU variant)");
-}
+static int32_t launch_measure_variant(const AttnArgs& a, dim3 grid, int kind, hipStream_t s);
 #endif
 
 }  // extern "C"
@@ -2598,8 +2286,5 @@ extern "C" unsigned long long tp_selftest_fastdiv(uint32_t d_max, unsigned long 
 }
 
 #ifdef TP_TIMELINE
-extern "C" void* tp_timeline_address() {
-  void* p = nullptr;
-  return hipGetSymbolAddress(&p, HIP_SYMBOL(tp::g_timeline)) == hipSuccess ? p : nullptr;
-}
+#include "tp_attention_measure.inc"
 #endif
