@@ -69,6 +69,9 @@ CASES = [
     dict(n_pages=5, kernel=1, layout="fast"),
     dict(n_pages=5, kernel=1, layout="deep2", hq=20, hkv=1),
     dict(n_pages=100, capacity=128, batch=2, hq=16, hkv=4),
+    dict(hq=24, hkv=2, n_pages=20, qjl=True),          # GQA 12: the row token order of default pages
+    dict(hq=40, hkv=2, n_pages=9, pps=2, dense_v=True),
+    dict(hq=8, hkv=2, n_pages=9, pps=2, qjl=True, tail=5, tail_stride=5),
 ]
 
 

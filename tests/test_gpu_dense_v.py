@@ -63,6 +63,7 @@ CASES = [
     ("fast", 32, 8, 17, 6, 0, 1, 0, False),     # 6-page splits, 4-wave workgroups
     ("default", 16, 2, 16, 8, 0, 2, 3, False),  # 8-page splits, batch 2, larger V capacity
     ("default", 40, 8, 12, 0, 17, 1, 0, True),  # g = 5
+    ("default", 40, 2, 3, 1, 5, 1, 1, False),   # g = 20: two head blocks, the row token order
 ]
 
 
@@ -147,6 +148,7 @@ def test_dense_v_shape_errors(device):
     ("default", 8, 2, 7, 3, 21, 2),
     ("default", 8, 1, 70, 1, 0, 1),   # two-tier combine
     ("fast", 32, 8, 17, 6, 0, 1),     # 4-wave workgroups
+    ("default", 24, 2, 4, 1, 7, 1),   # GQA 12: the row token order
 ])
 def test_dense_v_qjl_matches_oracle(device, layout_name, hq, hkv, S, pps, masked, B):
     print(f"[dense_v qjl] {layout_name} hq={hq} hkv={hkv} S={S} pps={pps} masked={masked} B={B}", flush=True)

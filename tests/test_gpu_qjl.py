@@ -107,6 +107,7 @@ def test_fused_qk_qjl_matches_oracle(device, layout_name, hq, hkv, S):
     ("default", 8, 1, 70, 5, 1, 0, 1),  # 70 splits: two-tier combine
     ("fast", 32, 8, 17, 11, 6, 0, 1),  # 6-page splits, one tier: 4-wave workgroups, two pages per wave
     ("default", 16, 2, 16, 0, 8, 0, 2),  # 8-page splits on 4 waves, batch 2
+    ("default", 24, 2, 5, 9, 2, 3, 1),  # GQA 12: the row token order (head blocks above 8 heads)
 ])
 def test_decode_attention_qjl_matches_oracle(device, layout_name, hq, hkv, S, tail, pps, masked, B):
     print(f"[qjl attn] {layout_name} hq={hq} hkv={hkv} S={S} tail={tail} pps={pps} masked={masked} B={B}", flush=True)

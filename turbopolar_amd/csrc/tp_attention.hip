@@ -70,7 +70,10 @@ __device__ unsigned long long g_timeline[kTimelineGroups][kTimelineStamps];
 // pairs arrived, 57 its record loads folded (thread 0's), 63 every wave's fold
 // in LDS, 58 split groups merged, 56 output stored.
 
-enum LayoutKind { kKindDefault = 0, kKindFast = 1, kKindGeneric = 2 };
+// kKindDefaultHR: default-layout pages in the half-row token order (below),
+// the decode kernel's form of the default layout for head blocks of at most 8
+// query heads.
+enum LayoutKind { kKindDefault = 0, kKindFast = 1, kKindGeneric = 2, kKindDefaultHR = 3 };
 
 // Division by a launch constant d as a multiply and a shift: for n < 2^31,
 // l = ceil(log2 d) and m = floor(2^(31+l) / d) + 1 (< 2^32), floor(n / d) =
@@ -248,7 +251,7 @@ struct Lut {
 template <int KIND>
 __device__ __forceinline__ void build_lut(Lut& lut, const AttnArgs& a, int tid) {
   const uint32_t c = (uint32_t)tid;
-  if constexpr (KIND == kKindDefault) {
+  if constexpr (KIND == kKindDefault || KIND == kKindDefaultHR) {
     lut.pair[c] = make_uint2(make_cs(c & 15u, 4), make_cs(c >> 4, 4));
   } else if constexpr (KIND == kKindFast) {
     lut.deep[c] = make_cs(c, 8);
@@ -262,21 +265,26 @@ __device__ __forceinline__ void build_lut(Lut& lut, const AttnArgs& a, int tid) 
 // (bits 18:15 = 4), every other field 0 (untyped loads, no swizzle).
 constexpr int kRawBufferWord3 = 0x00020000;
 
-// Q rows of the head block as MFMA B operands: lane (h = l16, l4) holds
-// q[h][32*l4 + 8*kk .. +8] for kk = 0..3, and zeros for heads past the
-// block's own (l16 >= nh).  The rows are read as raw buffer loads bounded to
-// the block's nh rows, so those lanes read zeros by the buffer's range check:
-// no branch around the loads.  Under a branch, the compiler waited for q
-// (s_waitcnt vmcnt) at the branch's join, before any page load was issued, so
-// every launch paid a memory round trip for q before its first page request.
+// Q rows of the head block as MFMA B operands.  Row order: lane (h = l16,
+// l4) holds q[h][32*l4 + 8*kk .. +8] for kk = 0..3.  Half-row order (at most
+// 8 heads): column l16 is head l16 & 7, half l16 >> 3, and the lane holds
+// q[h][64*(l16>>3) + 16*l4 + 8*kk .. +8] for kk = 0, 1.  Heads past the
+// block's own (>= nh) hold zeros.  The rows are read as raw buffer loads
+// bounded to the block's nh rows, so those lanes read zeros by the buffer's
+// range check: no branch around the loads.  Under a branch, the compiler
+// waited for q (s_waitcnt vmcnt) at the branch's join, before any page load
+// was issued, so every launch paid a memory round trip for q before its first
+// page request.
+template <bool HR>
 __device__ __forceinline__ void load_q(const AttnArgs& a, int b, int kv, int h0, int nh, int l16,
                                        int l4, half8v* qb) {
   const uint16_t* qblk = a.q + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0) * kHeadDim;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(qblk), (short)0, nh * kHeadDim * (int)sizeof(uint16_t), kRawBufferWord3);
-  const int off = (l16 * kHeadDim + 32 * l4) * (int)sizeof(uint16_t);
+  const int off = HR ? ((l16 & 7) * kHeadDim + 64 * (l16 >> 3) + 16 * l4) * (int)sizeof(uint16_t)
+                     : (l16 * kHeadDim + 32 * l4) * (int)sizeof(uint16_t);
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
+  for (int kk = 0; kk < (HR ? 2 : 4); ++kk) {
     const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * kk, 0, 0);
     qb[kk] = as_half8(w.x, w.y, w.z, w.w);
   }
@@ -291,13 +299,41 @@ __device__ __forceinline__ void load_q(const AttnArgs& a, int b, int kv, int h0,
 // enumerates the same functions over every lane, wave and workgroup of a
 // launch, so the check sees the kernels' own address arithmetic.
 
-__host__ __device__ inline int v_token(int ks, int l4, int e) { return 32 * ks + 4 * l4 + (e & 3) + 16 * (e >> 2); }
+// Token orders.  A lane (l16, l4) holds the page scores s[mt][i] of tokens
+// score_token(mt, i, l4) for the head of its column l16:
+//   row order (every kind but kKindDefaultHR): 16*mt + 4*l4 + i, the QK rows
+//     being 16 tokens of 128 dims;
+//   half-row order (kKindDefaultHR): 16*mt + 8*(i>>1) + 2*l4 + (i&1), the QK
+//     rows being 8 tokens x 2 halves of 64 dims (qk_regs).
+// The PV operands take the lane's scores in the order v_token(ks, l4, e) =
+// score_token(2 ks + e/4, e%4, l4), and V rows follow it.
+__host__ __device__ inline int score_token(int mt, int i, int l4, bool hr) {
+  return hr ? 16 * mt + 8 * (i >> 1) + 2 * l4 + (i & 1) : 16 * mt + 4 * l4 + i;
+}
+__host__ __device__ inline int v_token(int ks, int l4, int e, bool hr = false) {
+  return score_token(2 * ks + (e >> 2), e & 3, l4, hr);
+}
 
 // Key radii: default layout (fp16), the 32 bytes of pairs 16*l4 .. +15 of
 // token t = 16*mt + l16 at base + k_radii_row(t) (two 16-byte loads); fast
 // layout (int8 codes), 16 bytes at fast_radii_base + fast_row(t).
 __host__ __device__ inline int64_t k_radii_base(int64_t slot, int l4) { return (slot * (kPageTokens * kPairs) + 16 * l4) * 2; }
 __host__ __device__ inline int k_radii_row(int t) { return t * kPairs * 2; }
+// Half-row order: load g (0..7) of lane (l16, l4) reads the 16 bytes of pairs
+// 32*(l16&1) + 8*l4 .. +7 of token 8*g + l16/2, so one load instruction covers
+// 8 whole 128-byte token rows (the row order's loads cover half of each of 16
+// rows: 13.53 -> 12.99 us for a step's page loads alone at 32k); the codes of
+// those 8 pairs are 4 bytes of the token's level-1 row (l16 even: pairs 0..31)
+// or deep row (odd: pairs 32..63).
+__host__ __device__ inline int64_t hr_radii_base(int64_t slot, int l16, int l4) {
+  return slot * (kPageTokens * kPairs * 2) + 128 * (l16 >> 1) + 64 * (l16 & 1) + 16 * l4;
+}
+__host__ __device__ inline int hr_radii_row(int g) { return g * 8 * kPairs * 2; }
+__host__ __device__ inline bool hr_code_from_l1(int l16) { return (l16 & 1) == 0; }
+__host__ __device__ inline int64_t hr_code_base(int64_t slot, int l16, int l4) {
+  return slot * (kPageTokens * 16) + 16 * (l16 >> 1) + 4 * l4;
+}
+__host__ __device__ inline int hr_code_row(int g) { return g * 8 * 16; }
 // Key angle codes, default layout: 8 bytes of token t from angle_l1 (l4 < 2)
 // or angle_deep, at k_code_base + k_code_row(t).
 __host__ __device__ inline bool k_code_from_l1(int l4) { return l4 < 2; }
@@ -313,16 +349,23 @@ __host__ __device__ inline int64_t fast_scale(int64_t slot) { return slot * 2; }
 // v_code_base + v_code_row(ks, l4, e); the page's 512 bytes of scales as the
 // dwords `lane` and `lane + 64` at v_scale_base + 4*lane (+256).
 __host__ __device__ inline int64_t v_code_base(int64_t slot, int l16) { return slot * (kPageTokens * kHeadDim) + 8 * l16; }
-__host__ __device__ inline int v_code_row(int ks, int l4, int e) { return v_token(ks, l4, e) * kHeadDim; }
+__host__ __device__ inline int v_code_row(int ks, int l4, int e, bool hr = false) { return v_token(ks, l4, e, hr) * kHeadDim; }
 __host__ __device__ inline int64_t v_scale_base(int64_t slot) { return slot * (kPageTokens * kVGroups) * 2; }
 // Dense fp16 V rows (tp_decode_attention_dense_v): 16 bytes of the same rows.
 __host__ __device__ inline int64_t dense_v_base(int64_t slot, int l16) { return (slot * (kPageTokens * kHeadDim) + 8 * l16) * 2; }
-__host__ __device__ inline int dense_v_row(int ks, int l4, int e) { return v_token(ks, l4, e) * kHeadDim * 2; }
-// QJL sketches of tokens 16*mt + 4*l4 .. +3: 16 bytes at qjl_sign_base +
-// 128*mt and 16 bytes after them (8 bytes per token), and the tokens' fp16
-// norms, 8 bytes at qjl_norm_base + 32*mt.
-__host__ __device__ inline int64_t qjl_sign_base(int64_t slot, int l4) { return (slot * kPageTokens + 4 * l4) * 8; }
-__host__ __device__ inline int64_t qjl_norm_base(int64_t slot, int l4) { return (slot * kPageTokens + 4 * l4) * 2; }
+__host__ __device__ inline int dense_v_row(int ks, int l4, int e, bool hr = false) { return v_token(ks, l4, e, hr) * kHeadDim * 2; }
+// QJL sketches (8 bytes per token) and fp16 norms of a lane's scored tokens.
+// Row order, tokens 16*mt + 4*l4 .. +3: 32 bytes of sketches at
+// qjl_sign_base + 128*mt and 8 bytes of norms at qjl_norm_base + 32*mt.
+// Half-row order, tokens 16*mt + 2*l4 + {0, 1} and those + 8: 16 bytes of
+// sketches at qjl_sign_base + 128*mt and at + 64 more, 4 bytes of norms at
+// qjl_norm_base + 32*mt and at + 16 more.
+__host__ __device__ inline int64_t qjl_sign_base(int64_t slot, int l4, bool hr = false) {
+  return (slot * kPageTokens + (hr ? 2 : 4) * l4) * 8;
+}
+__host__ __device__ inline int64_t qjl_norm_base(int64_t slot, int l4, bool hr = false) {
+  return (slot * kPageTokens + (hr ? 2 : 4) * l4) * 2;
+}
 
 // A wave's first page loads: a wave with a page of its own (page < p_end)
 // loads it; a wave without one issues the same loads with every lane on lane
@@ -363,13 +406,16 @@ __device__ __forceinline__ void build_qjl_sin(float* tab, int tid) {
   if (tid <= kQjlBits) tab[tid] = sinf(1.57079632679489662f * (float)(kQjlBits - 2 * tid) / (float)kQjlBits);
 }
 
-// |q| of the lane's head from its MFMA B operands (32 dims per lane, rows
-// l4 = 0..3 hold the four quarters) and the head's sketch.
+// |q| of the lane's head from its MFMA B operands (row order: 32 dims per
+// lane, lane groups l4 = 0..3 hold the four quarters; half-row order: 16 dims
+// per lane, the four lane groups of columns l16 and l16 ^ 8 hold the two
+// halves) and the head's sketch.
+template <bool HR>
 __device__ __forceinline__ void qjl_query(const AttnArgs& a, int b, int kv, int h0, int nh, int l16, const half8v* qb,
                                           uint64_t& qsig, float& qnorm) {
   float ss = 0.0f;
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
+  for (int kk = 0; kk < (HR ? 2 : 4); ++kk) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float x = (float)qb[kk][e];
@@ -378,21 +424,28 @@ __device__ __forceinline__ void qjl_query(const AttnArgs& a, int b, int kv, int 
   }
   ss += __shfl_xor(ss, 16, 64);
   ss += __shfl_xor(ss, 32, 64);
+  if constexpr (HR) ss += __shfl_xor(ss, 8, 64);
   qnorm = sqrtf(ss);
   qsig = a.q_signs[(int64_t)b * a.hq + (int64_t)kv * a.g + h0 + min(l16, nh - 1)];  // unconditional, as load_q
 }
 
-// Adds the correction to one page's scores s[mt][i] (token 16*mt + 4*l4 + i,
-// head l16) of page slot `slot`.
+// Adds the correction to one page's scores s[mt][i] (token score_token(mt,
+// i, l4, HR), head l16) of page slot `slot`.
+template <bool HR>
 __device__ __forceinline__ void qjl_correct(const AttnArgs& a, int64_t slot, int l4, uint64_t qsig, float qnorm,
                                             const float* sin_tab, float4v* s) {
-  const char* sg = reinterpret_cast<const char*>(a.qjl_signs) + qjl_sign_base(slot, l4);
-  const char* nm = reinterpret_cast<const char*>(a.qjl_norms) + qjl_norm_base(slot, l4);
+  const char* sg = reinterpret_cast<const char*>(a.qjl_signs) + qjl_sign_base(slot, l4, HR);
+  const char* nm = reinterpret_cast<const char*>(a.qjl_norms) + qjl_norm_base(slot, l4, HR);
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
+    // Sketches and norms of tokens i = 0..3 of s[mt] (consecutive pairs i = 0, 1 and 2, 3).
     const u32x4 w01 = *reinterpret_cast<const u32x4*>(sg + 128 * mt);
-    const u32x4 w23 = *reinterpret_cast<const u32x4*>(sg + 128 * mt + 16);
-    const uint2 nn = *reinterpret_cast<const uint2*>(nm + 32 * mt);
+    const u32x4 w23 = *reinterpret_cast<const u32x4*>(sg + 128 * mt + (HR ? 64 : 16));
+    uint2 nn;
+    if constexpr (HR)
+      nn = make_uint2(*reinterpret_cast<const uint32_t*>(nm + 32 * mt), *reinterpret_cast<const uint32_t*>(nm + 32 * mt + 16));
+    else
+      nn = *reinterpret_cast<const uint2*>(nm + 32 * mt);
     const uint64_t k[4] = {((uint64_t)w01.y << 32) | w01.x, ((uint64_t)w01.w << 32) | w01.z,
                            ((uint64_t)w23.y << 32) | w23.x, ((uint64_t)w23.w << 32) | w23.z};
     const float n[4] = {h2f((uint16_t)(nn.x & 0xffffu)), h2f((uint16_t)(nn.x >> 16)), h2f((uint16_t)(nn.y & 0xffffu)),
@@ -414,6 +467,12 @@ template <>
 struct KRegs<kKindDefault> {  // fp16 radii, 4-bit l1 (pairs 0..31) + 4-bit deep (32..63)
   uint4 r[4][2];
   uint2 c[4];
+};
+
+template <>
+struct KRegs<kKindDefaultHR> {  // the default layout's page, half-row order: load g of hr_radii_row / hr_code_row
+  uint4 r[8];
+  uint32_t c[8];
 };
 
 template <>
@@ -442,6 +501,15 @@ __device__ __forceinline__ void load_k(const AttnArgs& a, int64_t slot, int l16,
       k.r[mt][1] = ldnt4(rp + 16);
       k.c[mt] = ldnt2(cbase + k_code_row(t));
     }
+  } else if constexpr (KIND == kKindDefaultHR) {
+    const char* rbase = static_cast<const char*>(a.radii) + hr_radii_base(slot, l16, l4);
+    const char* cbase = reinterpret_cast<const char*>(hr_code_from_l1(l16) ? a.angle_l1 : a.angle_deep) +
+                        hr_code_base(slot, l16, l4);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      k.r[g] = ldnt4(rbase + hr_radii_row(g));
+      k.c[g] = ldnt1(cbase + hr_code_row(g));
+    }
   } else if constexpr (KIND == kKindFast) {
     const char* rbase = static_cast<const char*>(a.radii) + fast_base(slot, l4);
     const char* cbase = reinterpret_cast<const char*>(a.angle_deep) + fast_base(slot, l4);
@@ -457,11 +525,49 @@ __device__ __forceinline__ void load_k(const AttnArgs& a, int64_t slot, int l16,
   }
 }
 
-// QK over one compressed page: s[mt][i] = score(token 16*mt + 4*l4 + i, head l16).
+// Half-row QK output of one group of 8 tokens: the MFMA's rows are (token
+// 8g + r/2, half r&1) and its columns (head c&7, half c>>3), so lane (l16, l4)
+// holds D[(2*l4 + u, half h)][l16] in acc[2u + h].  The score of token
+// 8g + 2*l4 + u for head l16 < 8 is D[(., 0)][(head, 0)] + D[(., 1)][(head,
+// 1)]: acc[2u] plus acc[2u + 1] of lane l16 + 8 (a row rotation by 8 lanes).
+// Lanes l16 >= 8 end with unused sums.  The scores go to s[mt][j], s[mt][j+1]
+// (token order score_token(mt, i, l4, true)).
+__device__ __forceinline__ float from_lane_xor8(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, true));  // row_ror:8
+}
+__device__ __forceinline__ void fold_halves(const float4v& acc, float4v& s, int j) {
+  s[j] = acc[0] + from_lane_xor8(acc[1]);
+  s[j + 1] = acc[2] + from_lane_xor8(acc[3]);
+}
+
+// QK over one compressed page: s[mt][i] = score(token score_token(mt, i, l4,
+// KIND == kKindDefaultHR), head l16).
 template <int KIND>
 __device__ __forceinline__ void qk_regs(const AttnArgs& a, const Lut& lut, const KRegs<KIND>& k,
                                         const half8v* qb, int l16, int l4, float4v* s) {
-  if constexpr (KIND == kKindDefault) {
+  if constexpr (KIND == kKindDefaultHR) {
+    // Load g: 8 pairs of one token half (A operand row l16 = (8g + l16/2,
+    // half l16&1)); k-step kk takes its pairs 4kk .. 4kk+3, code bytes 2kk
+    // and 2kk+1 (low nibble first).
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const uint32_t rw[4] = {k.r[g].x, k.r[g].y, k.r[g].z, k.r[g].w};
+      const uint32_t cw = k.c[g];
+      float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const uint2 cs01 = lut.pair[(cw >> (16 * kk)) & 0xffu];
+        const uint2 cs23 = lut.pair[(cw >> (16 * kk + 8)) & 0xffu];
+        uint32_t e[4];
+        e[0] = pack_h2(lo_lo(rw[2 * kk]) * __builtin_bit_cast(half2v, cs01.x));
+        e[1] = pack_h2(hi_hi(rw[2 * kk]) * __builtin_bit_cast(half2v, cs01.y));
+        e[2] = pack_h2(lo_lo(rw[2 * kk + 1]) * __builtin_bit_cast(half2v, cs23.x));
+        e[3] = pack_h2(hi_hi(rw[2 * kk + 1]) * __builtin_bit_cast(half2v, cs23.y));
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(e[0], e[1], e[2], e[3]), qb[kk], acc, 0, 0, 0);
+      }
+      fold_halves(acc, s[g >> 1], 2 * (g & 1));
+    }
+  } else if constexpr (KIND == kKindDefault) {
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const uint32_t rw[8] = {k.r[mt][0].x, k.r[mt][0].y, k.r[mt][0].z, k.r[mt][0].w,
@@ -546,7 +652,9 @@ __device__ __forceinline__ void qk_regs(const AttnArgs& a, const Lut& lut, const
 // ---- value pages --------------------------------------------------------------
 //
 // Lane (n = l16, l4) owns dims [8n, 8n+8) (group n/4) of the 16 tokens
-// 32*ks + 4*l4 + (e&3) + 16*(e>>2), ks = 0..1, e = 0..7.
+// v_token(ks, l4, e, HR), ks = 0..1, e = 0..7 (row order: 32*ks + 4*l4 +
+// (e&3) + 16*(e>>2); half-row order: 32*ks + 16*(e>>2) + 8*((e>>1)&1) +
+// 2*l4 + (e&1)); tokens e and e+1 (e even) are consecutive in both.
 
 struct VRegs {
   uint2 w[16];
@@ -557,12 +665,13 @@ struct VRegs {
 // two coalesced dwords per lane (the scale of token t, group g is half g & 1
 // of dword 2t + g / 2); PV gathers each lane's scales from these with lane
 // permutes, so the scales hold two registers, not one per token.
+template <bool HR>
 __device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16, int l4, int lane, VRegs& v) {
   const char* vbase = reinterpret_cast<const char*>(a.v_codes) + v_code_base(slot, l16);
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v.w[8 * ks + e] = ldnt2(vbase + v_code_row(ks, l4, e));
+    for (int e = 0; e < 8; ++e) v.w[8 * ks + e] = ldnt2(vbase + v_code_row(ks, l4, e, HR));
   }
   const char* sbase = reinterpret_cast<const char*>(a.v_scales) + v_scale_base(slot);
   v.sd[0] = ldnt1(sbase + 4 * lane);
@@ -586,20 +695,22 @@ __device__ __forceinline__ void pv_tile(const VRegs& v, int ks, const half2v* sp
   acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(e[0], e[1], e[2], e[3]), pb, acc, 0, 0, 0);
 }
 
-// sbase4: byte index of the lane holding the scale dword of token 4*l4 of the
-// lane's group (4 * (8*l4 + g/2)); ssel: v_perm selector taking half g & 1 of
-// two dwords.
+// sbase4: byte index of the lane holding the scale dword of token
+// v_token(0, l4, 0, HR) of the lane's group g (4 * (2 * that token + g/2));
+// ssel: v_perm selector taking half g & 1 of two dwords.
+template <bool HR>
 __device__ __forceinline__ void pv_regs(const VRegs& v, int sbase4, uint32_t ssel, const half8v* pb,
                                         float4v* acc) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     // Scales of tokens (2q, 2q+1) of this k-step as fp16 pairs: tokens
-    // 4*l4 + t0 and 4*l4 + t0 + 1 (t0 = 0, 2, 16, 18) sit in the dwords of
-    // lanes 8*l4 + g/2 + 2*t0 and two lanes further, in register ks.
+    // v_token(0, l4, 0) + t0 and one more (row order t0 = 0, 2, 16, 18;
+    // half-row order 0, 8, 16, 24) sit in the dwords of lanes sbase4/4 + 2*t0
+    // and two lanes further, in register ks.
     half2v sp[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int t0 = (2 * q & 3) + 16 * (q >> 1);
+      const int t0 = v_token(0, 0, 2 * q, HR);
       const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(sbase4 + 8 * t0, (int)v.sd[ks]);
       const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(sbase4 + 8 * t0 + 8, (int)v.sd[ks]);
       sp[q] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(hi, lo, ssel));
@@ -622,13 +733,15 @@ __device__ __forceinline__ void pv_regs(const VRegs& v, int sbase4, uint32_t sse
 // read as zero by the buffer's range check and no load sits under a branch.
 // (Loads under a per-row branch were each waited for before their MFMA: up to
 // 32 memory round trips in a row on the last split's critical path.)
-// k[4 mt + kk] = K[16 mt + l16][32 l4 + 8 kk .. +8] (the QK A operands);
-// v[8 ks + e] = V[v_token(ks, l4, e)][8 l16 .. +8] (the PV rows).
+// The QK A operands: row order k[4 mt + kk] = K[16 mt + l16][32 l4 + 8 kk ..
+// +8]; half-row order k[2 g + kk] = K[8 g + l16/2][64 (l16&1) + 16 l4 + 8 kk ..
+// +8].  v[8 ks + e] = V[v_token(ks, l4, e, HR)][8 l16 .. +8] (the PV rows).
 struct TailRegs {
   u32x4 k[16];
   u32x4 v[16];
 };
 
+template <bool HR>
 __device__ __forceinline__ void load_tail(const AttnArgs& a, int64_t bkv, int l16, int l4, TailRegs& r) {
   const int64_t plane = bkv * a.tail_stride * kHeadDim;
   const int bytes = a.tail_len * kHeadDim * (int)sizeof(uint16_t);
@@ -637,39 +750,52 @@ __device__ __forceinline__ void load_tail(const AttnArgs& a, int64_t bkv, int l1
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.tail_v + plane),
                                                                       (short)0, bytes, kRawBufferWord3);
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int off = ((16 * mt + l16) * kHeadDim + 32 * l4 + 8 * kk) * (int)sizeof(uint16_t);
-      r.k[4 * mt + kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
-    }
+  for (int j = 0; j < 16; ++j) {
+    const int elem = HR ? (8 * (j >> 1) + (l16 >> 1)) * kHeadDim + 64 * (l16 & 1) + 16 * l4 + 8 * (j & 1)
+                        : (16 * (j >> 2) + l16) * kHeadDim + 32 * l4 + 8 * (j & 3);
+    r.k[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, elem * (int)sizeof(uint16_t), 0, 0);
   }
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int off = (v_token(ks, l4, e) * kHeadDim + 8 * l16) * (int)sizeof(uint16_t);
+      const int off = (v_token(ks, l4, e, HR) * kHeadDim + 8 * l16) * (int)sizeof(uint16_t);
       r.v[8 * ks + e] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
     }
   }
 }
 
-// QK over the dense tail (rows past tail_len are zero).
+// QK over the dense tail (rows past tail_len are zero), in the token order
+// of the pages' scores.
+template <bool HR>
 __device__ __forceinline__ void qk_tail(const TailRegs& r, const half8v* qb, float4v* s) {
+  if constexpr (HR) {
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int g = 0; g < 8; ++g) {
+      float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const u32x4 w = r.k[4 * mt + kk];
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(w.x, w.y, w.z, w.w), qb[kk], acc, 0, 0, 0);
+      for (int kk = 0; kk < 2; ++kk) {
+        const u32x4 w = r.k[2 * g + kk];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(w.x, w.y, w.z, w.w), qb[kk], acc, 0, 0, 0);
+      }
+      fold_halves(acc, s[g >> 1], 2 * (g & 1));
     }
-    s[mt] = acc;
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const u32x4 w = r.k[4 * mt + kk];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(w.x, w.y, w.z, w.w), qb[kk], acc, 0, 0, 0);
+      }
+      s[mt] = acc;
+    }
   }
 }
 
-// PV over 64 dense fp16 V rows held as in TailRegs::v (row v_token(ks, l4, e)
-// in element 8 ks + e, dims 8 l16 .. +8).
+// PV over 64 dense fp16 V rows held as in TailRegs::v (row v_token(ks, l4, e,
+// HR) in element 8 ks + e, dims 8 l16 .. +8).
 __device__ __forceinline__ void pv_rows(const u32x4* v, const half8v* pb, float4v* acc) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
@@ -700,6 +826,7 @@ struct DenseVRegs {
   u32x4 w[16];
 };
 
+template <bool HR>
 __device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16, int l4, int lane, DenseVRegs& v) {
   (void)lane;
   const char* vbase = reinterpret_cast<const char*>(a.v_dense) + dense_v_base(slot, l16);
@@ -707,12 +834,13 @@ __device__ __forceinline__ void load_v(const AttnArgs& a, int64_t slot, int l16,
   for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const uint4 w = ldnt4(vbase + dense_v_row(ks, l4, e));
+      const uint4 w = ldnt4(vbase + dense_v_row(ks, l4, e, HR));
       v.w[8 * ks + e] = u32x4{w.x, w.y, w.z, w.w};
     }
   }
 }
 
+template <bool HR>
 __device__ __forceinline__ void pv_regs(const DenseVRegs& v, int sbase4, uint32_t ssel, const half8v* pb,
                                         float4v* acc) {
   (void)sbase4;
@@ -729,6 +857,7 @@ __device__ __forceinline__ void pv_regs(const DenseVRegs& v, int sbase4, uint32_
 // enough in fp16) and the 32-register accumulator rescale is rare.
 constexpr float kLazyRescale = 8.0f;
 
+template <bool HR>
 __device__ __forceinline__ void softmax_page(const float4v* s, int valid, float scale_log2, int l4,
                                              float& m_run, float& l_run, float4v* acc, half8v* pb) {
   float x[16];
@@ -742,7 +871,7 @@ __device__ __forceinline__ void softmax_page(const float4v* s, int valid, float 
     for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (16 * mt + 4 * l4 + i >= valid) x[4 * mt + i] = -INFINITY;
+        if (score_token(mt, i, l4, HR) >= valid) x[4 * mt + i] = -INFINITY;
       }
     }
   }
@@ -1194,6 +1323,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   // for the thread count.  The host launches 4 waves only for head blocks of
   // at most 8 query heads.
   static_assert(WAVES == 8 || WAVES == 4, "decode_attention_kernel takes 4 or 8 waves per workgroup");
+  // Half-row token order (kKindDefaultHR): the host launches it only for head
+  // blocks of at most 8 query heads.
+  constexpr bool HR = KIND == kKindDefaultHR;
   __shared__ AttnShared<WAVES> sh;
   TP_STAMP(0);
   // Every argument the prologue reads arrives in one round of scalar loads:
@@ -1235,7 +1367,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   // Q and the first page's loads go out before the table build and the
   // barrier, and nothing before the barrier uses them.
   half8v qb[4];
-  load_q(a, b, kv, h0, nh, l16, l4, qb);
+  load_q<HR>(a, b, kv, h0, nh, l16, l4, qb);
   TP_STAMP(60);
   int page = p_begin + wave;
   KRegs<KIND> kr;
@@ -1245,9 +1377,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     if (page < p_end) {
       load_k<KIND>(a, bkv * a.capacity + page, l16, l4, kr);
       if constexpr (DV)
-        load_v(a, bkv * a.v_capacity + page, l16, l4, lane, vr);
+        load_v<HR>(a, bkv * a.v_capacity + page, l16, l4, lane, vr);
       else
-        load_v(a, bkv * a.capacity + page, l16, l4, lane, vr);
+        load_v<HR>(a, bkv * a.capacity + page, l16, l4, lane, vr);
     }
   } else {
     // The specialised layouts always have pages (p_begin < n_pages).  A wave
@@ -1260,9 +1392,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
     first_page_load(page, p_begin, p_end, lane, p_load, lane_e);
     load_k<KIND>(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, kr);
     if constexpr (DV)
-      load_v(a, bkv * a.v_capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
+      load_v<HR>(a, bkv * a.v_capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
     else
-      load_v(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
+      load_v<HR>(a, bkv * a.capacity + p_load, lane_e & 15, lane_e >> 4, lane_e, vr);
   }
   TP_STAMP(1);
   if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
@@ -1272,12 +1404,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   float qnorm = 0.0f;
   if constexpr (QJL) {
     build_qjl_sin(qjl_sin, tid);
-    qjl_query(a, b, kv, h0, nh, l16, qb, qsig, qnorm);
+    qjl_query<HR>(a, b, kv, h0, nh, l16, qb, qsig, qnorm);
   }
   lds_barrier();
   TP_STAMP(2);
 
-  const int sbase4 = 4 * (8 * l4 + (l16 >> 3));
+  const int sbase4 = 4 * (2 * v_token(0, l4, 0, HR) + (l16 >> 3));
   const uint32_t ssel = (l16 & 4) ? 0x07060302u : 0x05040100u;
   float m_run = -INFINITY;
   float l_run = 0.0f;
@@ -1294,25 +1426,25 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   for (int it = 0; page + WAVES < p_end; page += WAVES, ++it) {
     float4v s[4];
     qk_regs<KIND>(a, sh.lut, kr, qb, l16, l4, s);
-    if constexpr (QJL) qjl_correct(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
+    if constexpr (QJL) qjl_correct<HR>(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
     if (it < 12) TP_STAMP(4 + 4 * it);
     load_k<KIND>(a, bkv * a.capacity + page + WAVES, l16, l4, kr);
     half8v pb[2];
-    softmax_page(s, kPageTokens, a.scale_log2, l4, m_run, l_run, acc, pb);
-    pv_regs(vr, sbase4, ssel, pb, acc);
+    softmax_page<HR>(s, kPageTokens, a.scale_log2, l4, m_run, l_run, acc, pb);
+    pv_regs<HR>(vr, sbase4, ssel, pb, acc);
     if constexpr (DV)
-      load_v(a, bkv * a.v_capacity + page + WAVES, l16, l4, lane, vr);
+      load_v<HR>(a, bkv * a.v_capacity + page + WAVES, l16, l4, lane, vr);
     else
-      load_v(a, bkv * a.capacity + page + WAVES, l16, l4, lane, vr);
+      load_v<HR>(a, bkv * a.capacity + page + WAVES, l16, l4, lane, vr);
     if (it < 12) TP_STAMP(5 + 4 * it);
   }
   if (page < p_end) {
     float4v s[4];
     qk_regs<KIND>(a, sh.lut, kr, qb, l16, l4, s);
-    if constexpr (QJL) qjl_correct(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
+    if constexpr (QJL) qjl_correct<HR>(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
     const int valid = (int)min((int64_t)kPageTokens, a.seq_len - (int64_t)page * kPageTokens);
     half8v pb[2];
-    softmax_page(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
+    softmax_page<HR>(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
     if constexpr (DV) {
       // Dense V rows of masked tokens get P = 0, but 0 * NaN is NaN in the
       // MFMA: rows at or past `valid` are zeroed, so whatever a caller's
@@ -1323,12 +1455,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
         for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            if (v_token(ks, l4, e) >= valid) vr.w[8 * ks + e] = u32x4{0u, 0u, 0u, 0u};
+            if (v_token(ks, l4, e, HR) >= valid) vr.w[8 * ks + e] = u32x4{0u, 0u, 0u, 0u};
           }
         }
       }
     }
-    pv_regs(vr, sbase4, ssel, pb, acc);
+    pv_regs<HR>(vr, sbase4, ssel, pb, acc);
   }
 
   // The dense tail follows the last page; the last split's least loaded wave
@@ -1340,12 +1472,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
       const int valid = (int)min((int64_t)a.tail_len, a.seq_len - tok0);
       if (valid > 0) {
         TailRegs tr;
-        load_tail(a, bkv, l16, l4, tr);
+        load_tail<HR>(a, bkv, l16, l4, tr);
         __builtin_amdgcn_sched_barrier(0);  // all 32 loads out before the first MFMA waits
         float4v s[4];
-        qk_tail(tr, qb, s);
+        qk_tail<HR>(tr, qb, s);
         half8v pb[2];
-        softmax_page(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
+        softmax_page<HR>(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
         pv_tail(tr, pb, acc);
       }
     }
@@ -1385,7 +1517,7 @@ __global__ __launch_bounds__(kQkWaves * 64) void fused_qk_kernel(AttnArgs a) {
   const int h0 = hb * 16;
   const int nh = min(16, a.g - h0);
   half8v qb[4];
-  load_q(a, b, kv, h0, nh, l16, l4, qb);
+  load_q<false>(a, b, kv, h0, nh, l16, l4, qb);
   // The page's K loads go out before the table build and the barrier (a wave
   // past the last page reloads the last page and leaves after the barrier).
   const int page = blockIdx.x * kQkWaves + wave;
@@ -1396,13 +1528,13 @@ __global__ __launch_bounds__(kQkWaves * 64) void fused_qk_kernel(AttnArgs a) {
   float qnorm = 0.0f;
   if constexpr (QJL) {
     build_qjl_sin(qjl_sin, tid);
-    qjl_query(a, b, kv, h0, nh, l16, qb, qsig, qnorm);
+    qjl_query<false>(a, b, kv, h0, nh, l16, qb, qsig, qnorm);
   }
   __syncthreads();
   if (page >= a.n_pages) return;
   float4v s[4];
   qk_regs<KIND>(a, lut, kr, qb, l16, l4, s);
-  if constexpr (QJL) qjl_correct(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
+  if constexpr (QJL) qjl_correct<false>(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
   uint16_t* st = reinterpret_cast<uint16_t*>(&stage[wave][0]);
   if (l16 < nh) {
 #pragma unroll
@@ -1671,6 +1803,15 @@ static void launch_decode_w(const AttnArgs& a, dim3 grid, hipStream_t s) {
 // 18.40 for the default 16-page splits on 8 waves).
 static bool four_waves(const AttnArgs& a) { return a.g <= 8 && a.pages_per_split <= 8; }
 
+// The decode kernel's kind for a layout kind: default-layout pages take the
+// half-row token order when every head block has at most 8 query heads (its
+// QK columns hold 8 heads x 2 halves).  Paired against the row order (same
+// process, same caches, two sessions): 8 kv heads x 4 query heads at 4k 8.51 ->
+// 8.32 and 8.63 -> 8.45 us; one kv head x 4 at 131k 14.41 -> 14.16; 8 x 8 at
+// 32k 18.40 -> 18.30; 8 x 4 at 8k, 32k and 131k within 0.05 us either way.
+// The 8-wave kernel's registers fall from 245 to 219 VGPRs.
+static int decode_kind(int kind, const AttnArgs& a) { return kind == kKindDefault && a.g <= 8 ? kKindDefaultHR : kind; }
+
 template <int KIND, bool QJL>
 static void launch_decode(const AttnArgs& a, dim3 grid, hipStream_t s) {
   if (four_waves(a))
@@ -1684,7 +1825,13 @@ static void launch_decode(const AttnArgs& a, dim3 grid, hipStream_t s) {
 template <bool QJL>
 static void launch_decode_dense_v(const AttnArgs& a, int kind, dim3 grid, hipStream_t s) {
   const bool w4 = four_waves(a);
-  switch (kind) {
+  switch (decode_kind(kind, a)) {
+    case kKindDefaultHR:
+      if (w4)
+        launch_decode_w<kKindDefaultHR, 4, QJL, true>(a, grid, s);
+      else
+        launch_decode_w<kKindDefaultHR, kDecodeWaves, QJL, true>(a, grid, s);
+      break;
     case kKindDefault:
       if (w4)
         launch_decode_w<kKindDefault, 4, QJL, true>(a, grid, s);
@@ -1810,7 +1957,8 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
     return launch_status("tp_decode_attention_dense_v");
   }
   if (use_qjl) {
-    switch (n_pages > 0 ? layout_kind(layout) : (int)kKindGeneric) {
+    switch (n_pages > 0 ? decode_kind(layout_kind(layout), a) : (int)kKindGeneric) {
+      case kKindDefaultHR: launch_decode<kKindDefaultHR, true>(a, grid, s); break;
       case kKindDefault: launch_decode<kKindDefault, true>(a, grid, s); break;
       case kKindFast: launch_decode<kKindFast, true>(a, grid, s); break;
       default: launch_decode<kKindGeneric, true>(a, grid, s); break;
@@ -1825,7 +1973,8 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
     return launch_measure_variant(a, grid, n_pages > 0 ? layout_kind(layout) : -1, s);
   }
 #endif
-  switch (n_pages > 0 ? layout_kind(layout) : (int)kKindGeneric) {
+  switch (n_pages > 0 ? decode_kind(layout_kind(layout), a) : (int)kKindGeneric) {
+    case kKindDefaultHR: launch_decode<kKindDefaultHR, false>(a, grid, s); break;
     case kKindDefault: launch_decode<kKindDefault, false>(a, grid, s); break;
     case kKindFast: launch_decode<kKindFast, false>(a, grid, s); break;
     default: launch_decode<kKindGeneric, false>(a, grid, s); break;
@@ -1917,6 +2066,10 @@ extern "C" unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c,
   const int kind = layout_kind(&c->layout);
   const int64_t BH = c->batch * c->hkv;
   const int g = c->hq / c->hkv;
+  AttnArgs ka{};
+  ka.g = g;
+  const int dkind = decode_kind(kind, ka);  // the decode kernel's kind (the fused QK kernel takes `kind`)
+  const bool hr = dkind == kKindDefaultHR;
   const int head_blocks = head_blocks_of(c->hq, c->hkv);
   const int n_pages = c->n_pages;
   const int64_t cap = c->capacity;
@@ -1946,7 +2099,13 @@ extern "C" unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c,
   auto page_loads = [&](int lin, int wave, int lane, int64_t bkv, int page, int lane_e) {
     const int64_t slot = bkv * cap + page;
     const int l16 = lane_e & 15, l4 = lane_e >> 4;
-    if (kind == kKindDefault) {
+    if (dkind == kKindDefaultHR) {
+      for (int g8 = 0; g8 < 8; ++g8) {
+        log.check("radii", hr_radii_base(slot, l16, l4) + hr_radii_row(g8), 16, sz_radii, lin, wave, lane);
+        log.check(hr_code_from_l1(l16) ? "angle_l1" : "angle_deep", hr_code_base(slot, l16, l4) + hr_code_row(g8), 4,
+                  hr_code_from_l1(l16) ? sz_l1 : sz_deep, lin, wave, lane);
+      }
+    } else if (dkind == kKindDefault) {
       for (int mt = 0; mt < 4; ++mt) {
         const int t = 16 * mt + l16;
         log.check("radii", k_radii_base(slot, l4) + k_radii_row(t), 32, sz_radii, lin, wave, lane);
@@ -1964,12 +2123,12 @@ extern "C" unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c,
     if (c->dense_v) {
       for (int ks = 0; ks < 2; ++ks)
         for (int e = 0; e < 8; ++e)
-          log.check("dense V", dense_v_base(bkv * c->v_capacity + page, l16) + dense_v_row(ks, l4, e), 16, sz_dv, lin,
+          log.check("dense V", dense_v_base(bkv * c->v_capacity + page, l16) + dense_v_row(ks, l4, e, hr), 16, sz_dv, lin,
                     wave, lane);
     } else {
       for (int ks = 0; ks < 2; ++ks)
         for (int e = 0; e < 8; ++e)
-          log.check("v_codes", v_code_base(slot, l16) + v_code_row(ks, l4, e), 8, sz_vc, lin, wave, lane);
+          log.check("v_codes", v_code_base(slot, l16) + v_code_row(ks, l4, e, hr), 8, sz_vc, lin, wave, lane);
       const int64_t sb = v_scale_base(slot);
       log.check("v_scales", sb + 4 * lane_e, 4, sz_vs, lin, wave, lane);
       log.check("v_scales", sb + 4 * (lane_e + 64) + (c->mutate == 1 ? 512 : 0), 4, sz_vs, lin, wave, lane);
@@ -2110,8 +2269,15 @@ extern "C" unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c,
               const int64_t qslot = bkv * c->qjl_capacity + pg;
               const int l4 = lane >> 4;
               for (int mt = 0; mt < 4; ++mt) {
-                log.check("qjl signs", qjl_sign_base(qslot, l4) + 128 * mt, 32, sz_sig, L, wave, lane);
-                log.check("qjl norms", qjl_norm_base(qslot, l4) + 32 * mt, 8, sz_nrm, L, wave, lane);
+                if (hr) {
+                  for (int j = 0; j < 2; ++j) {
+                    log.check("qjl signs", qjl_sign_base(qslot, l4, true) + 128 * mt + 64 * j, 16, sz_sig, L, wave, lane);
+                    log.check("qjl norms", qjl_norm_base(qslot, l4, true) + 32 * mt + 16 * j, 4, sz_nrm, L, wave, lane);
+                  }
+                } else {
+                  log.check("qjl signs", qjl_sign_base(qslot, l4) + 128 * mt, 32, sz_sig, L, wave, lane);
+                  log.check("qjl norms", qjl_norm_base(qslot, l4) + 32 * mt, 8, sz_nrm, L, wave, lane);
+                }
               }
             }
             log.check("q signs", ((int64_t)b * c->hq + (int64_t)kv * g + h0 + std::min(l16, nh - 1)) * 8, 8, sz_qs, L,
