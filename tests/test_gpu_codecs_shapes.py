@@ -59,3 +59,36 @@ def test_quantize_any_group_size(device, group, D, dtype):
     assert _same(q.scales.cpu().numpy(), scales_ref)
     deq = GroupedVQuantizer(group_size=group).dequantize_block(q).cpu().numpy()
     assert _same(deq, oracle.dequantize_block(codes_ref, scales_ref, group))
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_int8_log_radii_nan_row(device, dtype):
+    """A NaN pair in one (b, h) row: that row's max |log r| is NaN, so its scale
+    is NaN and every radius code 0 (the oracle's NumPy max); the other rows are
+    untouched."""
+    int8, l1b, deepb, split = LAYOUTS["fast"]
+    cfg = TurboPolarConfig(num_q_heads=4, num_kv_heads=2, use_int8_radii=int8, k_angle_bits_level1=l1b,
+                           k_angle_bits_deep=deepb, split_dim=split)
+    rng = np.random.default_rng(7)
+    k = (rng.standard_normal((2, 2, 37, 128)) * 4).astype(dtype)
+    k[0, 1, 5, 20] = np.nan
+    ref = oracle.encode_block(k, l1_bits=l1b, deep_bits=deepb, split_dim=split, use_int8_radii=True)
+    blk = PolarQuantEncoder(cfg).encode_block(torch.from_numpy(k).to(device))
+    assert _same(blk.radii.cpu().numpy(), ref["radii"])
+    assert _same(blk.radii_scales.cpu().numpy().reshape(2, 2, 1, 1), ref["radii_scales"])
+    assert _same(blk.angle_codes_deep.cpu().numpy(), ref["angle_codes_deep"])
+
+
+@pytest.mark.parametrize("group", [8, 32, 128])
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_quantize_nan_group(device, group, dtype):
+    """A NaN in a group: its scale is NaN and every code of the group 0 (the
+    oracle's NumPy max); an inf elsewhere gives codes 0 around a finite v / inf."""
+    rng = np.random.default_rng(group)
+    v = (rng.standard_normal((1, 2, 3, 5, 128)) * 3).astype(dtype)
+    v[0, 0, 1, 2, 3] = np.nan
+    v[0, 1, 0, 4, 100] = np.inf
+    codes_ref, scales_ref = oracle.quantize_block(v, group)
+    q = GroupedVQuantizer(group_size=group).quantize_block(torch.from_numpy(v).to(device))
+    assert _same(q.codes.cpu().numpy(), codes_ref)
+    assert _same(q.scales.cpu().numpy(), scales_ref)

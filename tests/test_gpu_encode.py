@@ -118,6 +118,21 @@ def test_encode_partial_page_zero_padded(device, layout_name):
     assert_bits_equal(gpu["v_scales"], vs, "v_scales")
 
 
+@pytest.mark.parametrize("layout_name", ["default", "fast"])
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_encode_nan_inputs(device, layout_name, dtype):
+    """NaN in x, in y and in a whole token row of K, and in one V group: the
+    oracle's rules (NaN codes are 0; in the log-int8 layout a NaN radius makes
+    the page's max |log r|, so its scale, NaN and every radius code 0)."""
+    print(f"[encode-nan] layout={layout_name} dtype={np.dtype(dtype).name}", flush=True)
+    k, v = gen_kv(31, 1, 2, 3 * PAGE, "normal", np.float32)
+    k[0, 0, 5, 10] = np.nan           # page 0: x of pair 5
+    k[0, 0, 40, 33] = np.nan          # page 0: y of pair 16
+    k[0, 1, PAGE + 7, :] = np.nan     # page 1 of head 1: a whole token
+    v[0, 0, 2 * PAGE + 3, 64 + 9] = np.nan  # page 2: one V group
+    check_against_oracle(k.astype(dtype), v.astype(dtype), LAYOUTS[layout_name], device)
+
+
 def test_encode_into_capacity_slot(device):
     """Pages land in slots [page_begin, page_begin + S) of a larger store."""
     k, v = gen_kv(8, 2, 2, 2 * PAGE, "normal", np.float16)

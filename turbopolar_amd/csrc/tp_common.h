@@ -84,6 +84,13 @@ __device__ __forceinline__ bool near_f16_midpoint(float v) {
   return u < 0x38800000u || (low <= kGuard && low >= -kGuard);
 }
 
+// Running maxima of group and page scales take NaN as NumPy's max does (the
+// reference's max reductions are restated with it): a NaN element makes the
+// maximum NaN, and the scale and every code of the group or page follow.
+// nan_max(m, x) for m, x >= 0 or NaN; max_abs_nan(m, x) = nan_max(m, |x|).
+__device__ __forceinline__ float nan_max(float m, float x) { return (x > m || x != x) ? x : m; }
+__device__ __forceinline__ float max_abs_nan(float m, float x) { return nan_max(m, fabsf(x)); }
+
 // fp32 atan2 for finite x, y: octant reduction to t = min(|x|,|y|)/max in
 // [0, 1], atan(t) = t * P(t^2) with a degree-9 polynomial in t^2 fitted here
 // for least maximum relative error on [0, 1] (Lawson-weighted least squares
@@ -123,10 +130,12 @@ __device__ __forceinline__ float atan2_poly(float y, float x) {
 // is cleared when the result is too close to an fp16 rounding boundary to be
 // trusted (the caller then uses atan2_f16_slow).
 __device__ __forceinline__ uint16_t atan2_f16_fast(float y, float x, bool* exact) {
-  *exact = true;
-  if (y == 0.0f && !__builtin_signbit(x)) return f2h(y);  // exact +-0
+  // atan2_poly's min / max drop a NaN operand: a NaN x or y takes the float64
+  // path, whose atan2 is NaN.
+  *exact = !__builtin_isunordered(x, y);
+  if (*exact && y == 0.0f && !__builtin_signbit(x)) return f2h(y);  // exact +-0
   const float a = atan2_poly(y, x);
-  *exact = !near_f16_midpoint<kGuardAtan2>(a);
+  *exact = *exact && !near_f16_midpoint<kGuardAtan2>(a);
   return f2h(a);
 }
 __device__ __forceinline__ uint16_t atan2_f16_slow(float y, float x) { return d2h(atan2((double)y, (double)x)); }

@@ -98,16 +98,26 @@ __device__ __forceinline__ void pack_rows(uint8_t* dst, int row_bytes, int bits,
   }
 }
 
-__device__ __forceinline__ float wave_max(float v) {
+// The page's max |lr| over the workgroup's 256 threads (16 values each) as
+// the reference's reduction takes it: NaN propagates (a NaN log radius makes
+// the maximum NaN, and with it the page scale and every radius code).  An
+// integer maximum of the |lr| bit patterns orders finite values and inf as
+// fmaxf does and puts every NaN above inf.  s_max: 4 words of LDS.
+__device__ __forceinline__ float page_abs_max(const float (&lr)[16], uint32_t* s_max, int tid) {
+  uint32_t m = 0;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  for (int j = 0; j < 16; ++j) m = max(m, __float_as_uint(lr[j]) & 0x7fffffffu);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+  if ((tid & 63) == 0) s_max[tid >> 6] = m;
+  __syncthreads();
+  return __uint_as_float(max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3])));
 }
 
 template <bool kF32>
 __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
   __shared__ uint8_t s_codes[kPageTokens * kPairs];
-  __shared__ float s_max[4];
+  __shared__ uint32_t s_max[4];
 
   const int page = blockIdx.x;
   const int64_t bh = blockIdx.y;
@@ -185,13 +195,7 @@ __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
 #pragma unroll
         for (int k2 = 0; k2 < 16; ++k2) lr[k2] = k2 == j ? exact_lr : lr[k2];
       }
-      float mx = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(lr[j]));
-      mx = wave_max(mx);
-      if ((tid & 63) == 0) s_max[tid >> 6] = mx;
-      __syncthreads();
-      mx = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+      const float mx = page_abs_max(lr, s_max, tid);
       const float ls = mx == 0.0f ? 1e-6f : mx;
       const uint16_t ls16 = f2h(ls / 127.0f);
       const float lsf = h2f(ls16);
@@ -227,7 +231,7 @@ __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
     // code = int8(clip(rint(v / s))) with an fp16 quotient for fp16 inputs.
     float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(raw_val(vraw, i)));
+    for (int i = 0; i < 32; ++i) m = max_abs_nan(m, raw_val(vraw, i));
     uint16_t s16 = f2h(m / 127.0f);
     if ((s16 & 0x7fffu) == 0) s16 = kF16VScaleFloor;
     const float s = h2f(s16);
@@ -268,6 +272,13 @@ __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
 constexpr int kEncDefault = 0;
 constexpr int kEncFast = 1;
 
+// x (an fp32 value holding an fp16 number) times s in fp32, rounded once: an
+// explicit FMA with a +0 addend, which the backend takes as one mixed-precision
+// FMA (v_fma_mix_f32) reading the fp16 operand directly.  A -0 product reads
+// as +0; the callers only test the result's distance from fp16 rounding
+// midpoints, which the sign of zero does not change.
+__device__ __forceinline__ float mul_f16_f32(float x, float s) { return __builtin_fmaf(x, s, 0.0f); }
+
 // fp16 (a16 + pi) as fp32, the numerator of the angle code (encoder.py:46-50).
 __device__ __forceinline__ float code_numerator(uint16_t a16) { return h2f(f2h(h2f(a16) + h2f(kF16Pi))); }
 
@@ -279,22 +290,27 @@ __device__ __forceinline__ float code_arg(float n16) {
 
 // The fast path's angle code of pair (x, y), as the argument of the byte
 // conversion, and whether it cannot be trusted: the fp32 atan2 or the fp32
-// quotient lies near an fp16 rounding midpoint.  An angle below 2^-14 leaves
-// fp16(a + pi) = fp16(pi) whichever way it rounds, so neither guard needs the
-// subnormal test, and atan2(+-0, x >= 0) = +-0 comes out of atan2_poly exactly.
+// quotient lies near an fp16 rounding midpoint, or x or y is NaN (atan2_poly's
+// min / max drop a NaN operand; the reference's NaN angle gives code 0).  An
+// angle below 2^-14 leaves fp16(a + pi) = fp16(pi) whichever way it rounds, so
+// neither guard needs the subnormal test, and atan2(+-0, x >= 0) = +-0 comes
+// out of atan2_poly exactly.
 template <int kBits>
 __device__ __forceinline__ float angle_arg_fast(float x, float y, bool* flag) {
   const float a = atan2_poly(y, x);
-  const float q = code_numerator(f2h(a)) * kF32InvF16TwoPi;
-  *flag = near_f16_midpoint_code<kGuardAtan2>(a) | near_f16_midpoint_code<kGuardDiv>(q);
+  const float q = mul_f16_f32(code_numerator(f2h(a)), kF32InvF16TwoPi);
+  *flag = near_f16_midpoint_code<kGuardAtan2>(a) | near_f16_midpoint_code<kGuardDiv>(q) |
+          __builtin_isunordered(x, y);
   return code_arg<kBits>(h2f(f2h(q)));
 }
 
 // Exact angle code of pair (x, y): correctly rounded fp16 atan2, except that
 // the float64 atan2 runs only when the two fp16 candidates around the fast
-// result's rounding midpoint give different codes.
+// result's rounding midpoint give different codes.  A NaN x or y gives the
+// NaN angle's code, 0 (angle_code_f16).
 template <int kBits>
 __device__ __forceinline__ uint32_t exact_angle_code(float y, float x) {
+  if (__builtin_isunordered(x, y)) return 0u;
   const float a = atan2_poly(y, x);
   const uint16_t a16 = f2h(a);
   const uint32_t c0 = angle_code_f16(a16, kBits);
@@ -312,7 +328,7 @@ __device__ __forceinline__ uint32_t exact_angle_code(float y, float x) {
 // written into byte `sel` of `old`, and whether the fp32 quotient is too close
 // to an fp16 midpoint to trust.
 __device__ __forceinline__ uint32_t vcode_fast_byte(float v, float rs, uint32_t sel, uint32_t old, bool* near) {
-  const float q = v * rs;
+  const float q = mul_f16_f32(v, rs);
   *near = near_f16_midpoint_code<kGuardDiv>(q);
   return __builtin_amdgcn_cvt_pk_u8_f32(h2f(f2h(q)) + 128.0f, sel, old);
 }
@@ -326,7 +342,7 @@ template <int L>
 __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
   constexpr bool kFastLayout = L == kEncFast;
   constexpr int kBits = kFastLayout ? 8 : 4;
-  __shared__ float s_max[4];
+  __shared__ uint32_t s_max[4];
 
   const int page = blockIdx.x;
   const int64_t bh = blockIdx.y;
@@ -404,28 +420,29 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
 #pragma unroll
       for (int k2 = 0; k2 < 16; ++k2) lr[k2] = k2 == j ? exact_lr : lr[k2];
     }
-    float mx = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(lr[j]));
-    mx = wave_max(mx);
-    if ((tid & 63) == 0) s_max[tid >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    const float mx = page_abs_max(lr, s_max, tid);
     const float ls = mx == 0.0f ? 1e-6f : mx;
     const uint16_t ls16 = f2h(ls / 127.0f);
     const float lsf = h2f(ls16);
     // code = int8(clip(rint(f32(lr / ls)))): a reciprocal product is within 2
     // ulps of the correctly rounded quotient, and |quotient| <= 128, so rint
     // agrees unless the product is within 2^-13 of a half-integer; those are
-    // redone with the division.  NaN quotients (0 / 0 scale) give code 0.
+    // redone with the division.  NaN quotients give code 0, and they come only
+    // from a scale that is 0 (every lr is 0: 0 / 0), inf (lr / inf is 0 or NaN)
+    // or NaN (a NaN lr): then every code of the page is 0, and otherwise every
+    // lr is finite.
     const float rl = __builtin_amdgcn_rcpf(lsf);
-    uint32_t packed[4] = {0u, 0u, 0u, 0u};
+    const bool zero_codes = !(lsf != 0.0f && fabsf(lsf) < INFINITY);  // uniform over the page
+    uint32_t packed[4] = {0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
     uint32_t dfix = 0;
+    if (!zero_codes) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float qd = lr[j] * rl;
-      dfix |= fabsf(qd - floorf(qd) - 0.5f) <= 0x1p-13f ? (1u << j) : 0u;
-      packed[j >> 2] = __builtin_amdgcn_cvt_pk_u8_f32((qd == qd ? qd : 0.0f) + 128.0f, (uint32_t)(j & 3), packed[j >> 2]);
+      for (int j = 0; j < 16; ++j) {
+        const float qd = lr[j] * rl;
+        // v_fract_f32 is qd - floor(qd) here (|qd| <= 128; it caps just below 1).
+        dfix |= fabsf(__builtin_amdgcn_fractf(qd) - 0.5f) <= 0x1p-13f ? (1u << j) : 0u;
+        packed[j >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(qd + 128.0f, (uint32_t)(j & 3), packed[j >> 2]);
+      }
     }
     while (dfix) {
       const int j = __builtin_ctz(dfix);
@@ -459,7 +476,8 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
   // Values (v_quant/encoder.py:21-25): s = f16(max|v| / 127) (1e-4 if zero),
   // code = int8(clip(rint(f16(v / s)), -128, 127)).  The group maximum is an
   // integer maximum of the |v| bit patterns, which orders finite fp16 values
-  // like fmaxf and exceeds 0x7c00 exactly when the group holds a NaN.
+  // and inf like fmaxf and puts every NaN above inf: a NaN makes the maximum
+  // NaN (nan_max, tp_common.h), so the scale is NaN and every code 0.
   RawRow32<false> vraw;
   load_row32<false>(a.v, in_off, valid, vraw);
   uint32_t mbits = 0;
@@ -470,16 +488,7 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
   }
   // inf or NaN in the group: exact path (v / inf and NaN quotients give code 0).
   const bool nonfinite = mbits >= 0x7c00u;
-  uint32_t mb = mbits;
-  if (mbits > 0x7c00u) {  // a NaN: the scale comes from the largest non-NaN |v|, as with fmaxf
-    mb = 0;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const uint32_t hb = (raw_word(vraw, i >> 1) >> (16 * (i & 1))) & 0x7fffu;
-      mb = hb <= 0x7c00u ? max(mb, hb) : mb;
-    }
-  }
-  uint16_t s16 = f2h(h2f((uint16_t)mb) / 127.0f);
+  uint16_t s16 = f2h(h2f((uint16_t)mbits) / 127.0f);
   if ((s16 & 0x7fffu) == 0) s16 = kF16VScaleFloor;
   const float s = h2f(s16);
   const float rs = __builtin_amdgcn_rcpf(s);
@@ -520,7 +529,7 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
 // One thread per group of `group` values of a row of `dim` (v_quant/encoder.py:
 // 16-30): s = f16(max|v| / 127) (fp16(1e-4) if zero), code = int8(clip(rint(v
 // / s))), the quotient rounded to fp16 first for fp16 input.  A NaN in the
-// group is skipped by the maximum, as in the page encoder.
+// group makes the maximum NaN (nan_max), as in the page encoder.
 template <bool F32IN>
 __global__ __launch_bounds__(256) void quantize_groups_kernel(const void* v, int64_t n_groups, int32_t group,
                                                               int8_t* codes, uint16_t* scales) {
@@ -532,7 +541,7 @@ __global__ __launch_bounds__(256) void quantize_groups_kernel(const void* v, int
     else return h2f(static_cast<const uint16_t*>(v)[base + i]);
   };
   float m = 0.0f;
-  for (int i = 0; i < group; ++i) m = fmaxf(m, fabsf(val(i)));
+  for (int i = 0; i < group; ++i) m = max_abs_nan(m, val(i));
   uint16_t s16 = f2h(m / 127.0f);
   if ((s16 & 0x7fffu) == 0) s16 = kF16VScaleFloor;
   const float s = h2f(s16);
@@ -545,8 +554,8 @@ __global__ __launch_bounds__(256) void quantize_groups_kernel(const void* v, int
 
 // One workgroup per (b, h) row of n fp16 radii (encoder.py:34-42): lr =
 // f32(f16 log(max(r, fp16(1e-6)))), scale = f16(max|lr| / 127) (max 0 ->
-// 1e-6), code = int8(clip(rint(lr / scale))).  The maximum skips NaN, as in
-// the page encoder.
+// 1e-6), code = int8(clip(rint(lr / scale))).  A NaN log radius makes the
+// maximum NaN (nan_max), as in the page encoder.
 __global__ __launch_bounds__(256) void log_radii_rows_kernel(const uint16_t* radii, int64_t n, int8_t* codes,
                                                              uint16_t* scales) {
   __shared__ float s_max[256];
@@ -557,11 +566,11 @@ __global__ __launch_bounds__(256) void log_radii_rows_kernel(const uint16_t* rad
     return h2f(log_f16(h2f(rb)));
   };
   float m = 0.0f;
-  for (int64_t i = threadIdx.x; i < n; i += 256) m = fmaxf(m, fabsf(log_r(i)));
+  for (int64_t i = threadIdx.x; i < n; i += 256) m = max_abs_nan(m, log_r(i));
   s_max[threadIdx.x] = m;
   __syncthreads();
   for (int w = 128; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) s_max[threadIdx.x] = fmaxf(s_max[threadIdx.x], s_max[threadIdx.x + w]);
+    if ((int)threadIdx.x < w) s_max[threadIdx.x] = nan_max(s_max[threadIdx.x], s_max[threadIdx.x + w]);
     __syncthreads();
   }
   const float mx = s_max[0];
