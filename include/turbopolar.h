@@ -75,9 +75,11 @@ typedef struct tp_pages {
  * it passes QJLPayload.packed_signs / norms and q_proj_signs as separate
  * arrays, metal.py:532-571).  signs: uint8 [bh][capacity][64][proj_dim / 8],
  * one sketch per token, page p of row bh in slot bh * capacity + p as in the
- * page store (16-byte aligned); norms: fp16 [bh][capacity][64] residual norms
- * (8-byte aligned); q_signs: uint8 [batch][hq][proj_dim / 8] sketches of the
- * queries (8-byte aligned).  The kernels take proj_dim == 64. */
+ * page store; norms: fp16 [bh][capacity][64] residual norms; q_signs: uint8
+ * [batch][hq][proj_dim / 8] sketches of the queries.  proj_dim: a multiple of
+ * 8 from 8 to 256 (turbo_polar_config.py:34-37 takes any positive multiple of
+ * 8).  Alignment: proj_dim == 64 (the kernels' 64-bit path) signs 16-byte,
+ * norms and q_signs 8-byte; any other width signs 4-byte, norms 2-byte. */
 typedef struct tp_qjl {
   const void* signs;
   const void* norms;
@@ -219,6 +221,7 @@ typedef struct tp_bounds_case {
   int64_t v_capacity;
   int32_t kernel;
   int32_t mutate;
+  int32_t qjl_bits; /* QJL sketch bits (0 reads as 64) */
 } tp_bounds_case;
 unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c, char* msg, int32_t msg_len);
 

@@ -24,7 +24,7 @@ LAYOUTS = {"default": (0, 4, 4, 64), "fast": (1, 4, 8, 0), "deep2": (0, 4, 2, 64
 
 
 def run(layout="default", batch=1, hq=32, hkv=8, n_pages=64, capacity=None, tail=0, tail_stride=None, seq=None,
-        pps=0, qjl=False, dense_v=False, kernel=0, mutate=0):
+        pps=0, qjl=False, dense_v=False, kernel=0, mutate=0, qjl_bits=0):
     c = _lib.TPBoundsCase()
     c.batch, c.hq, c.hkv = batch, hq, hkv
     c.layout = _lib.make_layout(*LAYOUTS[layout])
@@ -36,7 +36,7 @@ def run(layout="default", batch=1, hq=32, hkv=8, n_pages=64, capacity=None, tail
     c.pages_per_split = pps
     c.qjl, c.qjl_capacity = int(qjl), n_pages
     c.dense_v, c.v_capacity = int(dense_v), n_pages
-    c.kernel, c.mutate = kernel, mutate
+    c.kernel, c.mutate, c.qjl_bits = kernel, mutate, qjl_bits
     msg = ctypes.create_string_buffer(512)
     bad = _lib.lib().tp_selftest_decode_bounds(ctypes.byref(c), msg, 512)
     return bad, msg.value.decode()
@@ -72,6 +72,10 @@ CASES = [
     dict(hq=24, hkv=2, n_pages=20, qjl=True),          # GQA 12: the row token order of default pages
     dict(hq=40, hkv=2, n_pages=9, pps=2, dense_v=True),
     dict(hq=8, hkv=2, n_pages=9, pps=2, qjl=True, tail=5, tail_stride=5),
+    dict(n_pages=33, qjl=True, qjl_bits=40),           # QJL of any width: sketch dwords at byte offsets
+    dict(hq=24, hkv=2, n_pages=7, pps=2, qjl=True, qjl_bits=8),
+    dict(n_pages=5, pps=4, qjl=True, qjl_bits=256, layout="fast"),
+    dict(hq=4, hkv=4, n_pages=3, qjl=True, qjl_bits=24, dense_v=True),
 ]
 
 

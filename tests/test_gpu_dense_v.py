@@ -163,6 +163,18 @@ def test_dense_v_qjl_matches_oracle(device, layout_name, hq, hkv, S, pps, masked
     assert max_abs(plain, ref) > 1e-5
 
 
+@pytest.mark.parametrize("P", [16, 40])
+def test_dense_v_qjl_any_width(device, P):
+    """Dense V with QJL sketches of a width other than 64."""
+    block, _, host, _, _, q, qd, pay, qs, tup = _qjl_case(device, "default", 32, 8, 5, 0, 47, P=P)
+    vd = _dense_v(48, 1, 8, 5, 5)
+    seq = 5 * PAGE - 9
+    out = kernels.decode_attention_dense_v(qd, PageSet(block, None), torch.from_numpy(vd).to(device), seq,
+                                           SCALE16, pages_per_split=2, qjl=QJLPages(pay, qs))
+    ref = oracle.cpu_online_attention_dense_v(q, _blk(host), vd, SCALE16, seq, qjl=tup)
+    _check(out.float().cpu().numpy(), ref, f"dense_v qjl P={P}")
+
+
 def test_bridge_dense_v(device):
     block, _, host, _, _, q, qd, pay, qs, tup = _qjl_case(device, "default", 8, 2, 3, 0, 29)
     vt = torch.from_numpy(_dense_v(30, 1, 2, 3, 3)).to(device)

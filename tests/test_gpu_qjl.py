@@ -27,8 +27,8 @@ from turbopolar_amd.qjl import QJLPages, QJLResidualEncoder, qjl_dot_estimate
 pytestmark = pytest.mark.gpu
 
 
-def _cfg(hq=4, hkv=2):
-    return TurboPolarConfig(num_q_heads=hq, num_kv_heads=hkv, qjl_proj_dim=64)
+def _cfg(hq=4, hkv=2, P=64):
+    return TurboPolarConfig(num_q_heads=hq, num_kv_heads=hkv, qjl_proj_dim=P)
 
 
 def _fp16_ulp(x):
@@ -68,15 +68,15 @@ def _residual_payload(enc, block, k_full, S):
     return enc.compute_residual_sketch(res)
 
 
-def _qjl_case(device, layout_name, hq, hkv, S, tail, seed, B=1):
+def _qjl_case(device, layout_name, hq, hkv, S, tail, seed, B=1, P=64):
     block, qv, host, tk, tv, q = build_case(device, LAYOUTS[layout_name], hq, hkv, S, tail, seed=seed, B=B)
     from common import gen_kv
     k, _ = gen_kv(seed, B, hkv, S * PAGE + tail, "normal", np.float16)
-    enc = QJLResidualEncoder(_cfg(hq, hkv))
+    enc = QJLResidualEncoder(_cfg(hq, hkv, P))
     pay = _residual_payload(enc, block, torch.from_numpy(k[:, :, :S * PAGE]).to(device), S)
     qd = torch.from_numpy(q).to(device)
     qs = enc.query_signs(qd)
-    tup = (pay.packed_signs.cpu().numpy(), pay.norms.cpu().numpy(), qs.cpu().numpy(), 64)
+    tup = (pay.packed_signs.cpu().numpy(), pay.norms.cpu().numpy(), qs.cpu().numpy(), P)
     return block, qv, host, tk, tv, q, qd, pay, qs, tup
 
 
@@ -87,9 +87,12 @@ def test_dot_estimate_matches_oracle(device):
     assert np.allclose(got, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
 
 
-@pytest.mark.parametrize("layout_name,hq,hkv,S", [("default", 8, 2, 3), ("fast", 32, 8, 2), ("default", 64, 8, 2)])
-def test_fused_qk_qjl_matches_oracle(device, layout_name, hq, hkv, S):
-    block, qv, host, tk, tv, q, qd, pay, qs, tup = _qjl_case(device, layout_name, hq, hkv, S, 0, 3 + S)
+@pytest.mark.parametrize("layout_name,hq,hkv,S,P", [("default", 8, 2, 3, 64), ("fast", 32, 8, 2, 64), ("default", 64, 8, 2, 64),
+                                                   ("default", 8, 2, 3, 8), ("fast", 32, 8, 2, 40),
+                                                   ("default", 24, 2, 2, 256), ("deep2", 8, 2, 2, 24)])
+def test_fused_qk_qjl_matches_oracle(device, layout_name, hq, hkv, S, P):
+    print(f"[qjl qk] {layout_name} hq={hq} hkv={hkv} S={S} P={P}", flush=True)
+    block, qv, host, tk, tv, q, qd, pay, qs, tup = _qjl_case(device, layout_name, hq, hkv, S, 0, 3 + S, P=P)
     got = kernels.fused_qk(qd, PageSet(block, None), SCALE16, qjl=QJLPages(pay, qs)).float().cpu().numpy()
     blk = {k_: host[k_] for k_ in ("radii", "radii_scales", "angle_codes_l1", "angle_codes_deep", "metadata")}
     if blk["radii_scales"] is not None:
@@ -128,6 +131,47 @@ def test_decode_attention_qjl_matches_oracle(device, layout_name, hq, hkv, S, ta
     # The correction takes part: the oracle without it gives another output.
     plain = oracle_out(host, tk, tv, q, seq)
     assert max_abs(plain, ref) > 1e-5
+
+
+@pytest.mark.parametrize("layout_name,hq,hkv,S,tail,pps,masked,P", [
+    ("default", 32, 8, 5, 0, 2, 0, 8),      # half-row token order, one sketch byte per token
+    ("default", 32, 8, 6, 37, 2, 5, 40),    # 5 bytes per token: sketches at every byte offset of a dword
+    ("default", 24, 2, 5, 9, 2, 3, 24),     # GQA 12: row token order
+    ("fast", 64, 8, 4, 9, 1, 0, 128),
+    ("fast", 32, 8, 17, 11, 6, 0, 256),     # 4-wave workgroups
+    ("default", 8, 1, 70, 5, 1, 0, 32),     # two-tier combine
+    ("deep2", 8, 2, 3, 0, 0, 0, 56),        # generic layout kernel
+])
+def test_decode_attention_qjl_any_width(device, layout_name, hq, hkv, S, tail, pps, masked, P):
+    """qjl_proj_dim other than 64 (turbo_polar_config.py:36-37 takes any
+    positive multiple of 8): the byte-aligned sketch path against the oracle."""
+    print(f"[qjl attn P] {layout_name} hq={hq} hkv={hkv} S={S} tail={tail} pps={pps} masked={masked} P={P}", flush=True)
+    block, qv, host, tk, tv, q, qd, pay, qs, tup = _qjl_case(device, layout_name, hq, hkv, S, tail, 29 + S, P=P)
+    assert pay.packed_signs.shape[-1] == P // 8
+    seq = S * PAGE + tail - masked
+    tkt = torch.from_numpy(tk).to(device) if tail else None
+    tvt = torch.from_numpy(tv).to(device) if tail else None
+    out = kernels.decode_attention(qd, PageSet(block, qv), tkt, tvt, seq, SCALE16, pages_per_split=pps,
+                                   qjl=QJLPages(pay, qs)).float().cpu().numpy()
+    blk = {k_: host[k_] for k_ in ("radii", "radii_scales", "angle_codes_l1", "angle_codes_deep", "metadata")}
+    if blk["radii_scales"] is not None:
+        blk["radii_scales"] = blk["radii_scales"].reshape(blk["radii"].shape[:3] + (1, 1))
+    ref = oracle.cpu_online_attention_dense_tail(q, blk, (host["v_codes"], host["v_scales"]), tk, tv, SCALE16, seq,
+                                                 qjl=tup)
+    assert np.all(np.isfinite(out))
+    ma, rl = max_abs(out, ref), rel_l2(out, ref)
+    assert ma <= ATOL and rl <= RTOL_L2, f"max_abs={ma:.3g} rel_l2={rl:.3g}"
+    plain = oracle_out(host, tk, tv, q, seq)
+    assert max_abs(plain, ref) > 1e-5
+
+
+def test_qjl_width_outside_the_kernels_rejected(device):
+    from turbopolar_amd.qjl import QJLPayload
+    signs = torch.zeros((1, 2, 2, 64, 33), dtype=torch.uint8, device=device)
+    norms = torch.zeros((1, 2, 2, 64), dtype=torch.float16, device=device)
+    qs = torch.zeros((1, 8, 33), dtype=torch.uint8, device=device)
+    with pytest.raises(NotImplementedError, match="multiple of 8 up to 256"):
+        QJLPages(QJLPayload(signs, norms, 264, 42, (1, 2, 2, 64, 128)), qs)
 
 
 def test_bridge_qjl_paths(device):

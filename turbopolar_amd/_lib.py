@@ -83,6 +83,7 @@ class TPBoundsCase(ctypes.Structure):
         ("v_capacity", c_i64),
         ("kernel", c_i32),
         ("mutate", c_i32),
+        ("qjl_bits", c_i32),
     ]
 
 

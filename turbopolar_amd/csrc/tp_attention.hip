@@ -150,6 +150,7 @@ struct AttnArgs {
   const uint16_t* qjl_norms;
   const uint64_t* q_signs;
   int64_t qjl_capacity;  // sketch slots per bh
+  int32_t qjl_bits;      // sketch bits P (a multiple of 8, 8 .. 256)
   // Dense fp16 values instead of the V codes (tp_decode_attention_dense_v):
   // [bkv][v_capacity pages][64][128].  Last, so the other fields keep their
   // argument offsets.
@@ -366,6 +367,11 @@ __host__ __device__ inline int64_t qjl_sign_base(int64_t slot, int l4, bool hr =
 __host__ __device__ inline int64_t qjl_norm_base(int64_t slot, int l4, bool hr = false) {
   return (slot * kPageTokens + (hr ? 2 : 4) * l4) * 2;
 }
+// Any sketch width (nb = P/8 bytes per token): token t's sketch starts at byte
+// qjl_any_row(slot, t, nb); its loads are the qjl_any_dwords(row & 3, nb)
+// dwords from row - (row & 3); its fp16 norm is at byte 2 * (slot * 64 + t).
+__host__ __device__ inline int64_t qjl_any_row(int64_t slot, int t, int nb) { return (slot * kPageTokens + t) * nb; }
+__host__ __device__ inline int qjl_any_dwords(int sh, int nb) { return (sh + nb + 3) >> 2; }
 
 // A wave's first page loads: a wave with a page of its own (page < p_end)
 // loads it; a wave without one issues the same loads with every lane on lane
@@ -397,20 +403,29 @@ __host__ __device__ inline int fold_record(int r0, int u, int mine) { return r0 
 //
 // tqpolar_fused_qk.metal:200-231, metal.py:262-275 and score_estimate.py:6-54:
 // the score of token t for query head h gains |E_t| |q_h| sin(pi/2 (P - 2
-// hamming(sketch_t, sketch_h)) / P) (before the attention scale), P = 64
-// sketch bits.  The sine of the 65 possible Hamming distances is a table in LDS.
+// hamming(sketch_t, sketch_h)) / P) (before the attention scale), P sketch
+// bits (qjl/encoder.py:19-44 packs them little-endian, P/8 bytes per token).
+// The sine of the P + 1 possible Hamming distances is a table in LDS.  Two
+// kernel forms: kQjl64 (P = 64, the default; one 8-byte word per token, 16-byte
+// loads of two tokens) and kQjlAny (any multiple of 8 up to kQjlMaxBits: the
+// dwords covering a token's P/8 bytes, byte-aligned in registers).
 
+constexpr int kQjlOff = 0;
+constexpr int kQjl64 = 1;
+constexpr int kQjlAny = 2;
 constexpr int kQjlBits = 64;
+constexpr int kQjlMaxBits = 256;
+constexpr int kQjlMaxWords = kQjlMaxBits / 32;
 
-__device__ __forceinline__ void build_qjl_sin(float* tab, int tid) {
-  if (tid <= kQjlBits) tab[tid] = sinf(1.57079632679489662f * (float)(kQjlBits - 2 * tid) / (float)kQjlBits);
+__device__ __forceinline__ void build_qjl_sin(float* tab, int tid, int P) {
+  for (int t = tid; t <= P; t += blockDim.x) tab[t] = sinf(1.57079632679489662f * (float)(P - 2 * t) / (float)P);
 }
 
 // |q| of the lane's head from its MFMA B operands (row order: 32 dims per
 // lane, lane groups l4 = 0..3 hold the four quarters; half-row order: 16 dims
 // per lane, the four lane groups of columns l16 and l16 ^ 8 hold the two
-// halves) and the head's sketch.
-template <bool HR>
+// halves) and, for kQjl64, the head's sketch.
+template <bool HR, int QJL>
 __device__ __forceinline__ void qjl_query(const AttnArgs& a, int b, int kv, int h0, int nh, int l16, const half8v* qb,
                                           uint64_t& qsig, float& qnorm) {
   float ss = 0.0f;
@@ -426,11 +441,30 @@ __device__ __forceinline__ void qjl_query(const AttnArgs& a, int b, int kv, int 
   ss += __shfl_xor(ss, 32, 64);
   if constexpr (HR) ss += __shfl_xor(ss, 8, 64);
   qnorm = sqrtf(ss);
-  qsig = a.q_signs[(int64_t)b * a.hq + (int64_t)kv * a.g + h0 + min(l16, nh - 1)];  // unconditional, as load_q
+  if constexpr (QJL == kQjl64)
+    qsig = a.q_signs[(int64_t)b * a.hq + (int64_t)kv * a.g + h0 + min(l16, nh - 1)];  // unconditional, as load_q
+}
+
+// kQjlAny: the sketches of the block's heads as words in LDS, qw[8 h + w] =
+// bytes 4w .. 4w+3 of head h's P/8 (zero past them), one word per thread.
+__device__ __forceinline__ void qjl_query_words(const AttnArgs& a, int b, int kv, int h0, int nh, int tid,
+                                                uint32_t* qw) {
+  if (tid < 16 * kQjlMaxWords) {
+    const int h = tid / kQjlMaxWords, w = tid % kQjlMaxWords;
+    const int nb = a.qjl_bits >> 3;
+    const uint8_t* row = reinterpret_cast<const uint8_t*>(a.q_signs) + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + h) * nb;
+    uint32_t word = 0;
+    if (h < nh) {
+      for (int j = 0; j < 4; ++j) {
+        if (4 * w + j < nb) word |= (uint32_t)row[4 * w + j] << (8 * j);
+      }
+    }
+    qw[tid] = word;
+  }
 }
 
 // Adds the correction to one page's scores s[mt][i] (token score_token(mt,
-// i, l4, HR), head l16) of page slot `slot`.
+// i, l4, HR), head l16) of page slot `slot`, P = 64.
 template <bool HR>
 __device__ __forceinline__ void qjl_correct(const AttnArgs& a, int64_t slot, int l4, uint64_t qsig, float qnorm,
                                             const float* sin_tab, float4v* s) {
@@ -452,6 +486,48 @@ __device__ __forceinline__ void qjl_correct(const AttnArgs& a, int64_t slot, int
                         h2f((uint16_t)(nn.y >> 16))};
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[mt][i] += n[i] * qnorm * sin_tab[__builtin_popcountll(k[i] ^ qsig)];
+  }
+}
+
+// The same for any P (kQjlAny).  Token t's sketch is the P/8 bytes at byte
+// (slot * 64 + t) * P/8; the lane loads the dwords covering them (a page's
+// 64 * P/8 bytes start and end on a dword boundary, so they never leave the
+// page's sketches) and aligns them by the byte offset.  qw: the block's query
+// words (qjl_query_words), head_row: the lane's head in them.
+template <bool HR>
+__device__ __forceinline__ void qjl_correct_any(const AttnArgs& a, int64_t slot, int l4, const uint32_t* qw,
+                                                int head_row, float qnorm, const float* sin_tab, float4v* s) {
+  const int nb = a.qjl_bits >> 3;
+  const int nw = (nb + 3) >> 2;
+  const uint32_t last_mask = (nb & 3) ? (1u << (8 * (nb & 3))) - 1u : 0xffffffffu;
+  uint32_t q[kQjlMaxWords];
+#pragma unroll
+  for (int w = 0; w < kQjlMaxWords; ++w) q[w] = qw[kQjlMaxWords * head_row + w];
+  const char* sg = reinterpret_cast<const char*>(a.qjl_signs);
+  const uint16_t* nm = a.qjl_norms + slot * kPageTokens;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = score_token(mt, i, l4, HR);
+      const int64_t o = qjl_any_row(slot, t, nb);
+      const int sh = (int)(o & 3);
+      const uint32_t* p = reinterpret_cast<const uint32_t*>(sg + (o - sh));
+      const int cnt = qjl_any_dwords(sh, nb);
+      uint32_t d[kQjlMaxWords + 1];
+#pragma unroll
+      for (int k = 0; k <= kQjlMaxWords; ++k) d[k] = k < cnt ? p[k] : 0u;
+      int ham = 0;
+#pragma unroll
+      for (int w = 0; w < kQjlMaxWords; ++w) {
+        if (w < nw) {
+          uint32_t tw = __builtin_amdgcn_alignbyte(d[w + 1], d[w], (uint32_t)sh);
+          if (w == nw - 1) tw &= last_mask;
+          ham += __builtin_popcount(tw ^ q[w]);
+        }
+      }
+      s[mt][i] += h2f(nm[t]) * qnorm * sin_tab[ham];
+    }
   }
 }
 
@@ -1316,7 +1392,7 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
 
 // ---- decode attention kernel ---------------------------------------------------
 
-template <int KIND, int WAVES, int FL = 0, bool QJL = false, bool DV = false>
+template <int KIND, int WAVES, int FL = 0, int QJL = kQjlOff, bool DV = false>
 __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a) {
   // The fold maps the threads onto heads x 128 dims at 4 dims per thread (512
   // threads: 16 heads, 256 threads: 8), and the combine sizes its split groups
@@ -1399,12 +1475,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   TP_STAMP(1);
   if (tid < 256) build_lut<KIND>(sh.lut, a, tid);
   TP_STAMP(3);
-  __shared__ float qjl_sin[QJL ? kQjlBits + 1 : 1];
+  __shared__ float qjl_sin[QJL != kQjlOff ? kQjlMaxBits + 1 : 1];
+  __shared__ uint32_t qjl_qw[QJL == kQjlAny ? 16 * kQjlMaxWords : 1];
   uint64_t qsig = 0;
   float qnorm = 0.0f;
-  if constexpr (QJL) {
-    build_qjl_sin(qjl_sin, tid);
-    qjl_query<HR>(a, b, kv, h0, nh, l16, qb, qsig, qnorm);
+  if constexpr (QJL != kQjlOff) {
+    build_qjl_sin(qjl_sin, tid, a.qjl_bits);
+    qjl_query<HR, QJL>(a, b, kv, h0, nh, l16, qb, qsig, qnorm);
+    if constexpr (QJL == kQjlAny) qjl_query_words(a, b, kv, h0, nh, tid, qjl_qw);
   }
   lds_barrier();
   TP_STAMP(2);
@@ -1426,7 +1504,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   for (int it = 0; page + WAVES < p_end; page += WAVES, ++it) {
     float4v s[4];
     qk_regs<KIND>(a, sh.lut, kr, qb, l16, l4, s);
-    if constexpr (QJL) qjl_correct<HR>(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
+    if constexpr (QJL == kQjl64) qjl_correct<HR>(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
+    if constexpr (QJL == kQjlAny)
+      qjl_correct_any<HR>(a, bkv * a.qjl_capacity + page, l4, qjl_qw, HR ? (l16 & 7) : l16, qnorm, qjl_sin, s);
     if (it < 12) TP_STAMP(4 + 4 * it);
     load_k<KIND>(a, bkv * a.capacity + page + WAVES, l16, l4, kr);
     half8v pb[2];
@@ -1441,7 +1521,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   if (page < p_end) {
     float4v s[4];
     qk_regs<KIND>(a, sh.lut, kr, qb, l16, l4, s);
-    if constexpr (QJL) qjl_correct<HR>(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
+    if constexpr (QJL == kQjl64) qjl_correct<HR>(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
+    if constexpr (QJL == kQjlAny)
+      qjl_correct_any<HR>(a, bkv * a.qjl_capacity + page, l4, qjl_qw, HR ? (l16 & 7) : l16, qnorm, qjl_sin, s);
     const int valid = (int)min((int64_t)kPageTokens, a.seq_len - (int64_t)page * kPageTokens);
     half8v pb[2];
     softmax_page<HR>(s, valid, a.scale_log2, l4, m_run, l_run, acc, pb);
@@ -1500,10 +1582,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
 constexpr int kQkRow = 72;  // halves per staged head row
 constexpr int kQkWaves = 8;
 
-template <int KIND, bool QJL = false>
+template <int KIND, int QJL = kQjlOff>
 __global__ __launch_bounds__(kQkWaves * 64) void fused_qk_kernel(AttnArgs a) {
   __shared__ Lut lut;
-  __shared__ float qjl_sin[QJL ? kQjlBits + 1 : 1];
+  __shared__ float qjl_sin[QJL != kQjlOff ? kQjlMaxBits + 1 : 1];
+  __shared__ uint32_t qjl_qw[QJL == kQjlAny ? 16 * kQjlMaxWords : 1];
   __shared__ uint4 stage[kQkWaves][16 * kQkRow / 8];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1526,15 +1609,17 @@ __global__ __launch_bounds__(kQkWaves * 64) void fused_qk_kernel(AttnArgs a) {
   if (tid < 256) build_lut<KIND>(lut, a, tid);
   uint64_t qsig = 0;
   float qnorm = 0.0f;
-  if constexpr (QJL) {
-    build_qjl_sin(qjl_sin, tid);
-    qjl_query<false>(a, b, kv, h0, nh, l16, qb, qsig, qnorm);
+  if constexpr (QJL != kQjlOff) {
+    build_qjl_sin(qjl_sin, tid, a.qjl_bits);
+    qjl_query<false, QJL>(a, b, kv, h0, nh, l16, qb, qsig, qnorm);
+    if constexpr (QJL == kQjlAny) qjl_query_words(a, b, kv, h0, nh, tid, qjl_qw);
   }
   __syncthreads();
   if (page >= a.n_pages) return;
   float4v s[4];
   qk_regs<KIND>(a, lut, kr, qb, l16, l4, s);
-  if constexpr (QJL) qjl_correct<false>(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
+  if constexpr (QJL == kQjl64) qjl_correct<false>(a, bkv * a.qjl_capacity + page, l4, qsig, qnorm, qjl_sin, s);
+  if constexpr (QJL == kQjlAny) qjl_correct_any<false>(a, bkv * a.qjl_capacity + page, l4, qjl_qw, l16, qnorm, qjl_sin, s);
   uint16_t* st = reinterpret_cast<uint16_t*>(&stage[wave][0]);
   if (l16 < nh) {
 #pragma unroll
@@ -1662,6 +1747,16 @@ static bool fill_common(AttnArgs& a, const void* q, int64_t batch, int32_t hq, i
   return true;
 }
 
+// The fused QK kernel of a layout kind and QJL form.
+template <int QJL>
+static void launch_fused_qk(const AttnArgs& a, int kind, dim3 grid, hipStream_t s) {
+  switch (kind) {
+    case kKindDefault: hipLaunchKernelGGL((fused_qk_kernel<kKindDefault, QJL>), grid, dim3(kQkWaves * 64), 0, s, a); break;
+    case kKindFast: hipLaunchKernelGGL((fused_qk_kernel<kKindFast, QJL>), grid, dim3(kQkWaves * 64), 0, s, a); break;
+    default: hipLaunchKernelGGL((fused_qk_kernel<kKindGeneric, QJL>), grid, dim3(kQkWaves * 64), 0, s, a); break;
+  }
+}
+
 }  // namespace tp
 
 using namespace tp;
@@ -1713,11 +1808,7 @@ int32_t tp_fused_qk(const void* q, int64_t batch, int32_t hq, int32_t hkv,
   a.scale = scale;
   const dim3 grid((unsigned)((n_pages + kQkWaves - 1) / kQkWaves), (unsigned)(batch * hkv), (unsigned)a.head_blocks);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (layout_kind(layout)) {
-    case kKindDefault: hipLaunchKernelGGL(fused_qk_kernel<kKindDefault>, grid, dim3(kQkWaves * 64), 0, s, a); break;
-    case kKindFast: hipLaunchKernelGGL(fused_qk_kernel<kKindFast>, grid, dim3(kQkWaves * 64), 0, s, a); break;
-    default: hipLaunchKernelGGL(fused_qk_kernel<kKindGeneric>, grid, dim3(kQkWaves * 64), 0, s, a); break;
-  }
+  launch_fused_qk<kQjlOff>(a, layout_kind(layout), grid, s);
   return launch_status("tp_fused_qk");
 }
 
@@ -1727,13 +1818,19 @@ static bool fill_qjl(AttnArgs& a, const tp_qjl* qjl, int32_t n_pages) {
     set_error("qjl_payload and q_proj_signs are required when use_qjl=True");
     return false;
   }
-  if (qjl->proj_dim != kQjlBits) {
-    set_error("the QJL kernels take proj_dim == %d sketch bits, got %d", kQjlBits, qjl->proj_dim);
+  const int P = qjl->proj_dim;
+  if (P < 8 || P > kQjlMaxBits || P % 8 != 0) {
+    set_error("QJL proj_dim must be a multiple of 8 from 8 to %d sketch bits, got %d", kQjlMaxBits, P);
     return false;
   }
-  if (!qjl->q_signs || ((uintptr_t)qjl->q_signs & 7u) ||
-      (n_pages > 0 && (!qjl->signs || !qjl->norms || ((uintptr_t)qjl->signs & 15u) || ((uintptr_t)qjl->norms & 7u)))) {
-    set_error("QJL buffers missing or misaligned (sketches 16-byte, norms and query sketches 8-byte aligned)");
+  // P = 64 reads 16-byte sketch pairs, 8-byte norm quads and 8-byte query
+  // sketches; any other P reads sketch dwords, fp16 norms and query bytes.
+  const bool p64 = P == kQjlBits;
+  if (!qjl->q_signs || (p64 && ((uintptr_t)qjl->q_signs & 7u)) ||
+      (n_pages > 0 && (!qjl->signs || !qjl->norms || ((uintptr_t)qjl->signs & (p64 ? 15u : 3u)) ||
+                       ((uintptr_t)qjl->norms & (p64 ? 7u : 1u))))) {
+    set_error(p64 ? "QJL buffers missing or misaligned (sketches 16-byte, norms and query sketches 8-byte aligned)"
+                  : "QJL buffers missing or misaligned (sketches 4-byte, norms 2-byte aligned)");
     return false;
   }
   if (n_pages > 0 && qjl->capacity < n_pages) {
@@ -1744,6 +1841,7 @@ static bool fill_qjl(AttnArgs& a, const tp_qjl* qjl, int32_t n_pages) {
   a.qjl_signs = static_cast<const uint64_t*>(qjl->signs);
   a.qjl_norms = static_cast<const uint16_t*>(qjl->norms);
   a.q_signs = static_cast<const uint64_t*>(qjl->q_signs);
+  a.qjl_bits = P;
   return true;
 }
 
@@ -1763,11 +1861,10 @@ int32_t tp_fused_qk_qjl(const void* q, int64_t batch, int32_t hq, int32_t hkv, c
   a.scale = scale;
   const dim3 grid((unsigned)((n_pages + kQkWaves - 1) / kQkWaves), (unsigned)(batch * hkv), (unsigned)a.head_blocks);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (layout_kind(layout)) {
-    case kKindDefault: hipLaunchKernelGGL((fused_qk_kernel<kKindDefault, true>), grid, dim3(kQkWaves * 64), 0, s, a); break;
-    case kKindFast: hipLaunchKernelGGL((fused_qk_kernel<kKindFast, true>), grid, dim3(kQkWaves * 64), 0, s, a); break;
-    default: hipLaunchKernelGGL((fused_qk_kernel<kKindGeneric, true>), grid, dim3(kQkWaves * 64), 0, s, a); break;
-  }
+  if (a.qjl_bits == kQjlBits)
+    launch_fused_qk<kQjl64>(a, layout_kind(layout), grid, s);
+  else
+    launch_fused_qk<kQjlAny>(a, layout_kind(layout), grid, s);
   return launch_status("tp_fused_qk_qjl");
 }
 
@@ -1782,7 +1879,7 @@ static int32_t launch_measure_variant(const AttnArgs& a, dim3 grid, int kind, hi
 // tp_decode_attention and, with qjl, tp_decode_attention_qjl.
 // The decode kernel of a layout kind, with the two-tier combine compiled in
 // only for launches that use it.
-template <int KIND, int W, bool QJL, bool DV = false>
+template <int KIND, int W, int QJL, bool DV = false>
 static void launch_decode_w(const AttnArgs& a, dim3 grid, hipStream_t s) {
   const dim3 block(W * 64);
   if (a.tier_splits > 0)
@@ -1812,7 +1909,7 @@ static bool four_waves(const AttnArgs& a) { return a.g <= 8 && a.pages_per_split
 // The 8-wave kernel's registers fall from 245 to 219 VGPRs.
 static int decode_kind(int kind, const AttnArgs& a) { return kind == kKindDefault && a.g <= 8 ? kKindDefaultHR : kind; }
 
-template <int KIND, bool QJL>
+template <int KIND, int QJL>
 static void launch_decode(const AttnArgs& a, dim3 grid, hipStream_t s) {
   if (four_waves(a))
     launch_decode_w<KIND, 4, QJL>(a, grid, s);
@@ -1820,9 +1917,20 @@ static void launch_decode(const AttnArgs& a, dim3 grid, hipStream_t s) {
     launch_decode_w<KIND, kDecodeWaves, QJL>(a, grid, s);
 }
 
+// The decode kernel of a decode kind (decode_kind) and QJL form.
+template <int QJL>
+static void launch_decode_kind(const AttnArgs& a, int kind, dim3 grid, hipStream_t s) {
+  switch (kind) {
+    case kKindDefaultHR: launch_decode<kKindDefaultHR, QJL>(a, grid, s); break;
+    case kKindDefault: launch_decode<kKindDefault, QJL>(a, grid, s); break;
+    case kKindFast: launch_decode<kKindFast, QJL>(a, grid, s); break;
+    default: launch_decode<kKindGeneric, QJL>(a, grid, s); break;
+  }
+}
+
 // Dense V (the reference's dense_v_debug storage) takes the same workgroup
 // size rule as the quantised V pages.
-template <bool QJL>
+template <int QJL>
 static void launch_decode_dense_v(const AttnArgs& a, int kind, dim3 grid, hipStream_t s) {
   const bool w4 = four_waves(a);
   switch (decode_kind(kind, a)) {
@@ -1950,19 +2058,20 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (v_dense) {
     const int kind = layout_kind(layout);
-    if (use_qjl)
-      launch_decode_dense_v<true>(a, kind, grid, s);
+    if (!use_qjl)
+      launch_decode_dense_v<kQjlOff>(a, kind, grid, s);
+    else if (a.qjl_bits == kQjlBits)
+      launch_decode_dense_v<kQjl64>(a, kind, grid, s);
     else
-      launch_decode_dense_v<false>(a, kind, grid, s);
+      launch_decode_dense_v<kQjlAny>(a, kind, grid, s);
     return launch_status("tp_decode_attention_dense_v");
   }
   if (use_qjl) {
-    switch (n_pages > 0 ? decode_kind(layout_kind(layout), a) : (int)kKindGeneric) {
-      case kKindDefaultHR: launch_decode<kKindDefaultHR, true>(a, grid, s); break;
-      case kKindDefault: launch_decode<kKindDefault, true>(a, grid, s); break;
-      case kKindFast: launch_decode<kKindFast, true>(a, grid, s); break;
-      default: launch_decode<kKindGeneric, true>(a, grid, s); break;
-    }
+    const int kind = n_pages > 0 ? decode_kind(layout_kind(layout), a) : (int)kKindGeneric;
+    if (a.qjl_bits == kQjlBits)
+      launch_decode_kind<kQjl64>(a, kind, grid, s);
+    else
+      launch_decode_kind<kQjlAny>(a, kind, grid, s);
     return launch_status("tp_decode_attention_qjl");
   }
 #ifdef TP_TIMELINE
@@ -1973,12 +2082,7 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
     return launch_measure_variant(a, grid, n_pages > 0 ? layout_kind(layout) : -1, s);
   }
 #endif
-  switch (n_pages > 0 ? decode_kind(layout_kind(layout), a) : (int)kKindGeneric) {
-    case kKindDefaultHR: launch_decode<kKindDefaultHR, false>(a, grid, s); break;
-    case kKindDefault: launch_decode<kKindDefault, false>(a, grid, s); break;
-    case kKindFast: launch_decode<kKindFast, false>(a, grid, s); break;
-    default: launch_decode<kKindGeneric, false>(a, grid, s); break;
-  }
+  launch_decode_kind<kQjlOff>(a, n_pages > 0 ? decode_kind(layout_kind(layout), a) : (int)kKindGeneric, grid, s);
   return launch_status("tp_decode_attention");
 }
 
@@ -2091,9 +2195,11 @@ extern "C" unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c,
   const int64_t sz_vs = BH * cap * kPageTokens * kVGroups * 2;
   const int64_t sz_dv = BH * c->v_capacity * kPageTokens * kHeadDim * 2;
   const int64_t sz_tail = c->tail_len > 0 ? ((BH - 1) * c->tail_stride + c->tail_len) * kHeadDim * 2 : 0;
-  const int64_t sz_sig = BH * c->qjl_capacity * kPageTokens * 8;
+  const int qjl_p = c->qjl_bits > 0 ? c->qjl_bits : kQjlBits;  // sketch bits
+  const int qjl_nb = qjl_p / 8;                                  // sketch bytes per token and query head
+  const int64_t sz_sig = BH * c->qjl_capacity * kPageTokens * qjl_nb;
   const int64_t sz_nrm = BH * c->qjl_capacity * kPageTokens * 2;
-  const int64_t sz_qs = c->batch * c->hq * 8;
+  const int64_t sz_qs = c->batch * c->hq * qjl_nb;
 
   // One lane's loads of page `page` (lane addresses of lane_e), as the kernels issue them.
   auto page_loads = [&](int lin, int wave, int lane, int64_t bkv, int page, int lane_e) {
@@ -2269,7 +2375,15 @@ extern "C" unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c,
               const int64_t qslot = bkv * c->qjl_capacity + pg;
               const int l4 = lane >> 4;
               for (int mt = 0; mt < 4; ++mt) {
-                if (hr) {
+                if (qjl_p != kQjlBits) {  // qjl_correct_any: the dwords covering each token's sketch
+                  for (int i = 0; i < 4; ++i) {
+                    const int t = score_token(mt, i, l4, hr);
+                    const int64_t o = qjl_any_row(qslot, t, qjl_nb);
+                    const int sh = (int)(o & 3);
+                    log.check("qjl signs", o - sh, 4 * qjl_any_dwords(sh, qjl_nb), sz_sig, L, wave, lane);
+                    log.check("qjl norms", (qslot * kPageTokens + t) * 2, 2, sz_nrm, L, wave, lane);
+                  }
+                } else if (hr) {
                   for (int j = 0; j < 2; ++j) {
                     log.check("qjl signs", qjl_sign_base(qslot, l4, true) + 128 * mt + 64 * j, 16, sz_sig, L, wave, lane);
                     log.check("qjl norms", qjl_norm_base(qslot, l4, true) + 32 * mt + 16 * j, 4, sz_nrm, L, wave, lane);
@@ -2280,8 +2394,18 @@ extern "C" unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c,
                 }
               }
             }
-            log.check("q signs", ((int64_t)b * c->hq + (int64_t)kv * g + h0 + std::min(l16, nh - 1)) * 8, 8, sz_qs, L,
-                      wave, lane);
+            if (qjl_p == kQjlBits) {
+              log.check("q signs", ((int64_t)b * c->hq + (int64_t)kv * g + h0 + std::min(l16, nh - 1)) * 8, 8, sz_qs,
+                        L, wave, lane);
+            } else {  // qjl_query_words: thread t < 16 * kQjlMaxWords reads bytes 4w .. of head t / kQjlMaxWords
+              const int tid = wave * 64 + lane;
+              const int h = tid / kQjlMaxWords, w = tid % kQjlMaxWords;
+              if (tid < 16 * kQjlMaxWords && h < nh)
+                for (int j = 0; j < 4; ++j)
+                  if (4 * w + j < qjl_nb)
+                    log.check("q signs", ((int64_t)b * c->hq + (int64_t)kv * g + h0 + h) * qjl_nb + 4 * w + j, 1,
+                              sz_qs, L, wave, lane);
+            }
           }
           if (split == S - 1 && c->tail_len > 0 && wave == std::max(p_end - p_begin, 0) % waves &&
               std::min<int64_t>(c->tail_len, seq - (int64_t)n_pages * kPageTokens) > 0)

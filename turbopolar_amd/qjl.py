@@ -98,24 +98,32 @@ class QJLPages:
     """Device descriptor (``tp_qjl``) of a payload's sketches and the queries'
     sketches, for the QJL kernels; S pages of 64 tokens per (b, kv head)."""
 
+    # Sketch widths the QJL kernels take: P = 64 (the default) on their
+    # 64-bit path, any other multiple of 8 up to 256 on the byte-aligned one.
+    MAX_PROJ_DIM = 256
+
     def __init__(self, payload: QJLPayload, q_proj_signs: torch.Tensor):
-        if payload.proj_dim != 64:
-            raise NotImplementedError("the HIP QJL kernels take qjl_proj_dim == 64")
+        P = int(payload.proj_dim)
+        if P < 8 or P > self.MAX_PROJ_DIM or P % 8:
+            raise NotImplementedError(f"the HIP QJL kernels take qjl_proj_dim a multiple of 8 up to "
+                                      f"{self.MAX_PROJ_DIM}, got {P}")
         signs, norms = payload.packed_signs, payload.norms
         for name, t in (("packed_signs", signs), ("norms", norms), ("q_proj_signs", q_proj_signs)):
             _lib.require_hip(t, name)
-        if signs.dim() != 5 or signs.shape[3] != 64 or signs.shape[4] != 8 or tuple(norms.shape) != tuple(signs.shape[:4]):
-            raise ValueError(f"QJL payload must be [B, H, S, 64, 8] signs and [B, H, S, 64] norms, got "
+        if (signs.dim() != 5 or signs.shape[3] != 64 or signs.shape[4] != P // 8
+                or tuple(norms.shape) != tuple(signs.shape[:4])):
+            raise ValueError(f"QJL payload must be [B, H, S, 64, {P // 8}] signs and [B, H, S, 64] norms, got "
                              f"{tuple(signs.shape)} and {tuple(norms.shape)}")
         if signs.dtype != torch.uint8 or norms.dtype != torch.float16 or q_proj_signs.dtype != torch.uint8:
             raise ValueError("QJL payload dtypes must be uint8 signs, fp16 norms and uint8 query signs")
         self.keep = (signs.contiguous(), norms.contiguous(), q_proj_signs.contiguous())
         self.B, self.H, self.S = int(signs.shape[0]), int(signs.shape[1]), int(signs.shape[2])
         self.q_shape = tuple(q_proj_signs.shape)
-        self.desc = _lib.TPQjl(self.keep[0].data_ptr(), self.keep[1].data_ptr(), self.keep[2].data_ptr(), 64, self.S)
+        self.proj_dim = P
+        self.desc = _lib.TPQjl(self.keep[0].data_ptr(), self.keep[1].data_ptr(), self.keep[2].data_ptr(), P, self.S)
 
     def check_against(self, B: int, H: int, S: int, Hq: int) -> None:
-        if (self.B, self.H) != (B, H) or self.S < S or self.q_shape != (B, Hq, 8):
+        if (self.B, self.H) != (B, H) or self.S < S or self.q_shape != (B, Hq, self.proj_dim // 8):
             raise ValueError(f"QJL payload [{self.B}, {self.H}, {self.S}] / query signs {self.q_shape} do not match "
                              f"pages [{B}, {H}, {S}] and {Hq} query heads")
 
