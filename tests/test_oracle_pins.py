@@ -338,3 +338,23 @@ def test_angle_code_rule_consistent_with_encoder():
     for bits in (2, 4, 8):
         enc = oracle.encode_block(k, l1_bits=8, deep_bits=bits, split_dim=0)
         assert np.array_equal(oracle.angle_codes_f16(a16, bits)[0, 0], _codes(enc, "deep", bits))
+
+
+def test_angle_quotient_product_is_exact_for_every_fp16_numerator():
+    """The encoder's fast angle code divides the shifted angle s1 = fp16(a16 +
+    fp16(pi)) by fp16(2*pi) as one fp32 product with fp32(1 / 6.28125), rounded
+    once, then to fp16; its guards skip the quotient on the strength of this
+    check.  Over every finite fp16 s1 the product rounds to the same fp16 as
+    the oracle's fp16 division (encoder.py:48) and as the correctly rounded
+    quotient of the exact rationals."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    s1 = bits.view(F16)
+    s1 = s1[np.isfinite(s1)]
+    inv = np.float32(0.159203976392745972)
+    assert Fraction(float(inv)) - Fraction(1) / Fraction(6.28125) < Fraction(1, 2 ** 26)
+    prod = (s1.astype(np.float32) * inv).astype(F16)
+    div = (s1 / F16(2 * np.pi)).astype(F16)
+    assert np.array_equal(prod.view(np.uint16), div.view(np.uint16))
+    two_pi16 = Fraction(6.28125)
+    exact = np.array([r16(Fraction(float(x)) / two_pi16) for x in s1], dtype=np.float64).astype(F16)
+    assert np.array_equal(prod, exact)  # by value: the rationals carry no -0
