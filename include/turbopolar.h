@@ -394,6 +394,15 @@ int32_t tp_selftest_div_f16_exhaustive(unsigned long long* mismatches, int32_t s
 int32_t tp_selftest_vcode_exhaustive(unsigned long long* mismatches, int32_t s_begin,
                                      int32_t s_count, void* stream);
 
+/* Counts, over positive finite fp16 scale patterns [s_begin, s_begin+s_count)
+ * and all finite fp16 log radii lr with |lr / scale| < 127.1, the int8
+ * log-radius codes where the fast encoder's path (reciprocal FMA with the
+ * +128 bias, byte conversion, exact redo near a half-integer) differs from
+ * int8(clip(rint(f32(lr / scale)), -128, 127)).  *mismatches is accumulated
+ * (atomic add), so zero it first.  Test-only, as the other self-tests. */
+int32_t tp_selftest_lcode_exhaustive(unsigned long long* mismatches, int32_t s_begin,
+                                     int32_t s_count, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

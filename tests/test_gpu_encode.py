@@ -133,6 +133,28 @@ def test_encode_nan_inputs(device, layout_name, dtype):
     check_against_oracle(k.astype(dtype), v.astype(dtype), LAYOUTS[layout_name], device)
 
 
+@pytest.mark.parametrize("layout_name", ["default", "fast"])
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_encode_inf_inputs(device, layout_name, dtype):
+    """Infinite K components in every sign combination, alone and in pairs
+    (atan2(+-inf, +-inf) is an odd multiple of pi/4, atan2(+-inf, finite) is
+    +-pi/2 and atan2(finite, -inf) is +-pi), and infinite V values: codes and
+    scales as the oracle's (the radius is inf, so in the log-int8 layout the
+    page's scale is inf and its radius codes 0)."""
+    print(f"[encode-inf] layout={layout_name} dtype={np.dtype(dtype).name}", flush=True)
+    k, v = gen_kv(33, 1, 2, 2 * PAGE, "normal", np.float32)
+    inf = np.inf
+    pairs = [(inf, inf), (-inf, inf), (inf, -inf), (-inf, -inf), (inf, 3.0), (-inf, 0.0), (inf, 0.0),
+             (-2.0, inf), (5.0, -inf), (0.0, inf), (0.0, -inf), (-inf, -7.5)]
+    for i, (x, y) in enumerate(pairs):
+        t, j = 3 + 5 * i, (7 * i) % 64       # page 0 of head 0, scattered tokens and pairs
+        k[0, 0, t, 2 * j], k[0, 0, t, 2 * j + 1] = x, y
+    k[0, 1, PAGE + 11, 40] = -inf         # page 1 of head 1: one component
+    v[0, 0, 9, 3] = inf                   # V groups with +inf and -inf
+    v[0, 1, PAGE + 2, 100] = -inf
+    check_against_oracle(k.astype(dtype), v.astype(dtype), LAYOUTS[layout_name], device)
+
+
 def test_encode_into_capacity_slot(device):
     """Pages land in slots [page_begin, page_begin + S) of a larger store."""
     k, v = gen_kv(8, 2, 2, 2 * PAGE, "normal", np.float16)
@@ -203,3 +225,19 @@ def test_v_code_fast_path_exhaustive(device):
         _lib.check(st, "selftest vcode")
     torch.cuda.synchronize()
     assert int(cnt.item()) == 0, f"{int(cnt.item())} (v, s) pairs where the fast V code differs"
+
+
+def test_log_radius_code_fast_path_exhaustive(device):
+    """The specialised fp16 encoder's int8 log-radius codes (reciprocal FMA
+    with the +128 bias, byte conversion that rounds half to even, exact redo
+    near a half-integer) == int8(clip(rint(f32(lr / s)), -128, 127)) for every
+    positive finite fp16 scale s and every finite fp16 lr the encoder can pair
+    with it (|lr / s| < 127.1: lr is at most the page's max |lr|, and s is
+    fp16(max |lr| / 127))."""
+    cnt = torch.zeros(1, dtype=torch.int64, device=device)
+    step = 4096
+    for s0 in range(0, 32768, step):
+        st = _lib.lib().tp_selftest_lcode_exhaustive(cnt.data_ptr(), s0, step, torch.cuda.current_stream().cuda_stream)
+        _lib.check(st, "selftest lcode")
+    torch.cuda.synchronize()
+    assert int(cnt.item()) == 0, f"{int(cnt.item())} (lr, s) pairs where the fast log-radius code differs"

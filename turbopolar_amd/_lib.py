@@ -153,6 +153,7 @@ _SIGNATURES = {
     "tp_selftest_atan2_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
     "tp_selftest_div_f16_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
     "tp_selftest_vcode_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
+    "tp_selftest_lcode_exhaustive": (c_i32, [c_vp, c_i32, c_i32, c_vp]),
 }
 
 _lib = None

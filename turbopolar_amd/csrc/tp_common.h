@@ -98,13 +98,18 @@ __device__ __forceinline__ float max_abs_nan(float m, float x) { return nan_max(
 // pi/2 - a and pi - a with two-part constants.  Within a few fp32 ulps of the
 // true angle; atan2_f16 below only trusts it away from fp16 rounding
 // boundaries, and the result is checked against float64 over all fp16 pairs.
+//
+// NaN: a NaN x or y gives a NaN angle (IEEE maximum / minimum, v_maximum3_f32
+// and v_minimum3_f32, propagate it), and so do two infinite components, whose
+// ratio is inf * rcp(inf) = NaN; one infinite component gives the ratio 0 and
+// the exact angle.
 __device__ __forceinline__ float atan2_poly(float y, float x) {
   const float ax = fabsf(x);
   const float ay = fabsf(y);
-  const float mx = fmaxf(ax, ay);
-  const float mn = fminf(ax, ay);
+  const float mx = __builtin_elementwise_maximum(ax, ay);
+  const float mn = __builtin_elementwise_minimum(ax, ay);
   // mx >= 2^-24 for any non-zero fp16 input; for x = y = 0 the clamp keeps t = 0.
-  const float t = mn * __builtin_amdgcn_rcpf(fmaxf(mx, 0x1p-30f));
+  const float t = mn * __builtin_amdgcn_rcpf(__builtin_elementwise_maximum(mx, 0x1p-30f));
   const float u = t * t;
   float p = -0.0017539079999551177f;
   p = __builtin_fmaf(p, u, 0.010726844891905785f);
@@ -130,12 +135,14 @@ __device__ __forceinline__ float atan2_poly(float y, float x) {
 // is cleared when the result is too close to an fp16 rounding boundary to be
 // trusted (the caller then uses atan2_f16_slow).
 __device__ __forceinline__ uint16_t atan2_f16_fast(float y, float x, bool* exact) {
-  // atan2_poly's min / max drop a NaN operand: a NaN x or y takes the float64
-  // path, whose atan2 is NaN.
-  *exact = !__builtin_isunordered(x, y);
-  if (*exact && y == 0.0f && !__builtin_signbit(x)) return f2h(y);  // exact +-0
+  // A NaN angle (a NaN x or y, or two infinite components) takes the float64
+  // path, whose atan2 is NaN, or an odd multiple of pi/4 for two infinities.
+  if (y == 0.0f && !__builtin_signbit(x) && !__builtin_isnan(x)) {  // exact +-0
+    *exact = true;
+    return f2h(y);
+  }
   const float a = atan2_poly(y, x);
-  *exact = *exact && !near_f16_midpoint<kGuardAtan2>(a);
+  *exact = !__builtin_isnan(a) && !near_f16_midpoint<kGuardAtan2>(a);
   return f2h(a);
 }
 __device__ __forceinline__ uint16_t atan2_f16_slow(float y, float x) { return d2h(atan2((double)y, (double)x)); }

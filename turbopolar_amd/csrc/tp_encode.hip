@@ -98,20 +98,21 @@ __device__ __forceinline__ void pack_rows(uint8_t* dst, int row_bytes, int bits,
   }
 }
 
-// The page's max |lr| over the workgroup's 256 threads (16 values each) as
-// the reference's reduction takes it: NaN propagates (a NaN log radius makes
-// the maximum NaN, and with it the page scale and every radius code).  An
-// integer maximum of the |lr| bit patterns orders finite values and inf as
-// fmaxf does and puts every NaN above inf.  s_max: 4 words of LDS.
-__device__ __forceinline__ float page_abs_max(const float (&lr)[16], uint32_t* s_max, int tid) {
+// The page's max |lr| over the workgroup's 256 threads (16 fp16 values
+// each) as the reference's reduction takes it: NaN propagates (a NaN log
+// radius makes the maximum NaN, and with it the page scale and every radius
+// code).  An integer maximum of the |lr| fp16 bit patterns orders finite
+// values and inf as fmaxf does and puts every NaN above inf.  s_max: 4 words
+// of LDS.
+__device__ __forceinline__ float page_abs_max(const uint16_t (&lr)[16], uint32_t* s_max, int tid) {
   uint32_t m = 0;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) m = max(m, __float_as_uint(lr[j]) & 0x7fffffffu);
+  for (int j = 0; j < 16; ++j) m = max(m, (uint32_t)(lr[j] & 0x7fffu));
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
   if ((tid & 63) == 0) s_max[tid >> 6] = m;
   __syncthreads();
-  return __uint_as_float(max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3])));
+  return h2f((uint16_t)max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3])));
 }
 
 template <bool kF32>
@@ -175,13 +176,13 @@ __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
       // encoder.py:34-42: lr = f32(f16 log(max(r, fp16(1e-6)))); per-page scale
       // f16(max|lr| / 127); codes rint(lr / scale).  Flagged logs are redone in
       // float64 by one loop body that selects its element into place.
-      float lr[16];
+      uint16_t lr[16];  // fp16 log radii
       uint32_t lfix = 0;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const uint16_t rb = r16[j] > kF16RadiusFloor ? r16[j] : kF16RadiusFloor;
         bool exact;
-        lr[j] = h2f(log_f16_fast(h2f(rb), &exact));
+        lr[j] = log_f16_fast(h2f(rb), &exact);
         lfix |= exact ? 0u : (1u << j);
       }
       while (lfix) {
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
 #pragma unroll
         for (int k2 = 0; k2 < 16; ++k2) rb = k2 == j ? r16[k2] : rb;
         rb = rb > kF16RadiusFloor ? rb : kF16RadiusFloor;
-        const float exact_lr = h2f(log_f16_slow(h2f(rb)));
+        const uint16_t exact_lr = log_f16_slow(h2f(rb));
 #pragma unroll
         for (int k2 = 0; k2 < 16; ++k2) lr[k2] = k2 == j ? exact_lr : lr[k2];
       }
@@ -202,7 +203,7 @@ __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
       uint32_t packed[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const uint32_t c = (uint32_t)(to_int8_rne(lr[j] / lsf) & 0xff);
+        const uint32_t c = (uint32_t)(to_int8_rne(h2f(lr[j]) / lsf) & 0xff);
         packed[j >> 2] |= c << (8 * (j & 3));
       }
       *reinterpret_cast<uint4*>(static_cast<int8_t*>(a.radii) + row * kPairs + 16 * qq) =
@@ -282,16 +283,23 @@ __device__ __forceinline__ float mul_f16_f32(float x, float s) { return __builti
 // fp16 (a16 + pi) as fp32, the numerator of the angle code (encoder.py:46-50).
 __device__ __forceinline__ float code_numerator(uint16_t a16) { return h2f(f2h(h2f(a16) + h2f(kF16Pi))); }
 
-// Code of an angle numerator from its fp16 quotient n16 (clamped, NaN -> 0).
+// Argument of the code's byte conversion from the fp16 quotient n16 of a
+// fast-path angle: n16 * (2^bits - 1), one mixed-precision FMA reading the
+// fp16 value.  No clamp: a non-NaN atan2 lies in [-pi, pi], whose fp16
+// rounding lies in [-fp16(pi), fp16(pi)] (pi is below the midpoint between
+// fp16(pi) and the next fp16 value), so the shifted angle lies in [0,
+// fp16(2 pi)] and its quotient in [0, 1]; the NaN cases are flagged and
+// redone on the exact path.
 template <int kBits>
 __device__ __forceinline__ float code_arg(float n16) {
-  return fminf(fmaxf(n16, 0.0f), 1.0f) * (float)((1 << kBits) - 1);
+  return __builtin_fmaf(n16, (float)((1 << kBits) - 1), 0.0f);
 }
 
 // The fast path's angle code of pair (x, y), as the argument of the byte
 // conversion, and whether it cannot be trusted: the fp32 atan2 lies near an
-// fp16 rounding midpoint, or x or y is NaN (atan2_poly's min / max drop a NaN
-// operand; the reference's NaN angle gives code 0).  An angle below 2^-14
+// fp16 rounding midpoint or is NaN (a NaN x or y, whose code is the NaN
+// angle's 0, or two infinite components, an odd multiple of pi/4; atan2_poly
+// propagates both as NaN).  An angle below 2^-14
 // leaves fp16(a + pi) = fp16(pi) whichever way it rounds, so the guard needs
 // no subnormal test, and atan2(+-0, x >= 0) = +-0 comes out of atan2_poly
 // exactly.  The quotient needs no guard: for every fp16 numerator s1 the fp32
@@ -303,18 +311,20 @@ template <int kBits>
 __device__ __forceinline__ float angle_arg_fast(float x, float y, bool* flag) {
   const float a = atan2_poly(y, x);
   const float q = mul_f16_f32(code_numerator(f2h(a)), kF32InvF16TwoPi);
-  *flag = near_f16_midpoint_code<kGuardAtan2>(a) | __builtin_isunordered(x, y);
+  *flag = near_f16_midpoint_code<kGuardAtan2>(a) | __builtin_isnan(a);
   return code_arg<kBits>(h2f(f2h(q)));
 }
 
 // Exact angle code of pair (x, y): correctly rounded fp16 atan2, except that
 // the float64 atan2 runs only when the two fp16 candidates around the fast
 // result's rounding midpoint give different codes.  A NaN x or y gives the
-// NaN angle's code, 0 (angle_code_f16).
+// NaN angle's code, 0 (angle_code_f16); two infinite components take the
+// float64 atan2.
 template <int kBits>
 __device__ __forceinline__ uint32_t exact_angle_code(float y, float x) {
   if (__builtin_isunordered(x, y)) return 0u;
   const float a = atan2_poly(y, x);
+  if (__builtin_isnan(a)) return angle_code_f16(atan2_f16_slow(y, x), kBits);
   const uint16_t a16 = f2h(a);
   const uint32_t c0 = angle_code_f16(a16, kBits);
   if (!near_f16_midpoint_code<kGuardAtan2>(a)) return c0;
@@ -330,15 +340,51 @@ __device__ __forceinline__ uint32_t exact_angle_code(float y, float x) {
 // Biased byte (code + 128) of value v with scale s = 1/rs by the fast path,
 // written into byte `sel` of `old`, and whether the fp32 quotient is too close
 // to an fp16 midpoint to trust.
-__device__ __forceinline__ uint32_t vcode_fast_byte(float v, float rs, uint32_t sel, uint32_t old, bool* near) {
+// one: 1.0f, which the caller hides from the compiler (an empty asm that
+// yields it in an SGPR) so that fp16(q) * 1 + 128 stays one mixed-precision FMA
+// reading the fp16 value instead of a conversion and an add; x * 1 is exact,
+// so it rounds as the fp32 sum does.
+__device__ __forceinline__ uint32_t vcode_fast_byte(float v, float rs, float one, uint32_t sel, uint32_t old,
+                                                    bool* near) {
   const float q = mul_f16_f32(v, rs);
   *near = near_f16_midpoint_code<kGuardDiv>(q);
-  return __builtin_amdgcn_cvt_pk_u8_f32(h2f(f2h(q)) + 128.0f, sel, old);
+  return __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(h2f(f2h(q)), one, 128.0f), sel, old);
+}
+// 1.0f in an SGPR, opaque to the compiler's constant folding.
+__device__ __forceinline__ float opaque_one() {
+  float one;
+  asm volatile("s_mov_b32 %0, 1.0" : "=s"(one));
+  return one;
 }
 // The same byte from the correctly rounded quotient, NaN -> code 0.
 __device__ __forceinline__ uint32_t vcode_exact_byte(float v, float s) {
   const float qn = h2f(f2h(v / s));
   return __builtin_amdgcn_cvt_pk_u8_f32((qn == qn ? qn : 0.0f) + 128.0f, 0u, 0u);
+}
+
+// Biased byte (code + 128) of the int8 log-radius code rint(lr / ls) of the
+// fp16 log radius lr16 by the fast path, rl = 1 / ls by v_rcp_f32, written
+// into byte `sel` of `old`, and whether it must be redone.  The fast path
+// forms lr * rl + 128 in one FMA: the reciprocal is within 1 ulp, so for
+// |lr / ls| < 127.1 (lr is at most the page's max |lr| and ls its fp16 / 127)
+// the product is within 2^-16 of the exact quotient and the rounded sum within
+// 1.5 * 2^-16 of quotient + 128; rint agrees with the reference's unless the
+// sum lies within 2^-13 of a half-integer.  The sum is positive, and the byte
+// conversion rounds half to even.
+__device__ __forceinline__ uint32_t lcode_fast_byte(uint16_t lr16, float rl, uint32_t sel, uint32_t old,
+                                                    bool* near) {
+  const float qb = __builtin_fmaf(h2f(lr16), rl, 128.0f);
+  // v_fract_f32 is qb - floor(qb) here (0 < qb < 256; it caps just below 1).
+  *near = fabsf(__builtin_amdgcn_fractf(qb) - 0.5f) <= 0x1p-13f;
+  return __builtin_amdgcn_cvt_pk_u8_f32(qb, sel, old);
+}
+// The same byte from the correctly rounded fp32 quotient lr / ls (NaN -> code
+// 0).  The quotient of two fp16 values is a half-integer exactly or lies at
+// least 2^-13 from one, so adding 128 (one rounding at 2^-16) keeps rint's
+// answer, and a tie stays a tie whose even neighbour is shifted by 128.
+__device__ __forceinline__ uint32_t lcode_exact_byte(uint16_t lr16, float ls) {
+  const float qd = h2f(lr16) / ls;
+  return __builtin_amdgcn_cvt_pk_u8_f32((qd == qd ? qd : 0.0f) + 128.0f, 0u, 0u);
 }
 
 template <int L>
@@ -403,13 +449,15 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
   if constexpr (kFastLayout) {
     // encoder.py:34-42: lr = f32(f16 log(max(r, fp16(1e-6)))); per-page scale
     // f16(max|lr| / 127); codes rint(lr / scale).
-    float lr[16];
+    // The log radii stay fp16 (the reference's f16 log, widened exactly
+    // wherever it is used).
+    uint16_t lr[16];
     uint32_t lfix = 0;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const uint16_t rb = r16[j] > kF16RadiusFloor ? r16[j] : kF16RadiusFloor;
       bool exact;
-      lr[j] = h2f(log_f16_fast(h2f(rb), &exact));
+      lr[j] = log_f16_fast(h2f(rb), &exact);
       lfix |= exact ? 0u : (1u << j);
     }
     while (lfix) {
@@ -419,7 +467,7 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
 #pragma unroll
       for (int k2 = 0; k2 < 16; ++k2) rb = k2 == j ? r16[k2] : rb;
       rb = rb > kF16RadiusFloor ? rb : kF16RadiusFloor;
-      const float exact_lr = h2f(log_f16_slow(h2f(rb)));
+      const uint16_t exact_lr = log_f16_slow(h2f(rb));
 #pragma unroll
       for (int k2 = 0; k2 < 16; ++k2) lr[k2] = k2 == j ? exact_lr : lr[k2];
     }
@@ -427,13 +475,11 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
     const float ls = mx == 0.0f ? 1e-6f : mx;
     const uint16_t ls16 = f2h(ls / 127.0f);
     const float lsf = h2f(ls16);
-    // code = int8(clip(rint(f32(lr / ls)))): a reciprocal product is within 2
-    // ulps of the correctly rounded quotient, and |quotient| <= 128, so rint
-    // agrees unless the product is within 2^-13 of a half-integer; those are
-    // redone with the division.  NaN quotients give code 0, and they come only
-    // from a scale that is 0 (every lr is 0: 0 / 0), inf (lr / inf is 0 or NaN)
-    // or NaN (a NaN lr): then every code of the page is 0, and otherwise every
-    // lr is finite.
+    // code = int8(clip(rint(f32(lr / ls)))) by lcode_fast_byte, the flagged
+    // ones redone by lcode_exact_byte.  NaN quotients give code 0, and they
+    // come only from a scale that is 0 (every lr is 0: 0 / 0), inf (lr / inf
+    // is 0 or NaN) or NaN (a NaN lr): then every code of the page is 0, and
+    // otherwise every lr is finite.
     const float rl = __builtin_amdgcn_rcpf(lsf);
     const bool zero_codes = !(lsf != 0.0f && fabsf(lsf) < INFINITY);  // uniform over the page
     uint32_t packed[4] = {0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
@@ -441,20 +487,18 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
     if (!zero_codes) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const float qd = lr[j] * rl;
-        // v_fract_f32 is qd - floor(qd) here (|qd| <= 128; it caps just below 1).
-        dfix |= fabsf(__builtin_amdgcn_fractf(qd) - 0.5f) <= 0x1p-13f ? (1u << j) : 0u;
-        packed[j >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(qd + 128.0f, (uint32_t)(j & 3), packed[j >> 2]);
+        bool near;
+        packed[j >> 2] = lcode_fast_byte(lr[j], rl, (uint32_t)(j & 3), packed[j >> 2], &near);
+        dfix |= near ? (1u << j) : 0u;
       }
     }
     while (dfix) {
       const int j = __builtin_ctz(dfix);
       dfix &= dfix - 1u;
-      float lj = 0.0f;
+      uint16_t lj = 0;
 #pragma unroll
       for (int k2 = 0; k2 < 16; ++k2) lj = k2 == j ? lr[k2] : lj;
-      const float qd = lj / lsf;
-      const uint32_t b = __builtin_amdgcn_cvt_pk_u8_f32((qd == qd ? qd : 0.0f) + 128.0f, 0u, 0u);
+      const uint32_t b = lcode_exact_byte(lj, lsf);
       const uint32_t sh = 8u * (uint32_t)(j & 3);
 #pragma unroll
       for (int k2 = 0; k2 < 4; ++k2) packed[k2] = k2 == (j >> 2) ? (packed[k2] & ~(0xffu << sh)) | (b << sh) : packed[k2];
@@ -495,6 +539,7 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
   if ((s16 & 0x7fffu) == 0) s16 = kF16VScaleFloor;
   const float s = h2f(s16);
   const float rs = __builtin_amdgcn_rcpf(s);
+  const float one = opaque_one();
   uint32_t vw[8];
   uint32_t vfix = nonfinite ? 0xffffffffu : 0u;  // values whose quotient the fast path cannot vouch for
 #pragma unroll
@@ -502,7 +547,7 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
 #pragma unroll
   for (int i = 0; i < 32; ++i) {
     bool near;
-    vw[i >> 2] = vcode_fast_byte(raw_val(vraw, i), rs, (uint32_t)(i & 3), vw[i >> 2], &near);
+    vw[i >> 2] = vcode_fast_byte(raw_val(vraw, i), rs, one, (uint32_t)(i & 3), vw[i >> 2], &near);
     vfix |= near ? (1u << i) : 0u;
   }
   const uint16_t* vin = static_cast<const uint16_t*>(a.v) + in_off;
@@ -648,10 +693,33 @@ __global__ __launch_bounds__(256) void vcode_exhaustive_kernel(unsigned long lon
     const float s = h2f((uint16_t)sb);
     const float v = h2f((uint16_t)vb);
     bool near;
-    uint32_t fast = vcode_fast_byte(v, __builtin_amdgcn_rcpf(s), 0u, 0u, &near);
+    uint32_t fast = vcode_fast_byte(v, __builtin_amdgcn_rcpf(s), opaque_one(), 0u, 0u, &near);
     if (near) fast = vcode_exact_byte(v, s);
     const int32_t ref = to_int8_rne(h2f(f2h(v / s)));
     bad = (int32_t)(int8_t)(uint8_t)(fast ^ 0x80u) != ref ? 1u : 0u;
+  }
+  const unsigned long long ballot = __ballot(bad);
+  if ((threadIdx.x & 63) == 0 && ballot) atomicAdd(mismatches, (unsigned long long)__popcll(ballot));
+}
+
+// Every finite fp16 log radius lr against one positive finite fp16 scale ls
+// per blockIdx.y, over the quotients the encoder forms (|lr / ls| < 127.1):
+// the fast log-radius code byte (with its exact fallback) against
+// int8(clip(rint(f32(lr / ls)), -128, 127)).
+__global__ __launch_bounds__(256) void lcode_exhaustive_kernel(unsigned long long* mismatches, int32_t s_begin) {
+  const uint32_t sb = (uint32_t)(s_begin + (int32_t)blockIdx.y) & 0x7fffu;
+  const uint32_t lb = blockIdx.x * 256u + threadIdx.x;
+  uint32_t bad = 0;
+  if (sb != 0 && (sb & 0x7c00u) != 0x7c00u && (lb & 0x7c00u) != 0x7c00u) {
+    const float ls = h2f((uint16_t)sb);
+    const float lr = h2f((uint16_t)lb);
+    if (fabsf(lr) < 127.1f * ls) {
+      bool near;
+      uint32_t fast = lcode_fast_byte((uint16_t)lb, __builtin_amdgcn_rcpf(ls), 0u, 0u, &near);
+      if (near) fast = lcode_exact_byte((uint16_t)lb, ls);
+      const int32_t ref = to_int8_rne(lr / ls);
+      bad = (int32_t)(int8_t)(uint8_t)(fast ^ 0x80u) != ref ? 1u : 0u;
+    }
   }
   const unsigned long long ballot = __ballot(bad);
   if ((threadIdx.x & 63) == 0 && ballot) atomicAdd(mismatches, (unsigned long long)__popcll(ballot));
@@ -826,6 +894,18 @@ int32_t tp_selftest_vcode_exhaustive(unsigned long long* mismatches, int32_t s_b
   hipLaunchKernelGGL(vcode_exhaustive_kernel, dim3(256, (unsigned)s_count), dim3(256), 0,
                      static_cast<hipStream_t>(stream), mismatches, s_begin);
   return launch_status("tp_selftest_vcode_exhaustive");
+}
+
+int32_t tp_selftest_lcode_exhaustive(unsigned long long* mismatches, int32_t s_begin, int32_t s_count,
+                                     void* stream) {
+  clear_error();
+  if (!mismatches || s_begin < 0 || s_count < 1 || s_begin + s_count > 32768 || s_count > 65535) {
+    set_error("bad self-test range");
+    return TP_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(lcode_exhaustive_kernel, dim3(256, (unsigned)s_count), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), mismatches, s_begin);
+  return launch_status("tp_selftest_lcode_exhaustive");
 }
 
 int32_t tp_selftest_div_f16_exhaustive(unsigned long long* mismatches, int32_t s_begin, int32_t s_count,
