@@ -26,6 +26,7 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kPageTokens = 64;
 constexpr int kHeadDim = 128;
@@ -70,9 +71,11 @@ __device__ __forceinline__ uint16_t d2h(double d) {
 // the fp16 normal range (|v| < 2^-14) every code candidate rounds to 0, so no
 // subnormal test is needed.  ((u - 0x1000 + kGuard) mod 2^13) <= 2 kGuard is
 // |low 13 bits - 0x1000| <= kGuard.
+// The low 13 bits are tested in the top of the word: (x << 19) < (2 kGuard +
+// 1) << 19 is (x mod 2^13) <= 2 kGuard, one shift-add and one compare.
 template <int kGuard>
 __device__ __forceinline__ bool near_f16_midpoint_code(float v) {
-  return ((__float_as_uint(v) + (uint32_t)(kGuard - 0x1000)) & 0x1fffu) <= (uint32_t)(2 * kGuard);
+  return ((__float_as_uint(v) + (uint32_t)(kGuard - 0x1000)) << 19) < ((uint32_t)(2 * kGuard + 1) << 19);
 }
 
 // True when the fp32 value `v` is too close to an fp16 rounding boundary (or in
@@ -145,7 +148,10 @@ __device__ __forceinline__ uint16_t atan2_f16_fast(float y, float x, bool* exact
   *exact = !__builtin_isnan(a) && !near_f16_midpoint<kGuardAtan2>(a);
   return f2h(a);
 }
-__device__ __forceinline__ uint16_t atan2_f16_slow(float y, float x) { return d2h(atan2((double)y, (double)x)); }
+// The float64 fallbacks are real calls: inlined, the compiler hoists their
+// float64 constants out of the callers' rare redo loops into the main path
+// (some 40 register moves and 40 VGPRs per encoder thread).
+__device__ inline __attribute__((noinline)) uint16_t atan2_f16_slow(float y, float x) { return d2h(atan2((double)y, (double)x)); }
 
 // Correctly rounded fp16 atan2(y, x) for fp16-representable x, y.
 __device__ __forceinline__ uint16_t atan2_f16(float y, float x) {
@@ -168,7 +174,7 @@ __device__ __forceinline__ uint16_t log_f16_fast(float r, bool* exact) {
   *exact = !near_f16_midpoint_code<kGuardLog>(l);
   return f2h(l);
 }
-__device__ __forceinline__ uint16_t log_f16_slow(float r) { return d2h(log((double)r)); }
+__device__ inline __attribute__((noinline)) uint16_t log_f16_slow(float r) { return d2h(log((double)r)); }
 __device__ __forceinline__ uint16_t log_f16(float r) {
   bool exact;
   const uint16_t l = log_f16_fast(r, &exact);

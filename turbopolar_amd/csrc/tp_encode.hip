@@ -387,6 +387,13 @@ __device__ __forceinline__ uint32_t lcode_exact_byte(uint16_t lr16, float ls) {
   return __builtin_amdgcn_cvt_pk_u8_f32((qd == qd ? qd : 0.0f) + 128.0f, 0u, 0u);
 }
 
+// Per-lane masks of the items the fast path cannot vouch for are built most
+// significant first: push_flag shifts the mask up and ORs the new item's flag
+// in (a 0/1 select and a shift-or, where a bit of its own per item would need
+// a 32-bit constant in a register for every item past the sixth), so item j
+// of n sits in bit n - 1 - j.
+__device__ __forceinline__ uint32_t push_flag(uint32_t m, bool f) { return (m << 1) | (f ? 1u : 0u); }
+
 template <int L>
 __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
   constexpr bool kFastLayout = L == kEncFast;
@@ -419,7 +426,7 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
     r16[j] = __builtin_bit_cast(uint16_t, __builtin_sqrtf16((f16)(sq[0] + sq[1])));  // correctly rounded
     bool flag;
     const float arg = angle_arg_fast<kBits>((float)xy[0], (float)xy[1], &flag);
-    fixa |= flag ? (1u << j) : 0u;
+    fixa = push_flag(fixa, flag);
     if constexpr (kFastLayout) {
       cw[j >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(arg, (uint32_t)(j & 3), cw[j >> 2]);
     } else {
@@ -429,7 +436,7 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
   // Exact redo of the flagged codes (padding tokens are never flagged).
   const uint32_t* kin = reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.k) + in_off);
   while (fixa) {  // flagged pairs are never padding: reload the pair
-    const int j = __builtin_ctz(fixa);
+    const int j = 15 - __builtin_ctz(fixa);
     fixa &= fixa - 1u;
     const uint32_t w = kin[j];
     const uint32_t c = exact_angle_code<kBits>(h2f((uint16_t)(w >> 16)), h2f((uint16_t)(w & 0xffffu)));
@@ -458,10 +465,10 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
       const uint16_t rb = r16[j] > kF16RadiusFloor ? r16[j] : kF16RadiusFloor;
       bool exact;
       lr[j] = log_f16_fast(h2f(rb), &exact);
-      lfix |= exact ? 0u : (1u << j);
+      lfix = push_flag(lfix, !exact);
     }
     while (lfix) {
-      const int j = __builtin_ctz(lfix);
+      const int j = 15 - __builtin_ctz(lfix);
       lfix &= lfix - 1u;
       uint16_t rb = 0;
 #pragma unroll
@@ -489,11 +496,11 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
       for (int j = 0; j < 16; ++j) {
         bool near;
         packed[j >> 2] = lcode_fast_byte(lr[j], rl, (uint32_t)(j & 3), packed[j >> 2], &near);
-        dfix |= near ? (1u << j) : 0u;
+        dfix = push_flag(dfix, near);
       }
     }
     while (dfix) {
-      const int j = __builtin_ctz(dfix);
+      const int j = 15 - __builtin_ctz(dfix);
       dfix &= dfix - 1u;
       uint16_t lj = 0;
 #pragma unroll
@@ -527,12 +534,12 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
   // NaN (nan_max, tp_common.h), so the scale is NaN and every code 0.
   RawRow32<false> vraw;
   load_row32<false>(a.v, in_off, valid, vraw);
-  uint32_t mbits = 0;
+  // Both halves of each word at once (v_pk_max_u16), then the two halves.
+  u16x2 m2 = {0, 0};
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const uint32_t w = raw_word(vraw, i) & 0x7fff7fffu;
-    mbits = max(mbits, max(w & 0xffffu, w >> 16));
-  }
+  for (int i = 0; i < 16; ++i)
+    m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, raw_word(vraw, i) & 0x7fff7fffu));
+  const uint32_t mbits = max((uint32_t)m2[0], (uint32_t)m2[1]);
   // inf or NaN in the group: exact path (v / inf and NaN quotients give code 0).
   const bool nonfinite = mbits >= 0x7c00u;
   uint16_t s16 = f2h(h2f((uint16_t)mbits) / 127.0f);
@@ -541,18 +548,19 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
   const float rs = __builtin_amdgcn_rcpf(s);
   const float one = opaque_one();
   uint32_t vw[8];
-  uint32_t vfix = nonfinite ? 0xffffffffu : 0u;  // values whose quotient the fast path cannot vouch for
+  uint32_t vfix = 0;  // values whose quotient the fast path cannot vouch for (value i in bit 31 - i)
 #pragma unroll
   for (int i = 0; i < 8; ++i) vw[i] = 0u;
 #pragma unroll
   for (int i = 0; i < 32; ++i) {
     bool near;
     vw[i >> 2] = vcode_fast_byte(raw_val(vraw, i), rs, one, (uint32_t)(i & 3), vw[i >> 2], &near);
-    vfix |= near ? (1u << i) : 0u;
+    vfix = push_flag(vfix, near);
   }
+  if (nonfinite) vfix = 0xffffffffu;  // inf or NaN in the group: every value on the exact path
   const uint16_t* vin = static_cast<const uint16_t*>(a.v) + in_off;
   while (vfix) {  // exact quotients of the flagged values, reloaded (never padding)
-    const int i = __builtin_ctz(vfix);
+    const int i = 31 - __builtin_ctz(vfix);
     vfix &= vfix - 1u;
     const uint32_t b = vcode_exact_byte(h2f(vin[i]), s);
     const uint32_t sh = 8u * (uint32_t)(i & 3);
