@@ -94,19 +94,22 @@ __device__ __forceinline__ bool near_f16_midpoint(float v) {
 __device__ __forceinline__ float nan_max(float m, float x) { return (x > m || x != x) ? x : m; }
 __device__ __forceinline__ float max_abs_nan(float m, float x) { return nan_max(m, fabsf(x)); }
 
-// fp32 atan2 for finite x, y: octant reduction to t = min(|x|,|y|)/max in
-// [0, 1], atan(t) = t * P(t^2) with a degree-9 polynomial in t^2 fitted here
-// for least maximum relative error on [0, 1] (Lawson-weighted least squares
-// over Chebyshev nodes; 1.4 fp32 ulps in fp32 Horner), then the quadrant:
-// pi/2 - a and pi - a with two-part constants.  Within a few fp32 ulps of the
+// fp32 |atan2(y, x)| for fp16-representable x, y: octant reduction to t =
+// min(|x|,|y|)/max in [0, 1], atan(t) = t * P(t^2) with a degree-9
+// polynomial in t^2 fitted here for least maximum relative error on [0, 1]
+// (Lawson-weighted least squares over Chebyshev nodes), evaluated as t + (t
+// t^2) * P1(t^2) with P = 1 + t^2 P1 (the leading term exact), then the
+// quadrant: pi/2 - a and pi - a with single fp32 constants (each 0.37 to 0.73
+// ulp of the result from the true constant).  Within a few fp32 ulps of the
 // true angle; atan2_f16 below only trusts it away from fp16 rounding
-// boundaries, and the result is checked against float64 over all fp16 pairs.
+// boundaries, and the result and the encoder's codes built on it are checked
+// against float64 over all fp16 pairs.
 //
 // NaN: a NaN x or y gives a NaN angle (IEEE maximum / minimum, v_maximum3_f32
 // and v_minimum3_f32, propagate it), and so do two infinite components, whose
 // ratio is inf * rcp(inf) = NaN; one infinite component gives the ratio 0 and
 // the exact angle.
-__device__ __forceinline__ float atan2_poly(float y, float x) {
+__device__ __forceinline__ float atan2_poly_mag(float y, float x) {
   const float ax = fabsf(x);
   const float ay = fabsf(y);
   const float mx = __builtin_elementwise_maximum(ax, ay);
@@ -123,16 +126,14 @@ __device__ __forceinline__ float atan2_poly(float y, float x) {
   p = __builtin_fmaf(p, u, -0.142619326710701f);
   p = __builtin_fmaf(p, u, 0.1999826580286026f);
   p = __builtin_fmaf(p, u, -0.3333328366279602f);
-  p = __builtin_fmaf(p, u, 1.0f);
-  float r = t * p;
-  constexpr float kHalfPiHi = 1.57079637050628662f;   // fp32(pi/2)
-  constexpr float kHalfPiLo = -4.371138828673793e-8f;  // pi/2 - fp32(pi/2)
-  constexpr float kPiHi = 3.14159274101257324f;       // fp32(pi)
-  constexpr float kPiLo = -8.742277657347586e-8f;    // pi - fp32(pi)
-  if (ay > ax) r = (kHalfPiHi - r) + kHalfPiLo;
-  if (__builtin_signbit(x)) r = (kPiHi - r) + kPiLo;
-  return __builtin_copysignf(r, y);
+  float r = __builtin_fmaf(t * u, p, t);
+  constexpr float kHalfPi = 1.57079637050628662f;  // fp32(pi/2)
+  constexpr float kPi = 3.14159274101257324f;      // fp32(pi)
+  if (ay > ax) r = kHalfPi - r;
+  if (__builtin_signbit(x)) r = kPi - r;
+  return r;
 }
+__device__ __forceinline__ float atan2_poly(float y, float x) { return __builtin_copysignf(atan2_poly_mag(y, x), y); }
 
 // fp16 atan2(y, x) for fp16-representable x, y from the fp32 atan2_poly; *exact
 // is cleared when the result is too close to an fp16 rounding boundary to be

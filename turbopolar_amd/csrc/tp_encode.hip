@@ -307,9 +307,11 @@ __device__ __forceinline__ float code_arg(float n16) {
 // the fp16 division s1 / fp16(2 pi) (checked over all 65536 fp16 values by
 // tests/test_oracle_pins.py and, through this function, by
 // atan2_exhaustive_kernel).
+// xy: the pair's raw fp16 word (y in the high half), whose top bit is the
+// sign of y that the angle takes (one bit-field insert).
 template <int kBits>
-__device__ __forceinline__ float angle_arg_fast(float x, float y, bool* flag) {
-  const float a = atan2_poly(y, x);
+__device__ __forceinline__ float angle_arg_fast(float x, float y, uint32_t xy, bool* flag) {
+  const float a = __uint_as_float((__float_as_uint(atan2_poly_mag(y, x)) & 0x7fffffffu) | (xy & 0x80000000u));
   const float q = mul_f16_f32(code_numerator(f2h(a)), kF32InvF16TwoPi);
   *flag = near_f16_midpoint_code<kGuardAtan2>(a) | __builtin_isnan(a);
   return code_arg<kBits>(h2f(f2h(q)));
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(256) void encode_f16_kernel(EncodeArgs a) {
     const half2v sq = xy * xy;  // fp16 products, as the reference squares in fp16 (no FMA)
     r16[j] = __builtin_bit_cast(uint16_t, __builtin_sqrtf16((f16)(sq[0] + sq[1])));  // correctly rounded
     bool flag;
-    const float arg = angle_arg_fast<kBits>((float)xy[0], (float)xy[1], &flag);
+    const float arg = angle_arg_fast<kBits>((float)xy[0], (float)xy[1], w, &flag);
     fixa = push_flag(fixa, flag);
     if constexpr (kFastLayout) {
       cw[j >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(arg, (uint32_t)(j & 3), cw[j >> 2]);
@@ -665,8 +667,8 @@ __global__ __launch_bounds__(256) void atan2_exhaustive_kernel(unsigned long lon
     // result, else exact_angle_code (which skips the float64 atan2 when both
     // fp16 candidates give one code).
     bool f4, f8;
-    const float g4 = angle_arg_fast<4>(x, y, &f4);
-    const float g8 = angle_arg_fast<8>(x, y, &f8);
+    const float g4 = angle_arg_fast<4>(x, y, (yb << 16) | xb, &f4);
+    const float g8 = angle_arg_fast<8>(x, y, (yb << 16) | xb, &f8);
     const uint32_t c4 = f4 ? exact_angle_code<4>(y, x) : __builtin_amdgcn_cvt_pk_u8_f32(g4, 0u, 0u);
     const uint32_t c8 = f8 ? exact_angle_code<8>(y, x) : __builtin_amdgcn_cvt_pk_u8_f32(g8, 0u, 0u);
     bad |= c4 != angle_code_f16(ref, 4) ? 1u : 0u;
