@@ -116,11 +116,14 @@ def test_decode_attention_argument_validation():
     assert st == _lib.TP_ERR_INVALID and "nothing to attend" in msg
     st, msg = call(pps=1)  # 4 splits need a workspace
     assert st == _lib.TP_ERR_WORKSPACE and "workspace" in msg
-    # The grid (splits x units workgroups) must stay below 2^31: 2^30 one-page
-    # splits of 8 kv heads do not fit.
+    # The grid is (hkv, batch x head blocks, splits), at most 65535 splits:
+    # 2^30 one-page splits of 8 kv heads do not fit, nor do 65536.
     big = _fake_pages(capacity=1 << 30)
     st = L.tp_decode_attention(4096, 1, 8, 8, ctypes.byref(lay), ctypes.byref(big), 1 << 30, None, None, 0, 0,
                                (1 << 30) * 64, 0.088, 1, None, 0, 8192, None)
+    assert st == _lib.TP_ERR_INVALID and b"grid limit" in L.tp_last_error()
+    st = L.tp_decode_attention(4096, 1, 8, 8, ctypes.byref(lay), ctypes.byref(big), 65536, None, None, 0, 0,
+                               65536 * 64, 0.088, 1, None, 0, 8192, None)
     assert st == _lib.TP_ERR_INVALID and b"grid limit" in L.tp_last_error()
     st = L.tp_decode_attention(4096, 1, 8, 2, ctypes.byref(lay), ctypes.byref(big), 1537, None, None, 0, 0,
                                1537 * 64, 0.088, 1, None, 0, 8192, None)

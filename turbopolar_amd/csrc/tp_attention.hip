@@ -51,8 +51,9 @@ constexpr int kTimelineStamps = 80;
 __device__ unsigned long long g_timeline[kTimelineGroups][kTimelineStamps];
 #define TP_STAMP(k)                                                                            \
   do {                                                                                          \
-    if (threadIdx.x == 0 && blockIdx.x < kTimelineGroups)                                       \
-      g_timeline[blockIdx.x][(k)] = __builtin_amdgcn_s_memrealtime();                           \
+    const unsigned lin_ = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;       \
+    if (threadIdx.x == 0 && lin_ < kTimelineGroups)                                             \
+      g_timeline[lin_][(k)] = __builtin_amdgcn_s_memrealtime();                                 \
   } while (0)
 #else
 #define TP_STAMP(k) \
@@ -126,10 +127,8 @@ struct AttnArgs {
   float scale_log2;
   int32_t pages_per_split;
   int32_t n_splits;
-  int32_t units_total;     // batch x hkv x head_blocks (the grid is n_splits x units_total)
-  FastDiv div_units;       // division by units_total, head_blocks, hkv
-  FastDiv div_head_blocks;
-  FastDiv div_hkv;
+  int32_t live_end;        // min(n_pages, pages holding a token below seq_len)
+  FastDiv div_head_blocks; // division by head_blocks
   int32_t counter_stride;  // u32 words between two ticket counters
   int32_t counter_slots;   // ticket counters per unit: 1, or 1 + tier_groups
   uint32_t* counters;
@@ -1155,6 +1154,26 @@ __device__ __forceinline__ void fold_records(const float* pml, const uint16_t* p
   }
 }
 
+// A decode workgroup's place in the 3-D grid (hkv, batch * head_blocks,
+// n_splits).  x runs fastest, so consecutive workgroup ids go to different kv
+// heads and, with round-robin dispatch over the 8 XCDs, every split of one kv
+// head of a batch-1 step runs on the same XCD; the split and the kv head come
+// straight from the block index (no division before the first page request).
+struct DecodeSlot {
+  int split, b, kv, hb;
+  int64_t bkv;
+};
+
+__device__ __forceinline__ DecodeSlot decode_slot(const AttnArgs& a) {
+  DecodeSlot d;
+  d.kv = (int)blockIdx.x;
+  d.split = (int)blockIdx.z;
+  d.b = (int)fast_div(blockIdx.y, a.div_head_blocks);
+  d.hb = (int)blockIdx.y - d.b * a.head_blocks;
+  d.bkv = (int64_t)d.b * a.hkv + d.kv;
+  return d;
+}
+
 template <int WAVES>
 struct AttnShared {
   Lut lut;
@@ -1409,9 +1428,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   // for the grid fields, a second round trip to fresh argument memory before
   // the first page request.
   asm volatile("" ::"s"(a.q), "s"(a.radii), "s"(a.angle_l1), "s"(a.angle_deep), "s"(a.v_codes), "s"(a.v_scales),
-               "s"(a.capacity), "s"(a.n_pages), "s"(a.pages_per_split), "s"(a.seq_len), "s"(a.units_total),
-               "s"(a.head_blocks), "s"(a.hkv), "s"(a.g), "s"(a.hq), "s"(a.div_units.m), "s"(a.div_units.sh),
-               "s"(a.div_head_blocks.m), "s"(a.div_head_blocks.sh), "s"(a.div_hkv.m), "s"(a.div_hkv.sh));
+               "s"(a.capacity), "s"(a.pages_per_split), "s"(a.live_end), "s"(a.head_blocks), "s"(a.hkv), "s"(a.g),
+               "s"(a.hq), "s"(a.div_head_blocks.m), "s"(a.div_head_blocks.sh));
   TP_STAMP(59);
 
   const int tid = threadIdx.x;
@@ -1419,26 +1437,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_attention_kernel(AttnArgs a
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int l16 = lane & 15;
   const int l4 = lane >> 4;
-  // 1-D grid, unit-minor: consecutive workgroup ids go to different kv heads,
-  // so with round-robin dispatch over the 8 XCDs every split of one kv head
-  // runs on the same XCD and its partials stay within one L2.  32-bit index
-  // arithmetic (units_total * n_splits < 2^31).
-  const int units_total = a.units_total;
-  const int lin = blockIdx.x;
-  const int split = (int)fast_div((uint32_t)lin, a.div_units);
-  const int unit_id = lin - split * units_total;
-  const int bkv32 = (int)fast_div((uint32_t)unit_id, a.div_head_blocks);
-  const int hb = unit_id - bkv32 * a.head_blocks;
-  const int b = (int)fast_div((uint32_t)bkv32, a.div_hkv);
-  const int kv = bkv32 - b * a.hkv;
-  const int64_t bkv = bkv32;
+  const DecodeSlot ds = decode_slot(a);
+  const int split = ds.split, b = ds.b, kv = ds.kv, hb = ds.hb;
+  const int64_t bkv = ds.bkv;
   const int h0 = hb * 16;
   const int nh = min(16, a.g - h0);
 
   // Compressed pages of this split that hold at least one unmasked token.
   const int p_begin = split * a.pages_per_split;
-  const int64_t live_pages = (a.seq_len + kPageTokens - 1) / kPageTokens;
-  const int p_end = (int)min((int64_t)min(p_begin + a.pages_per_split, a.n_pages), live_pages);
+  const int p_end = min(p_begin + a.pages_per_split, a.live_end);
 
   // Q and the first page's loads go out before the table build and the
   // barrier, and nothing before the barrier uses them.
@@ -2012,9 +2019,11 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
   if (actual_seq_len > total) actual_seq_len = total;
   if (pages_per_split <= 0) pages_per_split = tp_default_pages_per_split(batch, hq, hkv, n_pages);
   const int32_t n_splits = n_splits_of(n_pages, pages_per_split);
-  const int64_t n_groups = (int64_t)n_splits * batch * hkv * a.head_blocks;
-  if (n_groups > INT32_MAX) {
-    set_error("%lld workgroups exceed the grid limit; raise pages_per_split", (long long)n_groups);
+  // The grid is (hkv, batch * head_blocks, n_splits); y and z are at most 65535.
+  const int64_t n_rows = (int64_t)batch * a.head_blocks;
+  if (n_splits > 65535 || n_rows > 65535) {
+    set_error("grid (%d, %lld, %d) exceeds the grid limit of 65535 in y and z%s", hkv, (long long)n_rows,
+              n_splits, n_splits > 65535 ? "; raise pages_per_split" : "");
     return TP_ERR_INVALID;
   }
   a.out = static_cast<uint16_t*>(out);
@@ -2027,10 +2036,8 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
   a.scale_log2 = scale * 1.4426950408889634f;
   a.pages_per_split = pages_per_split;
   a.n_splits = n_splits;
-  a.units_total = (int32_t)(batch * hkv * a.head_blocks);
-  a.div_units = make_fastdiv((uint32_t)a.units_total);
+  a.live_end = (int32_t)std::min<int64_t>(n_pages, (actual_seq_len + kPageTokens - 1) / kPageTokens);
   a.div_head_blocks = make_fastdiv((uint32_t)a.head_blocks);
-  a.div_hkv = make_fastdiv((uint32_t)hkv);
   if (n_splits > 1) {
     const size_t need = tp_decode_workspace_bytes(batch, hq, hkv, n_pages, tail_len, pages_per_split);
     if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u)) {
@@ -2054,7 +2061,7 @@ static int32_t decode_attention_impl(const void* q, int64_t batch, int32_t hq, i
     ws += align256(units * 16 * (((size_t)tiers.groups + 1) & ~(size_t)1) * 2 * sizeof(float));
     a.tier_acc = reinterpret_cast<uint16_t*>(ws);
   }
-  const dim3 grid((unsigned)n_groups);
+  const dim3 grid((unsigned)hkv, (unsigned)n_rows, (unsigned)n_splits);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (v_dense) {
     const int kind = layout_kind(layout);
