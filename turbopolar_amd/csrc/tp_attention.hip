@@ -9,10 +9,10 @@
 // fp16 -- goes to the workspace and the last workgroup of the kv head to
 // arrive (atomic ticket) combines all partials -- one launch per step.  Above 64 splits per kv head the combine
 // has two tiers: groups of 16 splits combine first, and the last group's
-// combiner folds the group results.  The 1-D grid is unit-minor, so with the
-// hardware's round-robin dispatch over the 8 XCDs every split of one kv head
-// runs on the same XCD (a locality choice only: correctness does not depend
-// on placement).
+// combiner folds the group results.  The grid is (hkv, batch x head blocks,
+// splits), kv head fastest, so with the hardware's round-robin dispatch over
+// the 8 XCDs every split of one kv head of a batch-1 step runs on the same XCD
+// (a locality choice only: correctness does not depend on placement).
 //
 // Per page (64 tokens) a wave runs two MFMA chains (v_mfma_f32_16x16x32_f16):
 //   QK: S[t][h] = sum_d Khat[t][d] Q[h][d]; A = Khat decoded in registers from
