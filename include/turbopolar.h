@@ -144,9 +144,9 @@ int32_t tp_fused_qk(const void* q, int64_t batch, int32_t hq, int32_t hkv,
  * Tokens with global index >= actual_seq_len are masked (actual_seq_len >= 1;
  *   a value past the stored tokens attends every stored token, as the
  *   reference's mask does).
- * pages_per_split: pages per workgroup (0 = library default); the grid,
- *   ceil(n_pages / pages_per_split) x batch x hkv x ceil(hq / hkv / 16)
- *   workgroups, must stay below 2^31.
+ * pages_per_split: pages per workgroup (0 = library default); the grid is
+ *   (hkv, batch x ceil(hq / hkv / 16), ceil(n_pages / pages_per_split))
+ *   workgroups, and its second and third sizes must not exceed 65535.
  * workspace: device memory of at least tp_decode_workspace_bytes(...) bytes.
  *   Its counter area (the first tp_decode_counter_bytes(batch, hq, hkv) bytes)
  *   must be zero before the first call; every call leaves it zero again.  One
