@@ -1290,6 +1290,86 @@ __device__ __forceinline__ void combine_records(Merge& sh, const CombineItem& ci
   }
 }
 
+// One-tier combine by whole head rows, for up to kHeadCombineMax records:
+// wave w combines heads w, w + WAVES, ... and lane l owns dims 2l and 2l + 1.
+// The records come in batches of B (16 when there are at most 16, else 32),
+// all B + 1 loads of a batch in flight together: lane j (mod B) reads record
+// j's (m, l), and every lane reads the 4 bytes of its two dims of each
+// record's fp16 output (a head's 256-byte row per record).  The batch maximum
+// and the sum of the weights w_j = l_j 2^(m_j - M) are B-lane reductions; the
+// weights reach every lane through the wave's own 32 words of LDS (written,
+// then read back as broadcast 16-byte reads by the same wave), and each lane
+// folds its 2 x B products with mixed-precision FMAs from the fp16 outputs.
+// No split groups and no merge between waves (the split-group combine of
+// combine_records spent 0.42 µs of the 32k step's end phase in its LDS merge
+// alone).  Records past `count` are read as the last one and enter with weight
+// 0 and output 0; records with m = -inf weigh 0 (a NaN they carry survives, as
+// in fold_records).
+constexpr int kHeadCombineMax = 64;
+
+template <int B>
+__device__ __forceinline__ void fold_head_records(const float* pml, const uint16_t* pac, int count, int lane, float* wb,
+                                                  float& Mc, float& Lc, float& A0, float& A1) {
+  const int64_t rstride = (int64_t)16 * kHeadDim;  // halves from one record of a head to the next
+  Mc = -INFINITY;
+  Lc = 0.0f;
+  A0 = 0.0f;
+  A1 = 0.0f;
+  for (int r0 = 0; r0 < count; r0 += B) {
+    const int rj = r0 + (lane & (B - 1));
+    const float2 ml = *reinterpret_cast<const float2*>(pml + 2 * min(rj, count - 1));
+    uint32_t o[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j) o[j] = *reinterpret_cast<const uint32_t*>(pac + min(r0 + j, count - 1) * rstride);
+    if (r0 == 0) TP_STAMP(61);
+    const float m = rj < count ? ml.x : -INFINITY;
+    float Mb = m;
+#pragma unroll
+    for (int off = 1; off < B; off <<= 1) Mb = fmaxf(Mb, __shfl_xor(Mb, off, 64));
+    const float Mn = fmaxf(Mc, Mb);
+    const float w = m == -INFINITY ? 0.0f : ml.y * __builtin_amdgcn_exp2f(m - Mn);
+    float Ls = w;
+#pragma unroll
+    for (int off = 1; off < B; off <<= 1) Ls += __shfl_xor(Ls, off, 64);
+    const float s0 = Mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mc - Mn);
+    Lc = Lc * s0 + Ls;
+    A0 *= s0;
+    A1 *= s0;
+    if (lane < B) wb[lane] = w;
+    if (r0 == 0) TP_STAMP(62);
+#pragma unroll
+    for (int k = 0; k < B / 4; ++k) {
+      const float4v wk = *reinterpret_cast<const float4v*>(wb + 4 * k);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t x = r0 + 4 * k + i < count ? o[4 * k + i] : 0u;
+        const half2v oj = __builtin_bit_cast(half2v, x);
+        A0 = __builtin_fmaf((float)oj[0], wk[i], A0);
+        A1 = __builtin_fmaf((float)oj[1], wk[i], A1);
+      }
+    }
+    Mc = Mn;
+  }
+}
+
+template <int WAVES, class Merge>
+__device__ __forceinline__ void combine_heads(Merge& sh, const AttnArgs& a, int wave, int lane, int64_t unit, int nh,
+                                              int S, int Sp, int count, uint16_t* out_rows) {
+  float* wb = reinterpret_cast<float*>(&sh.acc[0][0]) + wave * 32;  // this wave's 32 weights
+  for (int hh = wave; hh < nh; hh += WAVES) {
+    const float* pml = a.part_ml + record_ml(unit, hh, Sp, 0);
+    const uint16_t* pac = a.part_acc + record_acc(unit, S, 0, hh) + 2 * lane;
+    float Mc, Lc, A0, A1;
+    if (count <= 16)
+      fold_head_records<16>(pml, pac, count, lane, wb, Mc, Lc, A0, A1);
+    else
+      fold_head_records<32>(pml, pac, count, lane, wb, Mc, Lc, A0, A1);
+    TP_STAMP(57);
+    const float inv = __builtin_amdgcn_rcpf(Lc);
+    *reinterpret_cast<uint32_t*>(out_rows + hh * kHeadDim + 2 * lane) = pack_f2h2(A0 * inv, A1 * inv);
+  }
+}
+
 template <int WAVES, int FL, class Merge>
 __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int tid, int b, int kv, int h0, int nh,
                                               int64_t bkv, int hb, int split);
@@ -1371,6 +1451,15 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
 
   // Last workgroup of this (b, kv, head block), or of its split group:
   // combine the records.
+  if constexpr (!kTiers) {
+    if (count <= kHeadCombineMax) {
+      combine_heads<WAVES>(sh, a, __builtin_amdgcn_readfirstlane(tid >> 6), tid & 63, unit, nh, S, Sp, count,
+                           a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0) * kHeadDim);
+      if (tid == 0) __hip_atomic_store(unit_ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      TP_STAMP(56);
+      return;
+    }
+  }
   const CombineItem ci = combine_item(tid, nh, WAVES);
   float Mc, Lc;
   Acc8 Ac;
@@ -2440,6 +2529,27 @@ extern "C" unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c,
         if (group_last) {  // any workgroup may combine; its loads are the same, so check once per group
           const int first = grp * T;
           const int count = T > 0 ? std::min(T, S - first) : S;
+          if (T == 0 && count <= kHeadCombineMax) {
+            // combine_heads: wave w takes heads w, w + waves, ...; lane l dims 2l, 2l + 1; batches of B records.
+            for (int hh = 0; hh < nh; ++hh)
+              for (int lane = 0; lane < 64; ++lane) {
+                const int wave = hh % waves;
+                const int B = count <= 16 ? 16 : 32;
+                for (int r0 = 0; r0 < count; r0 += B) {
+                  const int rj = std::min(r0 + (lane & (B - 1)), count - 1);
+                  log.check("records (m, l)", ml_off + (record_ml(unit, hh, Sp, 0) + 2 * rj) * 4, 8, sz_ws, L, wave,
+                            lane);
+                  for (int j = 0; j < B; ++j)
+                    log.check("records o",
+                              acc_off + (record_acc(unit, S, 0, hh) + 2 * lane +
+                                         (int64_t)std::min(r0 + j, count - 1) * 16 * kHeadDim) * 2,
+                              4, sz_ws, L, wave, lane);
+                }
+                log.check("out", (((int64_t)b * c->hq + (int64_t)kv * g + h0 + hh) * kHeadDim + 2 * lane) * 2, 4,
+                          sz_out, L, wave, lane);
+              }
+            continue;
+          }
           combine_loads(L, unit, nh, ml_off, acc_off, S, Sp, first, count);
           if (T > 0) {
             for (int tid = 0; tid < waves * 64; ++tid) {
