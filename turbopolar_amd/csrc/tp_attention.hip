@@ -387,12 +387,16 @@ __host__ __device__ inline void first_page_load(int page, int p_begin, int p_end
 // Split records in the workspace: record r of unit `unit` (S_area records per
 // unit, (m, l) rows of Sp_area pairs per head) holds head h's (m, l) at float
 // offset record_ml(unit, h, Sp_area, r) and its normalised output (128 fp16)
-// at half offset record_acc(unit, S_area, r, h).
+// at half offset record_acc(unit, S_area, r, h).  Both are head-major: one
+// head's records are consecutive, its outputs consecutive 256-byte rows
+// (kRecordAccStride halves apart), so a combine that walks one head's records
+// addresses them from one base with immediate offsets.
+constexpr int64_t kRecordAccStride = kHeadDim;
 __host__ __device__ inline int64_t record_ml(int64_t unit, int h, int Sp_area, int r) {
   return ((unit * 16 + h) * Sp_area + r) * 2;
 }
 __host__ __device__ inline int64_t record_acc(int64_t unit, int S_area, int r, int h) {
-  return ((unit * S_area + r) * 16 + h) * kHeadDim;
+  return ((unit * 16 + h) * S_area + r) * kRecordAccStride;
 }
 // The combine's record of batch position u (records r0 + u past the thread's
 // `mine` reread its last one, then weigh 0).
@@ -1255,7 +1259,7 @@ __device__ __forceinline__ void combine_records(Merge& sh, const CombineItem& ci
   const int mine = active ? (count - ci.sg + SG - 1) >> lsg : 0;
   const uint16_t* pac = part_acc + record_acc(unit, S_area, first + ci.sg, ci.hh) + 8 * ci.c8;
   const float* pml = part_ml + record_ml(unit, ci.hh, Sp_area, first + ci.sg);
-  const int64_t rstride = (int64_t)SG * 16 * kHeadDim;
+  const int64_t rstride = (int64_t)SG * kRecordAccStride;
   TP_STAMP(65);
   TP_STAMP(66);
   Mc = -INFINITY;
@@ -1295,9 +1299,11 @@ __device__ __forceinline__ void combine_records(Merge& sh, const CombineItem& ci
 // The records come in batches of B (16 when there are at most 16, else 32),
 // all B + 1 loads of a batch in flight together: lane j (mod B) reads record
 // j's (m, l), and every lane reads the 4 bytes of its two dims of each
-// record's fp16 output (a head's 256-byte row per record).  The batch maximum
-// and the sum of the weights w_j = l_j 2^(m_j - M) are B-lane reductions; the
-// weights reach every lane through the wave's own 32 words of LDS (written,
+// record's fp16 output (a head's 256-byte row per record; a full batch's rows
+// are consecutive, so its loads take immediate offsets from one base).  The
+// batch maximum and the sum of the weights w_j = l_j 2^(m_j - M) are B-lane
+// reductions by DPP within each 16-lane row and scalar reads of rows 0 and 1
+// (no LDS round trips); the weights reach every lane through the wave's own 32 words of LDS (written,
 // then read back as broadcast 16-byte reads by the same wave), and each lane
 // folds its 2 x B products with mixed-precision FMAs from the fp16 outputs.
 // No split groups and no merge between waves (the split-group combine of
@@ -1307,48 +1313,79 @@ __device__ __forceinline__ void combine_records(Merge& sh, const CombineItem& ci
 // in fold_records).
 constexpr int kHeadCombineMax = 64;
 
+// x from lane l of the wave's 16-lane row, for the DPP row control CTRL.
+template <int CTRL>
+__device__ __forceinline__ float row_dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+// op over lanes 0 .. B - 1 (B = 16 or 32) of the wave, returned in every lane:
+// each 16-lane row reduces itself by DPP (quad swaps xor 1 and xor 2, then
+// the half-row and row mirrors, after which every lane holds its row's
+// result), and rows 0 and 1 are read back as scalars.
+template <int B, class Op>
+__device__ __forceinline__ float batch_reduce(float x, Op op) {
+  static_assert(B == 16 || B == 32, "batches of 16 or 32 records");
+  x = op(x, row_dpp<0xb1>(x));   // quad_perm [1, 0, 3, 2]
+  x = op(x, row_dpp<0x4e>(x));   // quad_perm [2, 3, 0, 1]
+  x = op(x, row_dpp<0x141>(x));  // row_half_mirror
+  x = op(x, row_dpp<0x140>(x));  // row_mirror
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  if constexpr (B == 16) return r0;
+  return op(r0, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16)));
+}
+
+// One batch of fold_head_records: records r0 .. r0 + B - 1 of one head.  A
+// full batch (kFull: all B records exist) reads record j at a fixed offset
+// j * 256 bytes from the batch's base, so its B loads need no address
+// arithmetic; the last, partial batch rereads the head's last record in place
+// of those past `count`.
+template <int B, bool kFull>
+__device__ __forceinline__ void fold_head_batch(const float* pml, const uint16_t* pac, int r0, int count, int lane,
+                                                float* wb, float& Mc, float& Lc, float& A0, float& A1) {
+  const int rj = r0 + (lane & (B - 1));
+  const float2 ml = *reinterpret_cast<const float2*>(pml + 2 * (kFull ? rj : min(rj, count - 1)));
+  const uint16_t* pb = pac + (int64_t)r0 * kRecordAccStride;
+  uint32_t o[B];
+#pragma unroll
+  for (int j = 0; j < B; ++j)
+    o[j] = *reinterpret_cast<const uint32_t*>(pb + (int64_t)(kFull ? j : min(j, count - 1 - r0)) * kRecordAccStride);
+  if (r0 == 0) TP_STAMP(61);
+  const float m = kFull || rj < count ? ml.x : -INFINITY;
+  const float Mn = fmaxf(Mc, batch_reduce<B>(m, [](float x, float y) { return fmaxf(x, y); }));
+  const float w = m == -INFINITY ? 0.0f : ml.y * __builtin_amdgcn_exp2f(m - Mn);
+  const float Ls = batch_reduce<B>(w, [](float x, float y) { return x + y; });
+  const float s0 = Mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mc - Mn);
+  Lc = Lc * s0 + Ls;
+  A0 *= s0;
+  A1 *= s0;
+  if (lane < B) wb[lane] = w;
+  if (r0 == 0) TP_STAMP(62);
+#pragma unroll
+  for (int k = 0; k < B / 4; ++k) {
+    const float4v wk = *reinterpret_cast<const float4v*>(wb + 4 * k);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t x = kFull || r0 + 4 * k + i < count ? o[4 * k + i] : 0u;
+      const half2v oj = __builtin_bit_cast(half2v, x);
+      A0 = __builtin_fmaf((float)oj[0], wk[i], A0);
+      A1 = __builtin_fmaf((float)oj[1], wk[i], A1);
+    }
+  }
+  Mc = Mn;
+}
+
 template <int B>
 __device__ __forceinline__ void fold_head_records(const float* pml, const uint16_t* pac, int count, int lane, float* wb,
                                                   float& Mc, float& Lc, float& A0, float& A1) {
-  const int64_t rstride = (int64_t)16 * kHeadDim;  // halves from one record of a head to the next
   Mc = -INFINITY;
   Lc = 0.0f;
   A0 = 0.0f;
   A1 = 0.0f;
   for (int r0 = 0; r0 < count; r0 += B) {
-    const int rj = r0 + (lane & (B - 1));
-    const float2 ml = *reinterpret_cast<const float2*>(pml + 2 * min(rj, count - 1));
-    uint32_t o[B];
-#pragma unroll
-    for (int j = 0; j < B; ++j) o[j] = *reinterpret_cast<const uint32_t*>(pac + min(r0 + j, count - 1) * rstride);
-    if (r0 == 0) TP_STAMP(61);
-    const float m = rj < count ? ml.x : -INFINITY;
-    float Mb = m;
-#pragma unroll
-    for (int off = 1; off < B; off <<= 1) Mb = fmaxf(Mb, __shfl_xor(Mb, off, 64));
-    const float Mn = fmaxf(Mc, Mb);
-    const float w = m == -INFINITY ? 0.0f : ml.y * __builtin_amdgcn_exp2f(m - Mn);
-    float Ls = w;
-#pragma unroll
-    for (int off = 1; off < B; off <<= 1) Ls += __shfl_xor(Ls, off, 64);
-    const float s0 = Mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mc - Mn);
-    Lc = Lc * s0 + Ls;
-    A0 *= s0;
-    A1 *= s0;
-    if (lane < B) wb[lane] = w;
-    if (r0 == 0) TP_STAMP(62);
-#pragma unroll
-    for (int k = 0; k < B / 4; ++k) {
-      const float4v wk = *reinterpret_cast<const float4v*>(wb + 4 * k);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t x = r0 + 4 * k + i < count ? o[4 * k + i] : 0u;
-        const half2v oj = __builtin_bit_cast(half2v, x);
-        A0 = __builtin_fmaf((float)oj[0], wk[i], A0);
-        A1 = __builtin_fmaf((float)oj[1], wk[i], A1);
-      }
-    }
-    Mc = Mn;
+    if (r0 + B <= count)
+      fold_head_batch<B, true>(pml, pac, r0, count, lane, wb, Mc, Lc, A0, A1);
+    else
+      fold_head_batch<B, false>(pml, pac, r0, count, lane, wb, Mc, Lc, A0, A1);
   }
 }
 
@@ -2433,7 +2470,7 @@ extern "C" unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c,
           for (int u = 0; u < B; ++u)
             log.check("records o",
                       acb + (record_acc(unit, S_area, first + ci.sg, ci.hh) + 8 * ci.c8 +
-                             (int64_t)fold_record(r0, u, mine) * SG * 16 * kHeadDim) * 2,
+                             (int64_t)fold_record(r0, u, mine) * SG * kRecordAccStride) * 2,
                       16, sz_ws, lin, tid >> 6, lane);
         }
       }
@@ -2542,7 +2579,7 @@ extern "C" unsigned long long tp_selftest_decode_bounds(const tp_bounds_case* c,
                   for (int j = 0; j < B; ++j)
                     log.check("records o",
                               acc_off + (record_acc(unit, S, 0, hh) + 2 * lane +
-                                         (int64_t)std::min(r0 + j, count - 1) * 16 * kHeadDim) * 2,
+                                         (int64_t)std::min(r0 + j, count - 1) * kRecordAccStride) * 2,
                               4, sz_ws, L, wave, lane);
                 }
                 log.check("out", (((int64_t)b * c->hq + (int64_t)kv * g + h0 + hh) * kHeadDim + 2 * lane) * 2, 4,
