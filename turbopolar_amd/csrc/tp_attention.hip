@@ -604,6 +604,24 @@ __device__ __forceinline__ void load_k(const AttnArgs& a, int64_t slot, int l16,
   }
 }
 
+// The four 16-lane rows of the wave (lanes l, l ^ 16, l ^ 32 and l ^ 48)
+// combined in every lane as op(op(row 0, row 1), op(row 2, row 3)):
+// v_permlane16_swap pairs rows 0-1 and 2-3 and v_permlane32_swap the halves,
+// both register to register (no LDS round trip, unlike a lane shuffle).
+template <class Op>
+__device__ __forceinline__ float across_rows(float x, Op op) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float s = op(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return op(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float sum_rows(float x) {
+  return across_rows(x, [](float u, float v) { return u + v; });
+}
+__device__ __forceinline__ float max_rows(float x) {
+  return across_rows(x, [](float u, float v) { return fmaxf(u, v); });
+}
+
 // Half-row QK output of one group of 8 tokens: the MFMA's rows are (token
 // 8g + r/2, half r&1) and its columns (head c&7, half c>>3), so lane (l16, l4)
 // holds D[(2*l4 + u, half h)][l16] in acc[2u + h].  The score of token
@@ -957,8 +975,7 @@ __device__ __forceinline__ void softmax_page(const float4v* s, int valid, float 
   float pm = x[0];
 #pragma unroll
   for (int k = 1; k < 16; ++k) pm = fmaxf(pm, x[k]);
-  pm = fmaxf(pm, __shfl_xor(pm, 16, 64));
-  pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
+  pm = max_rows(pm);
   if (__builtin_amdgcn_ballot_w64(pm > m_run + kLazyRescale)) {
     const float m_new = fmaxf(m_run, pm);
     // From an empty state (m_run = -inf) the factor is 0: l and acc are 0,
@@ -1420,8 +1437,7 @@ __device__ __forceinline__ void finish_unit(Merge& sh, const AttnArgs& a, int wa
   const int l4 = lane >> 4;
   const bool member = wave < WAVES;  // waves past WAVES hold no state and only keep the barriers
   // Merge the waves through LDS.
-  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
+  const float l_tot = sum_rows(l_run);
   if (member && l4 == 0) sh.ml[wave][l16] = make_float2(m_run, l_tot);
   // The lane holds dims 32*l4 + 8*i + j (acc[j][i]) of head l16: eight 16-byte
   // writes of 4 consecutive dims each; with the 132-float row stride the 8
