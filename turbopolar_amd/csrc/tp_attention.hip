@@ -1406,13 +1406,24 @@ __device__ __forceinline__ void fold_head_records(const float* pml, const uint16
   }
 }
 
+// Where combine_heads' wave finds its first head's records and output row:
+// computed before the ticket is drawn, so a last workgroup issues its record
+// loads without address arithmetic (or instruction fetches for it) after the
+// ticket returns.
+struct HeadRecords {
+  const float* pml;     // record_ml(unit, wave, Sp, 0)
+  const uint16_t* pac;  // record_acc(unit, S, 0, wave) + 2 * lane
+  uint16_t* out;        // output row of head h0 + wave, dims 2 * lane
+};
+
 template <int WAVES, class Merge>
-__device__ __forceinline__ void combine_heads(Merge& sh, const AttnArgs& a, int wave, int lane, int64_t unit, int nh,
-                                              int S, int Sp, int count, uint16_t* out_rows) {
+__device__ __forceinline__ void combine_heads(Merge& sh, int wave, int lane, int nh, int S, int Sp, int count,
+                                              const HeadRecords& hr) {
   float* wb = reinterpret_cast<float*>(&sh.acc[0][0]) + wave * 32;  // this wave's 32 weights
+  const float* pml = hr.pml;
+  const uint16_t* pac = hr.pac;
+  uint16_t* out_rows = hr.out;
   for (int hh = wave; hh < nh; hh += WAVES) {
-    const float* pml = a.part_ml + record_ml(unit, hh, Sp, 0);
-    const uint16_t* pac = a.part_acc + record_acc(unit, S, 0, hh) + 2 * lane;
     float Mc, Lc, A0, A1;
     if (count <= 16)
       fold_head_records<16>(pml, pac, count, lane, wb, Mc, Lc, A0, A1);
@@ -1420,7 +1431,10 @@ __device__ __forceinline__ void combine_heads(Merge& sh, const AttnArgs& a, int 
       fold_head_records<32>(pml, pac, count, lane, wb, Mc, Lc, A0, A1);
     TP_STAMP(57);
     const float inv = __builtin_amdgcn_rcpf(Lc);
-    *reinterpret_cast<uint32_t*>(out_rows + hh * kHeadDim + 2 * lane) = pack_f2h2(A0 * inv, A1 * inv);
+    *reinterpret_cast<uint32_t*>(out_rows) = pack_f2h2(A0 * inv, A1 * inv);
+    pml += (int64_t)WAVES * Sp * 2;  // record_ml of head hh + WAVES
+    pac += (int64_t)WAVES * S * kRecordAccStride;
+    out_rows += WAVES * kHeadDim;
   }
 }
 
@@ -1496,6 +1510,15 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
   const int count = T > 0 ? min(T, S - first) : S;
   uint32_t* unit_ctr = a.counters + unit * a.counter_slots * a.counter_stride;
   uint32_t* ctr = T > 0 ? unit_ctr + (1 + grp) * a.counter_stride : unit_ctr;
+  HeadRecords hr;
+  if constexpr (!kTiers) {
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    hr.pml = a.part_ml + record_ml(unit, wave, Sp, 0);
+    hr.pac = a.part_acc + record_acc(unit, S, 0, wave) + 2 * lane;
+    hr.out = a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0 + wave) * kHeadDim + 2 * lane;
+    asm volatile("" : : "s"(hr.pml), "v"(hr.pac), "v"(hr.out));  // computed here, before the ticket
+  }
   if (tid == 0) sh.last = draw_ticket<FL>(ctr, (uint32_t)count);
   __syncthreads();
   TP_STAMP(55);
@@ -1505,9 +1528,8 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
   // Last workgroup of this (b, kv, head block), or of its split group:
   // combine the records.
   if constexpr (!kTiers) {
-    if (count <= kHeadCombineMax) {
-      combine_heads<WAVES>(sh, a, __builtin_amdgcn_readfirstlane(tid >> 6), tid & 63, unit, nh, S, Sp, count,
-                           a.out + ((int64_t)b * a.hq + (int64_t)kv * a.g + h0) * kHeadDim);
+    if (__builtin_expect(count <= kHeadCombineMax, 1)) {
+      combine_heads<WAVES>(sh, __builtin_amdgcn_readfirstlane(tid >> 6), tid & 63, nh, S, Sp, count, hr);
       if (tid == 0) __hip_atomic_store(unit_ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       TP_STAMP(56);
       return;
