@@ -1420,6 +1420,18 @@ template <int WAVES, class Merge>
 __device__ __forceinline__ void combine_heads(Merge& sh, int wave, int lane, int nh, int S, int Sp, int count,
                                               const HeadRecords& hr) {
   float* wb = reinterpret_cast<float*>(&sh.acc[0][0]) + wave * 32;  // this wave's 32 weights
+  if (nh <= WAVES && count == 32) {
+    // One head per wave and one full batch of 32: straight-line code from
+    // the ticket to the record loads.
+    if (wave < nh) {
+      float Mc = -INFINITY, Lc = 0.0f, A0 = 0.0f, A1 = 0.0f;
+      fold_head_batch<32, true>(hr.pml, hr.pac, 0, count, lane, wb, Mc, Lc, A0, A1);
+      TP_STAMP(57);
+      const float inv = __builtin_amdgcn_rcpf(Lc);
+      *reinterpret_cast<uint32_t*>(hr.out) = pack_f2h2(A0 * inv, A1 * inv);
+    }
+    return;
+  }
   const float* pml = hr.pml;
   const uint16_t* pac = hr.pac;
   uint16_t* out_rows = hr.out;
