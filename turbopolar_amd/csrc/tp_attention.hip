@@ -1221,6 +1221,7 @@ struct AttnShared {
 constexpr int kFlRelease = 1;    // agent-scope release fence before the ticket
 constexpr int kFlNoAcquire = 2;  // no acquire fence in the combining workgroup
 constexpr int kFlTiers = 4;      // two-tier combine (launched only when tier_splits > 0)
+constexpr int kFlBatch16 = 8;    // one-tier combine of exactly 16 splits (4-wave launches)
 
 // One thread draws a ticket of a counter that `count` workgroups increment:
 // relaxed agent-scope add; the workgroup that draws the last ticket issues an
@@ -1416,16 +1417,19 @@ struct HeadRecords {
   uint16_t* out;        // output row of head h0 + wave, dims 2 * lane
 };
 
-template <int WAVES, class Merge>
+template <int WAVES, int FL, class Merge>
 __device__ __forceinline__ void combine_heads(Merge& sh, int wave, int lane, int nh, int S, int Sp, int count,
                                               const HeadRecords& hr) {
   float* wb = reinterpret_cast<float*>(&sh.acc[0][0]) + wave * 32;  // this wave's 32 weights
-  if (nh <= WAVES && count == 32) {
-    // One head per wave and one full batch of 32: straight-line code from
-    // the ticket to the record loads.
+  // One head per wave and one full batch: straight-line code from the ticket
+  // to the record loads.  Launches of exactly 16 splits (kFlBatch16, 4-wave
+  // workgroups: 4k tokens) take the 16-record batch in a kernel of their own;
+  // a second straight path in one kernel measured slower for the other.
+  constexpr int kB = (FL & kFlBatch16) != 0 ? 16 : 32;
+  if (nh <= WAVES && count == kB) {
     if (wave < nh) {
       float Mc = -INFINITY, Lc = 0.0f, A0 = 0.0f, A1 = 0.0f;
-      fold_head_batch<32, true>(hr.pml, hr.pac, 0, count, lane, wb, Mc, Lc, A0, A1);
+      fold_head_batch<kB, true>(hr.pml, hr.pac, 0, count, lane, wb, Mc, Lc, A0, A1);
       TP_STAMP(57);
       const float inv = __builtin_amdgcn_rcpf(Lc);
       *reinterpret_cast<uint32_t*>(hr.out) = pack_f2h2(A0 * inv, A1 * inv);
@@ -1541,7 +1545,7 @@ __device__ __forceinline__ void finish_merged(Merge& sh, const AttnArgs& a, int 
   // combine the records.
   if constexpr (!kTiers) {
     if (__builtin_expect(count <= kHeadCombineMax, 1)) {
-      combine_heads<WAVES>(sh, __builtin_amdgcn_readfirstlane(tid >> 6), tid & 63, nh, S, Sp, count, hr);
+      combine_heads<WAVES, FL>(sh, __builtin_amdgcn_readfirstlane(tid >> 6), tid & 63, nh, S, Sp, count, hr);
       if (tid == 0) __hip_atomic_store(unit_ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       TP_STAMP(56);
       return;
@@ -2062,13 +2066,23 @@ static int32_t launch_measure_variant(const AttnArgs& a, dim3 grid, int kind, hi
 // tp_decode_attention and, with qjl, tp_decode_attention_qjl.
 // The decode kernel of a layout kind, with the two-tier combine compiled in
 // only for launches that use it.
+// Plain (no QJL, quantised V) 4-wave launches of exactly 16 splits take the
+// kernel whose combine is specialised for one batch of 16 records (kFlBatch16;
+// paired: 4k 8.06 -> 7.90 us).
 template <int KIND, int W, int QJL, bool DV = false>
 static void launch_decode_w(const AttnArgs& a, dim3 grid, hipStream_t s) {
   const dim3 block(W * 64);
-  if (a.tier_splits > 0)
+  if (a.tier_splits > 0) {
     hipLaunchKernelGGL((decode_attention_kernel<KIND, W, kFlTiers, QJL, DV>), grid, block, 0, s, a);
-  else
-    hipLaunchKernelGGL((decode_attention_kernel<KIND, W, 0, QJL, DV>), grid, block, 0, s, a);
+    return;
+  }
+  if constexpr (W == 4 && QJL == kQjlOff && !DV) {
+    if (a.n_splits == 16) {
+      hipLaunchKernelGGL((decode_attention_kernel<KIND, 4, kFlBatch16, kQjlOff, false>), grid, block, 0, s, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((decode_attention_kernel<KIND, W, 0, QJL, DV>), grid, block, 0, s, a);
 }
 
 // A split of at most 4 pages leaves waves 4-7 of an 8-wave workgroup without
