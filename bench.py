@@ -180,11 +180,37 @@ def run_gpu(args, layout):
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+    graph_equal = None
+    if getattr(args, "graph", False):
+        # The timed launches captured once into a HIP graph (the same calls on
+        # the capture stream) and timed as one replay: the GPU runs them back
+        # to back without waiting for the host's launch path.
+        eager = [c["out"].clone() for c in caches]
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            cap = torch.cuda.current_stream(dev).cuda_stream
+            for i in range(args.steps):
+                st = fn(*calls[i % len(calls)][:-1], cap)
+                if st:
+                    _lib.check(st, "tp_decode_attention")
+        graph_equal = True
+        for _ in range(3):  # replays between eager launches and syncs must match the eager outputs
+            for c in caches:
+                c["out"].zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            covered = range(min(args.steps, len(caches)))  # the caches the captured launches write
+            graph_equal &= all(torch.equal(caches[k]["out"], eager[k]) for k in covered)
+            step(0)
+            torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record()
-    for i in range(args.steps):
-        step(i)
+    if graph_equal is not None:
+        graph.replay()
+    else:
+        for i in range(args.steps):
+            step(i)
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / args.steps
@@ -196,7 +222,7 @@ def run_gpu(args, layout):
     torch.cuda.synchronize()
     ok = bool(torch.isfinite(caches[0]["out"]).all())
     return {"ms": ms, "pps": pps, "n_pages": n_pages, "finite": ok, "cfg": cfg, "caches": caches,
-            "ws_bytes": need, "rerun_equal": bool(torch.equal(ref_out, caches[0]["out"]))}
+            "ws_bytes": need, "rerun_equal": bool(torch.equal(ref_out, caches[0]["out"])), "graph_equal": graph_equal}
 
 
 def host_cores() -> int:
@@ -1249,7 +1275,8 @@ def main():
     ap.add_argument("--model-path", default=None,
                     help="model: a local Llama checkpoint directory (config.json + safetensors) instead of the "
                          "randomly initialised configs[1] shape; never downloads")
-    ap.add_argument("--graph", action="store_true", help="layers: replay the step as one HIP graph")
+    ap.add_argument("--graph", action="store_true",
+                    help="layers: replay the step as one HIP graph; decode: time the steps as one graph replay")
     ap.add_argument("--dense-v", action="store_true",
                     help="decode: tp_decode_attention_dense_v (compressed K pages, dense fp16 V pages)")
     ap.add_argument("--qjl", action="store_true",
@@ -1566,6 +1593,9 @@ def main():
     }
     if args.variant is not None:
         line["kernel_variant"] = f"{args.variant} (measurement library: phase stamps compiled in)"
+    if res.get("graph_equal") is not None:
+        line["config"]["hip_graph"] = f"the {args.steps} timed launches captured once and timed as one replay"
+        line["checks"]["graph_replays_equal_eager"] = bool(res["graph_equal"])
     if args.dense_v:
         line["metric"] = "decode-attn with dense V µs/step + achieved HBM GB/s, Llama-3-8B shape"
         line["config"]["workload"] += " + dense fp16 V (tp_decode_attention_dense_v)"
