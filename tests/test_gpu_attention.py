@@ -103,6 +103,14 @@ CASES = [
     ("default", 32, 8, 21, 5, 8),  # 8-page splits, one tier: 4-wave workgroups, two pages per wave, ragged last split
     ("fast", 16, 4, 13, 0, 6),  # 6-page splits, one tier, 4 waves: waves with one and two pages
     ("default", 64, 8, 10, 37, 5),  # GQA 8, 5-page splits on 4 waves, a dense tail
+    # exactly 16 splits on 4 waves: the kernel instance whose combine takes one straight batch of 16
+    ("default", 32, 8, 16, 37, 1),
+    ("fast", 16, 4, 16, 0, 1),
+    ("default", 64, 8, 16, 5, 1),  # 8 heads on 4 waves: the same instance's batch loop, two heads per wave
+    # exactly 32 splits: one straight batch of 32 records per head, on 4 waves and on 8
+    ("default", 32, 8, 32, 11, 1),
+    ("default", 8, 2, 288, 3, 9),
+    ("fast", 8, 2, 288, 0, 9),
 ]
 
 
@@ -123,6 +131,8 @@ BATCHED = [
     (3, "default", 32, 8, 3, 0, 1, 0),
     (2, "fast", 16, 4, 3, 5, 1, 0),
     (2, "default", 4, 2, 0, 37, 0, 0),  # dense tail only
+    (2, "default", 8, 2, 16, 20, 1, 100),  # 16 splits, the tail and part of the last page masked: a record of m = -inf
+    (2, "default", 8, 2, 32, 0, 1, 70),  # 32 splits (one straight batch), a masked suffix into the last page
 ]
 
 
