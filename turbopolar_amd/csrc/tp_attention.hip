@@ -1417,28 +1417,13 @@ struct HeadRecords {
   uint16_t* out;        // output row of head h0 + wave, dims 2 * lane
 };
 
-template <int WAVES, int FL, class Merge>
-__device__ __forceinline__ void combine_heads(Merge& sh, int wave, int lane, int nh, int S, int Sp, int count,
-                                              const HeadRecords& hr) {
-  float* wb = reinterpret_cast<float*>(&sh.acc[0][0]) + wave * 32;  // this wave's 32 weights
-  // One head per wave and one full batch: straight-line code from the ticket
-  // to the record loads.  Launches of exactly 16 splits (kFlBatch16, 4-wave
-  // workgroups: 4k tokens) take the 16-record batch in a kernel of their own;
-  // a second straight path in one kernel measured slower for the other.
-  constexpr int kB = (FL & kFlBatch16) != 0 ? 16 : 32;
-  if (nh <= WAVES && count == kB) {
-    if (wave < nh) {
-      float Mc = -INFINITY, Lc = 0.0f, A0 = 0.0f, A1 = 0.0f;
-      fold_head_batch<kB, true>(hr.pml, hr.pac, 0, count, lane, wb, Mc, Lc, A0, A1);
-      TP_STAMP(57);
-      const float inv = __builtin_amdgcn_rcpf(Lc);
-      *reinterpret_cast<uint32_t*>(hr.out) = pack_f2h2(A0 * inv, A1 * inv);
-    }
-    return;
-  }
-  const float* pml = hr.pml;
-  const uint16_t* pac = hr.pac;
-  uint16_t* out_rows = hr.out;
+// The general head-row combine (any count, heads w, w + WAVES, ...), as a
+// real call: its code then sits away from the straight path that follows the
+// ticket, which the compiler lays out as the fall-through.
+template <int WAVES>
+__device__ __attribute__((noinline)) void combine_head_rows(float* wb, int wave, int lane, int nh, int S, int Sp,
+                                                            int count, const float* pml, const uint16_t* pac,
+                                                            uint16_t* out_rows) {
   for (int hh = wave; hh < nh; hh += WAVES) {
     float Mc, Lc, A0, A1;
     if (count <= 16)
@@ -1452,6 +1437,48 @@ __device__ __forceinline__ void combine_heads(Merge& sh, int wave, int lane, int
     pac += (int64_t)WAVES * S * kRecordAccStride;
     out_rows += WAVES * kHeadDim;
   }
+}
+
+template <int WAVES, int FL, class Merge>
+__device__ __forceinline__ void combine_heads(Merge& sh, int wave, int lane, int nh, int S, int Sp, int count,
+                                              const HeadRecords& hr) {
+  float* wb = reinterpret_cast<float*>(&sh.acc[0][0]) + wave * 32;  // this wave's 32 weights
+  // One full batch per head: straight-line code from the ticket to the
+  // record loads.  Launches of exactly 16 splits (kFlBatch16, 4-wave
+  // workgroups: 4k tokens) take the 16-record batch in a kernel of their own;
+  // a second straight path in one kernel measured slower for the other.
+  constexpr int kB = (FL & kFlBatch16) != 0 ? 16 : 32;
+  if constexpr (WAVES == 8) {
+    // 8-wave launches have at most 8 heads per block below GQA 16: one head
+    // per wave (a loop here measured slower at the headline shape).
+    if (nh <= WAVES && count == kB) {
+      if (wave < nh) {
+        float Mc = -INFINITY, Lc = 0.0f, A0 = 0.0f, A1 = 0.0f;
+        fold_head_batch<kB, true>(hr.pml, hr.pac, 0, count, lane, wb, Mc, Lc, A0, A1);
+        TP_STAMP(57);
+        const float inv = __builtin_amdgcn_rcpf(Lc);
+        *reinterpret_cast<uint32_t*>(hr.out) = pack_f2h2(A0 * inv, A1 * inv);
+      }
+      return;
+    }
+  } else if (count == kB) {
+    // 4-wave launches carry up to 8 heads: two per wave at GQA 8.
+    const float* pml = hr.pml;
+    const uint16_t* pac = hr.pac;
+    uint16_t* out_rows = hr.out;
+    for (int hh = wave; hh < nh; hh += WAVES) {
+      float Mc = -INFINITY, Lc = 0.0f, A0 = 0.0f, A1 = 0.0f;
+      fold_head_batch<kB, true>(pml, pac, 0, count, lane, wb, Mc, Lc, A0, A1);
+      TP_STAMP(57);
+      const float inv = __builtin_amdgcn_rcpf(Lc);
+      *reinterpret_cast<uint32_t*>(out_rows) = pack_f2h2(A0 * inv, A1 * inv);
+      pml += (int64_t)WAVES * Sp * 2;  // record_ml of head hh + WAVES
+      pac += (int64_t)WAVES * S * kRecordAccStride;
+      out_rows += WAVES * kHeadDim;
+    }
+    return;
+  }
+  combine_head_rows<WAVES>(wb, wave, lane, nh, S, Sp, count, hr.pml, hr.pac, hr.out);
 }
 
 template <int WAVES, int FL, class Merge>
