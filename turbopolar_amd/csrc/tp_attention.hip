@@ -1321,9 +1321,10 @@ __device__ __forceinline__ void combine_records(Merge& sh, const CombineItem& ci
 // are consecutive, so its loads take immediate offsets from one base).  The
 // batch maximum and the sum of the weights w_j = l_j 2^(m_j - M) are B-lane
 // reductions by DPP within each 16-lane row and scalar reads of rows 0 and 1
-// (no LDS round trips); the weights reach every lane through the wave's own 32 words of LDS (written,
-// then read back as broadcast 16-byte reads by the same wave), and each lane
-// folds its 2 x B products with mixed-precision FMAs from the fp16 outputs.
+// (no LDS round trips); the weights reach every lane through the wave's own
+// 32 words of LDS (written, then read back as broadcast 16-byte reads by the
+// same wave), and each lane folds its 2 x B products with mixed-precision FMAs
+// from the fp16 outputs.
 // No split groups and no merge between waves (the split-group combine of
 // combine_records spent 0.42 µs of the 32k step's end phase in its LDS merge
 // alone).  Records past `count` are read as the last one and enter with weight
